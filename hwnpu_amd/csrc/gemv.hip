@@ -1,0 +1,139 @@
+// Batch-1 GEMV over int8 per-channel weights (K2) and fp16 weights (K7, the tied head).
+//
+// Both stream a row once in 16-byte chunks per lane, hold x in registers across a wave's rows,
+// multiply in fp16 pairs with fp32 accumulation (v_dot2) and reduce a row across its lanes. int8
+// codes become fp16 exactly with the exponent trick: byte b+128 placed under exponent bits 0x64
+// is the half 1024+b+128, less 1152 is b (exact for every int8).
+#include "hwk_common.h"
+
+namespace {
+
+__device__ __forceinline__ void i8x4_to_h2x2(uint32_t w, h2 &lo, h2 &hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  const h2 bias = {(f16)1152.0f, (f16)1152.0f};
+  lo = h2_of_bits(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+  hi = h2_of_bits(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+}
+
+// WIDE: bytes of x a chunk covers per byte of weight (2 for int8: 16 codes <-> 16 halves; 1 for
+// fp16: 8 halves <-> 8 halves). LPR lanes a row, CPL chunks a lane a pass, RPW row sets a wave.
+template <bool INT8, int LPR, int CPL, int RPW>
+__global__ __launch_bounds__(256) void k_gemv(const uint4 *__restrict__ w, const uint16_t *__restrict__ scale16,
+                                              const uint4 *__restrict__ x, void *__restrict__ y, uint32_t n,
+                                              uint32_t nc, int mode) {
+  constexpr int RS = 64 / LPR;
+  constexpr int XQ = INT8 ? 2 : 1;  // uint4s of x a chunk multiplies
+  const int lane = threadIdx.x & 63;
+  const int l = lane % LPR, sub = lane / LPR;
+  const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const uint32_t row0 = wave * (RPW * RS) + sub;
+  float acc[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) acc[i] = 0.0f;
+  for (uint32_t base = 0; base < nc; base += LPR * CPL) {
+    uint4 c[RPW][CPL];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+#pragma unroll
+      for (int j = 0; j < CPL; j++) {
+        const uint32_t r = row0 + i * RS, ch = base + j * LPR + l;
+        c[i][j] = (r < n && ch < nc) ? load_stream(&w[(size_t)r * nc + ch]) : make_uint4(0, 0, 0, 0);
+      }
+    }
+    uint4 xr[CPL][XQ];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+      const uint32_t ch = base + j * LPR + l;
+#pragma unroll
+      for (int q = 0; q < XQ; q++) xr[j][q] = ch < nc ? x[(size_t)ch * XQ + q] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; j++) {
+        const uint32_t cw[4] = {c[i][j].x, c[i][j].y, c[i][j].z, c[i][j].w};
+        if constexpr (INT8) {
+          const uint32_t xw[8] = {xr[j][0].x, xr[j][0].y, xr[j][0].z, xr[j][0].w,
+                                  xr[j][1].x, xr[j][1].y, xr[j][1].z, xr[j][1].w};
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            h2 lo, hi;
+            i8x4_to_h2x2(cw[q], lo, hi);
+            d0 = __builtin_amdgcn_fdot2(lo, h2_of_bits(xw[2 * q]), d0, false);
+            d1 = __builtin_amdgcn_fdot2(hi, h2_of_bits(xw[2 * q + 1]), d1, false);
+          }
+        } else {
+          const uint32_t xw[4] = {xr[j][0].x, xr[j][0].y, xr[j][0].z, xr[j][0].w};
+#pragma unroll
+          for (int q = 0; q < 4; q += 2) {
+            d0 = __builtin_amdgcn_fdot2(h2_of_bits(cw[q]), h2_of_bits(xw[q]), d0, false);
+            d1 = __builtin_amdgcn_fdot2(h2_of_bits(cw[q + 1]), h2_of_bits(xw[q + 1]), d1, false);
+          }
+        }
+      }
+      acc[i] += d0 + d1;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    float v = group_sum<LPR>(acc[i]);
+    const uint32_t r = row0 + i * RS;
+    if (l == 0 && r < n) {
+      if constexpr (INT8) v *= (float)__builtin_bit_cast(f16, scale16[r]);
+      store_out(y, r, v, mode);
+    }
+  }
+}
+
+template <bool INT8, int LPR, int CPL, int RPW>
+void launch(hipStream_t st, const void *w, const void *s, const void *x, void *y, uint32_t n, uint32_t nc,
+            int mode) {
+  constexpr uint32_t rows_per_wave = RPW * (64 / LPR);
+  const uint32_t waves = (n + rows_per_wave - 1) / rows_per_wave;
+  hipLaunchKernelGGL((k_gemv<INT8, LPR, CPL, RPW>), dim3((waves + 3) / 4), dim3(256), 0, st, (const uint4 *)w,
+                     (const uint16_t *)s, (const uint4 *)x, y, n, nc, mode);
+}
+
+// nc chunks a row: 64 lanes over up to 4 chunks a pass; narrower rows share a wave.
+template <bool INT8>
+void dispatch(hipStream_t st, const void *w, const void *s, const void *x, void *y, uint32_t n, uint32_t nc,
+              int mode) {
+  if (nc >= 256) launch<INT8, 64, 4, 2>(st, w, s, x, y, n, nc, mode);
+  else if (nc > 128) launch<INT8, 64, 3, 2>(st, w, s, x, y, n, nc, mode);
+  else if (nc > 64) launch<INT8, 64, 2, 4>(st, w, s, x, y, n, nc, mode);
+  else if (nc > 32) launch<INT8, 64, 1, 4>(st, w, s, x, y, n, nc, mode);
+  else if (nc > 16) launch<INT8, 32, 1, 4>(st, w, s, x, y, n, nc, mode);
+  else if (nc > 8) launch<INT8, 16, 1, 4>(st, w, s, x, y, n, nc, mode);
+  else launch<INT8, 8, 1, 4>(st, w, s, x, y, n, nc, mode);
+}
+
+}  // namespace
+
+extern "C" {
+
+HWK_API char *hwk_i8_gemv(void *stream, const void *q, const void *scale16, const void *x, void *y, uint32_t n,
+                          uint32_t k, int out_mode) {
+  HWK_CHECK(q && scale16 && x && y, "hwk_i8_gemv: null pointer");
+  HWK_CHECK(k % 16 == 0 && k > 0, "hwk_i8_gemv: k=%u is not a positive multiple of 16", k);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "hwk_i8_gemv: unknown out_mode %d", out_mode);
+  HWK_CHECK(hwk::aligned(q, 16) && hwk::aligned(x, 16), "hwk_i8_gemv: q and x must be 16-byte aligned");
+  HWK_CHECK(hwk::aligned(scale16, 2) && hwk::aligned(y, out_mode == HWK_OUT_F16 ? 2 : 4), "hwk_i8_gemv: misaligned");
+  if (n == 0) return nullptr;
+  dispatch<true>((hipStream_t)stream, q, scale16, x, y, n, k / 16, out_mode);
+  return hwk::launched("hwk_i8_gemv");
+}
+
+HWK_API char *hwk_f16_gemv(void *stream, const void *w, const void *x, void *y, uint32_t n, uint32_t k,
+                           int out_mode) {
+  HWK_CHECK(w && x && y, "hwk_f16_gemv: null pointer");
+  HWK_CHECK(k % 8 == 0 && k > 0, "hwk_f16_gemv: k=%u is not a positive multiple of 8", k);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "hwk_f16_gemv: unknown out_mode %d", out_mode);
+  HWK_CHECK(hwk::aligned(w, 16) && hwk::aligned(x, 16), "hwk_f16_gemv: w and x must be 16-byte aligned");
+  HWK_CHECK(hwk::aligned(y, out_mode == HWK_OUT_F16 ? 2 : 4), "hwk_f16_gemv: y misaligned");
+  if (n == 0) return nullptr;
+  dispatch<false>((hipStream_t)stream, w, nullptr, x, y, n, k / 8, out_mode);
+  return hwk::launched("hwk_f16_gemv");
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// Shared by libhwk's sources: error strings, launch checks and the device helpers every kernel
+// uses (fp16 pairs, e8m0 scales, wave reductions). gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/hwk.h"
+
+typedef _Float16 f16;
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+namespace hwk {
+
+// A malloc'd message for the C ABI (freed by hwk_free_error).
+static inline char *errf(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  char buf[512];
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  size_t n = strlen(buf) + 1;
+  char *out = (char *)malloc(n);
+  if (out) memcpy(out, buf, n);
+  return out;
+}
+
+static inline char *hip_err(const char *what, hipError_t e) {
+  return errf("%s: %s (hipError %d)", what, hipGetErrorString(e), (int)e);
+}
+
+// The launch's own error, if any (hipGetLastError clears it).
+static inline char *launched(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_err(what, e);
+  return nullptr;
+}
+
+static inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+static inline float f32_of_bits(uint32_t b) {
+  float f;
+  memcpy(&f, &b, 4);
+  return f;
+}
+
+}  // namespace hwk
+
+#define HWK_TRY(what, call)                          \
+  do {                                               \
+    hipError_t e_ = (call);                          \
+    if (e_ != hipSuccess) return hwk::hip_err(what, e_); \
+  } while (0)
+
+#define HWK_CHECK(cond, ...)                 \
+  do {                                       \
+    if (!(cond)) return hwk::errf(__VA_ARGS__); \
+  } while (0)
+
+// ---- device helpers ----
+
+// e8m0 scale 2^(e-127) as the float whose bits are e<<23: e=0 is +0 and e=255 is +Inf, as the
+// reference's scale (internal/mxfp4/mxfp4.go:77).
+__device__ __forceinline__ float e8m0_scale(uint32_t e) { return __uint_as_float(e << 23); }
+
+__device__ __forceinline__ h2 h2_of_bits(uint32_t b) { return __builtin_bit_cast(h2, b); }
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// A 16-byte load of data read once (weights streamed from HBM): marked non-temporal so that it
+// does not displace what is reused in the caches.
+__device__ __forceinline__ uint4 load_stream(const uint4 *p) {
+  const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Two e2m1 codes of byte `sel` of w, as fp16 (low nibble in .x): exact, the hardware's fp4
+// conversion at scale 1.
+template <int SEL>
+__device__ __forceinline__ h2 fp4x2_to_h2(uint32_t w) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, SEL);
+}
+
+// Sum of a value over groups of G lanes (G a power of two up to 64), every lane gets its group's.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Store one GEMV/GEMM output per out_mode.
+__device__ __forceinline__ void store_out(void *y, size_t i, float v, int mode) {
+  if (mode == HWK_OUT_F16)
+    ((f16 *)y)[i] = (f16)v;
+  else if (mode == HWK_OUT_ADD_F32)
+    ((float *)y)[i] += v;
+  else
+    ((float *)y)[i] = v;
+}

@@ -1,0 +1,415 @@
+// MXFP4 weights on gfx950: dequantization, the batch-1 GEMV (K1) and the encoder.
+//
+// K1 streams each weight row once with 128-bit loads (a lane takes a 32-value block: 16 code
+// bytes and its scale byte), turns codes into fp16 pairs in registers with the hardware fp4
+// conversion (exact at scale 1), multiplies them against x in fp16 pairs with fp32 accumulation
+// (v_dot2), applies the block's power-of-two scale to the block's fp32 sum (exact), and sums the
+// lanes of a row with cross-lane shuffles. x stays in registers for all of a wave's rows.
+#include "hwk_common.h"
+#include "synth.h"
+
+namespace {
+
+// e2m1's values by their 4 bits; code 8 is -0 (reference internal/mxfp4/mxfp4.go:17)
+__constant__ float kE2M1[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                                -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+__global__ void k_mxfp4_dequant_f16(const uint8_t *__restrict__ w, const uint8_t *__restrict__ e,
+                                    uint32_t *__restrict__ out, uint64_t nbytes) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nbytes) return;
+  uint8_t by = w[i];
+  float s = e8m0_scale(e[i >> 4]);
+  h2 v;
+  v.x = (f16)(kE2M1[by & 15] * s);
+  v.y = (f16)(kE2M1[by >> 4] * s);
+  out[i] = __builtin_bit_cast(uint32_t, v);
+}
+
+// LPR lanes share a row (RS = 64/LPR rows side by side in a wave), a lane takes BPL blocks of a
+// pass, and a wave runs RPW such row sets. Passes cover nb blocks LPR*BPL at a time; with one
+// pass (the configurations of the model) x is loaded into registers once for all the rows.
+template <int LPR, int BPL, int RPW>
+__global__ __launch_bounds__(256) void k_mxfp4_gemv(const uint4 *__restrict__ w, const uint8_t *__restrict__ e,
+                                                    const uint4 *__restrict__ x, void *__restrict__ y,
+                                                    uint32_t n, uint32_t nb, int mode) {
+  constexpr int RS = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const int l = lane % LPR, sub = lane / LPR;
+  const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const uint32_t row0 = wave * (RPW * RS) + sub;
+  float acc[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) acc[i] = 0.0f;
+
+  for (uint32_t base = 0; base < nb; base += LPR * BPL) {
+    uint4 c[RPW][BPL];
+    uint32_t s[RPW][BPL];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+#pragma unroll
+      for (int j = 0; j < BPL; j++) {
+        const uint32_t r = row0 + i * RS, b = base + j * LPR + l;
+        if (r < n && b < nb) {
+          const size_t blk = (size_t)r * nb + b;
+          c[i][j] = load_stream(&w[blk]);
+          s[i][j] = e[blk];
+        } else {
+          c[i][j] = make_uint4(0, 0, 0, 0);
+          s[i][j] = 0;
+        }
+      }
+    }
+    uint4 xr[BPL][4];
+#pragma unroll
+    for (int j = 0; j < BPL; j++) {
+      const uint32_t b = base + j * LPR + l;
+#pragma unroll
+      for (int q = 0; q < 4; q++) xr[j][q] = b < nb ? x[(size_t)b * 4 + q] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+#pragma unroll
+      for (int j = 0; j < BPL; j++) {
+        float d0 = 0.0f, d1 = 0.0f;
+        const uint32_t cw[4] = {c[i][j].x, c[i][j].y, c[i][j].z, c[i][j].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<0>(cw[q]), h2_of_bits(xr[j][q].x), d0, false);
+          d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<1>(cw[q]), h2_of_bits(xr[j][q].y), d1, false);
+          d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<2>(cw[q]), h2_of_bits(xr[j][q].z), d0, false);
+          d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<3>(cw[q]), h2_of_bits(xr[j][q].w), d1, false);
+        }
+        acc[i] += (d0 + d1) * e8m0_scale(s[i][j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    const float v = group_sum<LPR>(acc[i]);
+    const uint32_t r = row0 + i * RS;
+    if (l == 0 && r < n) store_out(y, r, v, mode);
+  }
+}
+
+// One row set of a single-pass layout (nb <= LPR*BPL): the codes and scales of RPW rows.
+template <int BPL, int RPW>
+struct RowSet {
+  uint4 c[RPW][BPL];
+  uint32_t s[RPW][BPL];
+};
+
+template <int LPR, int BPL, int RPW>
+__device__ __forceinline__ void load_rowset(RowSet<BPL, RPW> &rs, const uint4 *__restrict__ w,
+                                            const uint8_t *__restrict__ e, uint32_t row0, uint32_t n,
+                                            uint32_t nb, int l) {
+  constexpr int RS = 64 / LPR;
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+#pragma unroll
+    for (int j = 0; j < BPL; j++) {
+      const uint32_t r = row0 + i * RS, b = j * LPR + l;
+      if (r < n && b < nb) {
+        const size_t blk = (size_t)r * nb + b;
+        rs.c[i][j] = load_stream(&w[blk]);
+        rs.s[i][j] = e[blk];
+      } else {
+        rs.c[i][j] = make_uint4(0, 0, 0, 0);
+        rs.s[i][j] = 0;
+      }
+    }
+  }
+}
+
+// The single-pass GEMV over a grid sized to the device: a wave loads x once, then walks row sets
+// wave_count apart, issuing the next set's loads before it computes the current one, so that
+// every lane keeps 2*RPW*BPL 16-byte loads in flight while the grid streams the matrix.
+template <int LPR, int BPL, int RPW>
+__global__ __launch_bounds__(256) void k_mxfp4_gemv_stream(const uint4 *__restrict__ w, const uint8_t *__restrict__ e,
+                                                           const uint4 *__restrict__ x, void *__restrict__ y,
+                                                           uint32_t n, uint32_t nb, int mode) {
+  constexpr int RS = 64 / LPR;
+  constexpr uint32_t ROWS = RPW * RS;  // rows of a row set
+  const int lane = threadIdx.x & 63;
+  const int l = lane % LPR, sub = lane / LPR;
+  const uint32_t waves = gridDim.x * 4;
+  uint32_t set = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const uint32_t sets = (n + ROWS - 1) / ROWS;
+  if (set >= sets) return;
+  RowSet<BPL, RPW> cur, nxt;
+  load_rowset<LPR, BPL, RPW>(cur, w, e, set * ROWS + sub, n, nb, l);
+  uint4 xr[BPL][4];
+#pragma unroll
+  for (int j = 0; j < BPL; j++) {
+    const uint32_t b = j * LPR + l;
+#pragma unroll
+    for (int q = 0; q < 4; q++) xr[j][q] = b < nb ? x[(size_t)b * 4 + q] : make_uint4(0, 0, 0, 0);
+  }
+  for (;;) {
+    const uint32_t next = set + waves;
+    if (next < sets) load_rowset<LPR, BPL, RPW>(nxt, w, e, next * ROWS + sub, n, nb, l);
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < BPL; j++) {
+        float d0 = 0.0f, d1 = 0.0f;
+        const uint32_t cw[4] = {cur.c[i][j].x, cur.c[i][j].y, cur.c[i][j].z, cur.c[i][j].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<0>(cw[q]), h2_of_bits(xr[j][q].x), d0, false);
+          d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<1>(cw[q]), h2_of_bits(xr[j][q].y), d1, false);
+          d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<2>(cw[q]), h2_of_bits(xr[j][q].z), d0, false);
+          d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<3>(cw[q]), h2_of_bits(xr[j][q].w), d1, false);
+        }
+        acc += (d0 + d1) * e8m0_scale(cur.s[i][j]);
+      }
+      const float v = group_sum<LPR>(acc);
+      const uint32_t r = set * ROWS + sub + i * RS;
+      if (l == 0 && r < n) store_out(y, r, v, mode);
+    }
+    if (next >= sets) break;
+    set = next;
+    cur = nxt;
+  }
+}
+
+// ---- the encoder (reference internal/mxfp4/encode.go:11-78), one thread a block, in float64
+// with every product and sum rounded on its own, as the reference computes it ----
+
+__device__ __forceinline__ uint8_t nearest_code(double x) {
+#pragma clang fp contract(off)
+  uint8_t sign = 0;
+  if (x < 0) {
+    sign = 8;
+    x = -x;
+  }
+  // midpoints between consecutive e2m1 magnitudes; on a midpoint the even code wins
+  const double mids[7] = {0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0};
+  uint8_t c = 7;
+  for (int k = 0; k < 7; k++) {
+    if (x < mids[k] || (x == mids[k] && k % 2 == 0)) {
+      c = (uint8_t)k;
+      break;
+    }
+    if (x == mids[k]) {
+      c = (uint8_t)(k + 1);
+      break;
+    }
+  }
+  if (c == 0) return 0;
+  return sign | c;
+}
+
+__device__ void encode_block(const float v[32], uint8_t *__restrict__ wout, uint8_t *__restrict__ eout) {
+#pragma clang fp contract(off)
+  float m = 0.0f;
+  for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(v[j]));
+  uint32_t best = 0;
+  double best_err = __builtin_huge_val();
+  if (m > 0.0f) {
+    int ex;
+    frexp((double)m, &ex);
+    const int rule = ex - 1 - 2;
+    for (int xx = rule - 1; xx <= rule + 1; xx++) {
+      const int eb = xx + 127;
+      if (eb < 1 || eb > 254) continue;
+      const double s = (double)e8m0_scale((uint32_t)eb);
+      double se = 0.0;
+      for (int j = 0; j < 32; j++) {
+        const double vv = (double)v[j];
+        const double d = vv - (double)kE2M1[nearest_code(vv / s)] * s;
+        se += d * d;
+      }
+      if (se < best_err) {
+        best = (uint32_t)eb;
+        best_err = se;
+      }
+    }
+  }
+  uint32_t words[4] = {0, 0, 0, 0};
+  if (best != 0) {
+    const double s = (double)e8m0_scale(best);
+    for (int j = 0; j < 16; j++) {
+      const uint32_t lo = nearest_code((double)v[2 * j] / s), hi = nearest_code((double)v[2 * j + 1] / s);
+      words[j >> 2] |= (lo | hi << 4) << (8 * (j & 3));
+    }
+  }
+  *(uint4 *)wout = make_uint4(words[0], words[1], words[2], words[3]);
+  *eout = (uint8_t)best;
+}
+
+__global__ void k_mxfp4_encode(const float *__restrict__ x, uint8_t *__restrict__ w, uint8_t *__restrict__ e,
+                               uint64_t nblocks) {
+  uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  float v[32];
+  const float4 *src = (const float4 *)(x + b * 32);
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    float4 f = src[q];
+    v[4 * q] = f.x;
+    v[4 * q + 1] = f.y;
+    v[4 * q + 2] = f.z;
+    v[4 * q + 3] = f.w;
+  }
+  encode_block(v, w + b * 16, e + b);
+}
+
+// Block b of a (rows, k) matrix of N(0, std) values: element i = b*32 + j of the normal stream,
+// float32(z * std), then encoded.
+__global__ void k_synth_mxfp4(uint8_t *__restrict__ w, uint8_t *__restrict__ e, uint64_t nblocks, uint64_t key,
+                              float stdv) {
+  uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  float v[32];
+  for (int j = 0; j < 32; j++) v[j] = (float)(hwk::normal_at(key, b * 32 + j) * (double)stdv);
+  encode_block(v, w + b * 16, e + b);
+}
+
+// Tuning knobs read once per process: HWK_MXFP4_RPW (row sets of 1, 2, 4 or 8 rows a lane group;
+// default 2) and HWK_GEMV_WPC (resident waves a CU the streaming grid is sized for; default 24).
+int env_int(const char *name, int dflt) {
+  const char *s = getenv(name);
+  return s ? atoi(s) : dflt;
+}
+
+int gemv_rpw() {
+  static int v = [] {
+    int r = env_int("HWK_MXFP4_RPW", 2);
+    return (r == 1 || r == 2 || r == 4 || r == 8) ? r : 2;
+  }();
+  return v;
+}
+
+// Waves the streaming grid runs: resident waves per CU times the current device's CUs.
+uint32_t stream_waves() {
+  static int wpc = [] {
+    int v = env_int("HWK_GEMV_WPC", 24);
+    return v < 1 ? 1 : v > 32 ? 32 : v;
+  }();
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  return (uint32_t)(wpc * (cus > 0 ? cus : 256));
+}
+
+template <int LPR, int BPL, int RPW>
+void launch_gemv(hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n, uint32_t nb,
+                 int mode) {
+  constexpr uint32_t rows_per_wave = RPW * (64 / LPR);
+  const uint32_t sets = (n + rows_per_wave - 1) / rows_per_wave;
+  if (nb <= (uint32_t)(LPR * BPL)) {
+    uint32_t waves = sets < stream_waves() ? sets : stream_waves();
+    hipLaunchKernelGGL((k_mxfp4_gemv_stream<LPR, BPL, RPW>), dim3((waves + 3) / 4), dim3(256), 0, st,
+                       (const uint4 *)w, (const uint8_t *)e, (const uint4 *)x, y, n, nb, mode);
+    return;
+  }
+  hipLaunchKernelGGL((k_mxfp4_gemv<LPR, BPL, RPW>), dim3((sets + 3) / 4), dim3(256), 0, st, (const uint4 *)w,
+                     (const uint8_t *)e, (const uint4 *)x, y, n, nb, mode);
+}
+
+template <int LPR, int BPL>
+void launch_rpw(hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n, uint32_t nb,
+                int mode) {
+  switch (gemv_rpw()) {
+    case 1: launch_gemv<LPR, BPL, 1>(st, w, e, x, y, n, nb, mode); break;
+    case 4: launch_gemv<LPR, BPL, 4>(st, w, e, x, y, n, nb, mode); break;
+    case 8: launch_gemv<LPR, BPL, 8>(st, w, e, x, y, n, nb, mode); break;
+    default: launch_gemv<LPR, BPL, 2>(st, w, e, x, y, n, nb, mode); break;
+  }
+}
+
+template <int LPR>
+void launch_bpl(int bpl, hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n,
+                uint32_t nb, int mode) {
+  switch (bpl) {
+    case 1: launch_rpw<LPR, 1>(st, w, e, x, y, n, nb, mode); break;
+    case 2: launch_rpw<LPR, 2>(st, w, e, x, y, n, nb, mode); break;
+    case 3: launch_rpw<LPR, 3>(st, w, e, x, y, n, nb, mode); break;
+    default: launch_rpw<LPR, 4>(st, w, e, x, y, n, nb, mode); break;
+  }
+}
+
+}  // namespace
+
+// The lane layout for nb blocks a row: the fewest idle block slots over one pass when a pass can
+// hold the row (ties to more lanes a row), else 64 lanes of 4 blocks over several passes.
+static void gemv_layout(uint32_t nb, int *lpr, int *bpl) {
+  int best_l = 64, best_b = 4;
+  long best_waste = -1;
+  const int lprs[4] = {64, 32, 16, 8};
+  for (int li = 0; li < 4; li++)
+    for (int b = 1; b <= 4; b++) {
+      long slots = (long)lprs[li] * b;
+      if (slots < (long)nb) continue;
+      long waste = slots - nb;
+      if (best_waste < 0 || waste < best_waste) {
+        best_waste = waste;
+        best_l = lprs[li];
+        best_b = b;
+      }
+    }
+  *lpr = best_l;
+  *bpl = best_b;
+}
+
+extern "C" {
+
+HWK_API char *hwk_mxfp4_dequant_f16(void *stream, const void *w, const void *e, void *out, uint32_t rows,
+                                    uint32_t k) {
+  HWK_CHECK(w && e && out, "hwk_mxfp4_dequant_f16: null pointer");
+  HWK_CHECK(k % 32 == 0 && k > 0, "hwk_mxfp4_dequant_f16: k=%u is not a positive multiple of 32", k);
+  HWK_CHECK(hwk::aligned(out, 4), "hwk_mxfp4_dequant_f16: out not 4-byte aligned");
+  if (rows == 0) return nullptr;
+  const uint64_t nbytes = (uint64_t)rows * (k / 2);
+  const uint64_t blocks = (nbytes + 255) / 256;
+  hipLaunchKernelGGL(k_mxfp4_dequant_f16, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t *)w, (const uint8_t *)e, (uint32_t *)out, nbytes);
+  return hwk::launched("hwk_mxfp4_dequant_f16");
+}
+
+HWK_API char *hwk_mxfp4_gemv(void *stream, const void *w, const void *e, const void *x, void *y, uint32_t n,
+                             uint32_t k, int out_mode) {
+  HWK_CHECK(w && e && x && y, "hwk_mxfp4_gemv: null pointer");
+  HWK_CHECK(k % 32 == 0 && k > 0, "hwk_mxfp4_gemv: k=%u is not a positive multiple of 32", k);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "hwk_mxfp4_gemv: unknown out_mode %d", out_mode);
+  HWK_CHECK(hwk::aligned(w, 16) && hwk::aligned(x, 16), "hwk_mxfp4_gemv: w and x must be 16-byte aligned");
+  HWK_CHECK(hwk::aligned(y, out_mode == HWK_OUT_F16 ? 2 : 4), "hwk_mxfp4_gemv: y misaligned");
+  if (n == 0) return nullptr;
+  const uint32_t nb = k / 32;
+  int lpr, bpl;
+  gemv_layout(nb, &lpr, &bpl);
+  hipStream_t st = (hipStream_t)stream;
+  switch (lpr) {
+    case 64: launch_bpl<64>(bpl, st, w, e, x, y, n, nb, out_mode); break;
+    case 32: launch_bpl<32>(bpl, st, w, e, x, y, n, nb, out_mode); break;
+    case 16: launch_bpl<16>(bpl, st, w, e, x, y, n, nb, out_mode); break;
+    default: launch_bpl<8>(bpl, st, w, e, x, y, n, nb, out_mode); break;
+  }
+  return hwk::launched("hwk_mxfp4_gemv");
+}
+
+HWK_API char *hwk_mxfp4_encode(void *stream, const void *x, void *w, void *e, uint32_t rows, uint32_t k) {
+  HWK_CHECK(x && w && e, "hwk_mxfp4_encode: null pointer");
+  HWK_CHECK(k % 32 == 0 && k > 0, "hwk_mxfp4_encode: k=%u is not a positive multiple of 32", k);
+  HWK_CHECK(hwk::aligned(x, 16) && hwk::aligned(w, 16), "hwk_mxfp4_encode: x and w must be 16-byte aligned");
+  const uint64_t nblocks = (uint64_t)rows * (k / 32);
+  if (nblocks == 0) return nullptr;
+  hipLaunchKernelGGL(k_mxfp4_encode, dim3((uint32_t)((nblocks + 127) / 128)), dim3(128), 0, (hipStream_t)stream,
+                     (const float *)x, (uint8_t *)w, (uint8_t *)e, nblocks);
+  return hwk::launched("hwk_mxfp4_encode");
+}
+
+HWK_API char *hwk_synth_mxfp4(void *stream, void *w, void *e, uint32_t rows, uint32_t k, uint64_t key,
+                              uint32_t std_bits) {
+  HWK_CHECK(w && e, "hwk_synth_mxfp4: null pointer");
+  HWK_CHECK(k % 32 == 0 && k > 0, "hwk_synth_mxfp4: k=%u is not a positive multiple of 32", k);
+  HWK_CHECK(hwk::aligned(w, 16), "hwk_synth_mxfp4: w must be 16-byte aligned");
+  const uint64_t nblocks = (uint64_t)rows * (k / 32);
+  if (nblocks == 0) return nullptr;
+  hipLaunchKernelGGL(k_synth_mxfp4, dim3((uint32_t)((nblocks + 127) / 128)), dim3(128), 0, (hipStream_t)stream,
+                     (uint8_t *)w, (uint8_t *)e, nblocks, key, hwk::f32_of_bits(std_bits));
+  return hwk::launched("hwk_synth_mxfp4");
+}
+
+}  // extern "C"

@@ -1,0 +1,133 @@
+"""ctypes binding of libhwk (include/hwk.h), the way a purego binding in hwnpu would bind it.
+
+The library is loaded from the package's own lib/ directory (built in-tree by
+``__graft_entry__.build()``). There is no fallback: when libhwk is missing or of another ABI,
+every call raises :class:`HwkLibraryError` (the reference's ``types.ErrLibrary``,
+internal/types/errors.go:9-30, raised by ``dl.Open`` with every path it tried,
+internal/dl/dl.go:23-36).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+ABI = 1
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libhwk.so")
+
+# include/hwk.h enums
+BUF_MIRRORED, BUF_DEVICE = 0, 1
+SYNC_TO_DEVICE, SYNC_FROM_DEVICE = 0, 1
+INFO_NAME, INFO_ARCH, INFO_PCI_BUS, INFO_CUS, INFO_MEM_BYTES = 0, 1, 2, 3, 4
+STATE_DONE, STATE_PENDING = 0, 1
+OUT_F32, OUT_F16, OUT_ADD_F32 = 0, 1, 2
+
+
+class HwkError(RuntimeError):
+    """An error string returned by a libhwk call (a HIP error or a rejected argument)."""
+
+
+class HwkLibraryError(HwkError):
+    """libhwk could not be loaded (missing, or built for another ABI)."""
+
+
+P = C.c_void_p
+U32, U64, I32, SZ = C.c_uint32, C.c_uint64, C.c_int32, C.c_size_t
+
+# name -> (restype, argtypes). ERR marks calls returning an error string (NULL on success).
+ERR = "err"
+SIGNATURES = {
+    "hwk_abi": (C.c_int, []),
+    "hwk_free_error": (None, [P]),
+    "hwk_device_count": (ERR, [C.POINTER(U32)]),
+    "hwk_device_open": (ERR, [U32, C.POINTER(P)]),
+    "hwk_device_free": (None, [P]),
+    "hwk_device_info": (ERR, [P, C.c_int, C.c_char_p, SZ, C.POINTER(SZ)]),
+    "hwk_device_synchronize": (ERR, [P]),
+    "hwk_buf_alloc": (ERR, [P, SZ, C.c_int, C.POINTER(P)]),
+    "hwk_buf_free": (None, [P]),
+    "hwk_buf_host_ptr": (P, [P]),
+    "hwk_buf_dev_ptr": (P, [P]),
+    "hwk_buf_size": (SZ, [P]),
+    "hwk_buf_sync": (ERR, [P, C.c_int, SZ, SZ]),
+    "hwk_stream_new": (ERR, [P, C.POINTER(P)]),
+    "hwk_stream_free": (None, [P]),
+    "hwk_stream_sync": (ERR, [P]),
+    "hwk_event_new": (ERR, [P, C.POINTER(P)]),
+    "hwk_event_free": (None, [P]),
+    "hwk_event_record": (ERR, [P, P]),
+    "hwk_event_wait": (ERR, [P, U32, C.POINTER(C.c_int)]),
+    "hwk_event_elapsed_ns": (ERR, [P, P, C.POINTER(U64)]),
+    "hwk_module_load": (ERR, [P, P, SZ, C.POINTER(P)]),
+    "hwk_module_free": (None, [P]),
+    "hwk_module_function": (ERR, [P, C.c_char_p, C.POINTER(P)]),
+    "hwk_function_free": (None, [P]),
+    "hwk_launch": (ERR, [P, C.POINTER(U32), C.POINTER(U32), U32, P, P, SZ]),
+    "hwk_mxfp4_dequant_f16": (ERR, [P, P, P, P, U32, U32]),
+    "hwk_mxfp4_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
+    "hwk_i8_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
+    "hwk_f16_gemv": (ERR, [P, P, P, P, U32, U32, C.c_int]),
+    "hwk_synth_bytes": (ERR, [P, P, U64, U64]),
+    "hwk_synth_uniform": (ERR, [P, P, U64, U64, I32, U32, C.c_int]),
+    "hwk_synth_normal": (ERR, [P, P, U64, U64, U32, C.c_int]),
+    "hwk_synth_mxfp4": (ERR, [P, P, P, U32, U32, U64, U32]),
+    "hwk_mxfp4_encode": (ERR, [P, P, P, P, U32, U32]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class _Lib:
+    """The loaded library: attribute access gives a checked Python callable per entry point."""
+
+    def __init__(self, path: str):
+        self.path = path
+        self._cdll = C.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(self._cdll, name)
+            fn.restype = P if res == ERR else res
+            fn.argtypes = args
+        abi = self._cdll.hwk_abi()
+        if abi != ABI:
+            raise HwkLibraryError(f"{path}: ABI {abi}, this binding speaks {ABI}")
+
+    def raw(self, name: str):
+        return getattr(self._cdll, name)
+
+    def __getattr__(self, name: str):
+        if name not in SIGNATURES:
+            raise AttributeError(name)
+        fn = getattr(self._cdll, name)
+        if SIGNATURES[name][0] != ERR:
+            return fn
+        free = self._cdll.hwk_free_error
+
+        def call(*args):
+            err = fn(*args)
+            if err:
+                msg = C.string_at(err).decode(errors="replace")
+                free(err)
+                raise HwkError(msg)
+
+        call.__name__ = name
+        return call
+
+
+def load(path: str | None = None) -> _Lib:
+    """The process's libhwk; raises HwkLibraryError when it is missing or of another ABI."""
+    global _lib
+    with _lock:
+        if _lib is not None and (path is None or path == _lib.path):
+            return _lib
+        p = path or os.environ.get("HWNPU_HWK_LIB", LIB_PATH)
+        if not os.path.exists(p):
+            raise HwkLibraryError(f"libhwk not found (tried {p}); build it with __graft_entry__.build()")
+        try:
+            lib = _Lib(p)
+        except OSError as e:
+            raise HwkLibraryError(f"libhwk at {p} failed to load: {e}") from e
+        _lib = lib
+        return lib

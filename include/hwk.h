@@ -1,0 +1,157 @@
+/*
+ * hwk.h - libhwk, the MI355X (gfx950) kernel library behind hwnpu's backend API.
+ *
+ * A C ABI in the style of hwnpu's XRT shim (reference native/xrtshim/xrtshim.h:1-113) so that Go
+ * without cgo binds it through purego (reference internal/dl/dl.go:23-64,
+ * internal/backend/amdxrt/shim.go:47-80):
+ *   - every call that can fail returns NULL on success, or a malloc'd message that the caller
+ *     frees with hwk_free_error;
+ *   - objects are opaque and freed by their *_free;
+ *   - arguments are integers and pointers only: no float scalars (they travel as uint32 bit
+ *     patterns) and no structs by value (reference docs/design/architecture.md:145-152);
+ *   - no callbacks.
+ *
+ * Device memory is plain device pointers (`const void *` / `void *`); a stream is a hipStream_t
+ * passed as `void *` (NULL: the null stream). Every op is asynchronous on its stream. There is
+ * no CPU fallback: an op this library cannot run on the GPU returns an error.
+ */
+#ifndef HWNPU_HWK_H
+#define HWNPU_HWK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define HWK_API __attribute__((visibility("default")))
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The ABI version: a binding refuses a library of another (reference xrtshim.h:25-26, the XS_ABI
+ * check of internal/backend/amdxrt/shim.go:25-26). */
+#define HWK_ABI 1
+
+typedef struct hwk_device hwk_device;
+typedef struct hwk_buf hwk_buf;
+typedef struct hwk_module hwk_module;
+typedef struct hwk_function hwk_function;
+
+/* Buffer kinds of hwk_buf_alloc (reference internal/types BufferKind): a device allocation with a
+ * pinned host mirror synced explicitly (hwnpu Buffer.Bytes/SyncToDevice/SyncFromDevice), or a
+ * device allocation alone. */
+enum { HWK_BUF_MIRRORED = 0, HWK_BUF_DEVICE = 1 };
+
+/* Directions of hwk_buf_sync. */
+enum { HWK_SYNC_TO_DEVICE = 0, HWK_SYNC_FROM_DEVICE = 1 };
+
+/* Keys of hwk_device_info. */
+enum { HWK_INFO_NAME = 0, HWK_INFO_ARCH = 1, HWK_INFO_PCI_BUS = 2, HWK_INFO_CUS = 3, HWK_INFO_MEM_BYTES = 4 };
+
+/* Event states of hwk_event_wait. */
+enum { HWK_STATE_DONE = 0, HWK_STATE_PENDING = 1 };
+
+/* Output modes of the GEMV/GEMM ops: fp32 or fp16 (RNE of the fp32 accumulator), or the fp32
+ * result added into y (y += W x), for a residual stream. */
+enum { HWK_OUT_F32 = 0, HWK_OUT_F16 = 1, HWK_OUT_ADD_F32 = 2 };
+
+HWK_API int hwk_abi(void);
+HWK_API void hwk_free_error(char *err);
+
+/* ---- devices (reference Provider.Enumerate/Open, internal/backend/backend.go:13-19) ---- */
+HWK_API char *hwk_device_count(uint32_t *count);
+/* Fails unless the device is gfx950: the code objects in this library are built for it alone. */
+HWK_API char *hwk_device_open(uint32_t index, hwk_device **out);
+HWK_API void hwk_device_free(hwk_device *d);
+/* Writes the value, NUL terminated, into buf of n bytes; *need is its length with the NUL. */
+HWK_API char *hwk_device_info(hwk_device *d, int key, char *buf, size_t n, size_t *need);
+HWK_API char *hwk_device_synchronize(hwk_device *d);
+
+/* ---- buffers (reference Device.AllocBuffer, Buffer, backend.go:54-67) ---- */
+HWK_API char *hwk_buf_alloc(hwk_device *d, size_t size, int kind, hwk_buf **out);
+HWK_API void hwk_buf_free(hwk_buf *b);
+/* The pinned host mirror (NULL for HWK_BUF_DEVICE) and the device address. */
+HWK_API void *hwk_buf_host_ptr(hwk_buf *b);
+HWK_API void *hwk_buf_dev_ptr(hwk_buf *b);
+HWK_API size_t hwk_buf_size(hwk_buf *b);
+/* Copies n bytes from byte off between the mirror and the device, synchronously. */
+HWK_API char *hwk_buf_sync(hwk_buf *b, int dir, size_t off, size_t n);
+
+/* ---- streams and events (reference Run.Submit -> Fence.Wait/Done, graph.go:144-150) ---- */
+HWK_API char *hwk_stream_new(hwk_device *d, void **stream);
+HWK_API void hwk_stream_free(void *stream);
+HWK_API char *hwk_stream_sync(void *stream);
+HWK_API char *hwk_event_new(hwk_device *d, void **event);
+HWK_API void hwk_event_free(void *event);
+HWK_API char *hwk_event_record(void *event, void *stream);
+/* Waits up to timeout_ms (0: poll once) and writes HWK_STATE_DONE or HWK_STATE_PENDING. */
+HWK_API char *hwk_event_wait(void *event, uint32_t timeout_ms, int *state);
+/* The time between two recorded events, in nanoseconds. */
+HWK_API char *hwk_event_elapsed_ns(void *start, void *end, uint64_t *ns);
+
+/* ---- code objects (reference KernelDevice.LoadProgram, Program, Run; backend.go:27-46) ----
+ * A gfx950 code object loaded with hipModuleLoadData; a kernel launched with its arguments packed
+ * as the kernel's argument buffer (little endian, at the offsets the kernel's metadata gives). */
+HWK_API char *hwk_module_load(hwk_device *d, const void *image, size_t n, hwk_module **out);
+HWK_API void hwk_module_free(hwk_module *m);
+HWK_API char *hwk_module_function(hwk_module *m, const char *name, hwk_function **out);
+HWK_API void hwk_function_free(hwk_function *f);
+HWK_API char *hwk_launch(hwk_function *f, const uint32_t grid[3], const uint32_t block[3],
+                         uint32_t shared_bytes, void *stream, const void *args, size_t args_size);
+
+/* ---- MXFP4 weights: rows of k values, blocks of 32; codes (rows, k/32, 16) bytes with the even
+ * value in the low nibble, e8m0 scales (rows, k/32) (reference internal/mxfp4/mxfp4.go:1-20,
+ * internal/llm/experts/host.go:21-27). ---- */
+
+/* Dequantize into fp16 (rows, k): RNE(Values[code] * 2^(e-127)) with e=0 giving 0 and e=255
+ * Inf (replaces reference mxfp4.Dequantize, internal/mxfp4/mxfp4.go:120-128). */
+HWK_API char *hwk_mxfp4_dequant_f16(void *stream, const void *w, const void *e, void *out,
+                                    uint32_t rows, uint32_t k);
+/* K1: y (n) = W (n, k) x (k), x fp16, fp32 accumulation; y per out_mode (replaces the MXFP4
+ * GEMV of reference internal/mxfp4/matvec.go:33-160 with mxfp4.go:80-117, and milcpu's
+ * dequantize + linear, internal/milcpu/ops.go:940-956). k a multiple of 32; w 16-byte aligned. */
+HWK_API char *hwk_mxfp4_gemv(void *stream, const void *w, const void *e, const void *x, void *y,
+                             uint32_t n, uint32_t k, int out_mode);
+
+/* ---- int8 per-output-channel weights: codes (n, k) int8 row-major, scales (n) fp16
+ * (reference internal/milcpu/ops.go:1589-1610 constexpr_blockwise_shift_scale, the
+ * mlpackage.Int8Scaled layout internal/mlpackage/program.go:421-461). ---- */
+
+/* K2: y (n) = scale * (Q (n, k) x (k)), x fp16, fp32 accumulation (replaces shiftScale +
+ * sgemm of reference internal/milcpu/ops.go:940-956 at one row). k a multiple of 16. */
+HWK_API char *hwk_i8_gemv(void *stream, const void *q, const void *scale16, const void *x,
+                          void *y, uint32_t n, uint32_t k, int out_mode);
+
+/* ---- fp16 weights (reference internal/llm/blocks/blocks.go:135-184, format "fp16") ---- */
+
+/* K7: y (n) = W (n, k) x (k), W and x fp16, fp32 accumulation: the tied head (reference
+ * internal/llm/qwen3/build.go:107-109). k a multiple of 8. */
+HWK_API char *hwk_f16_gemv(void *stream, const void *w, const void *x, void *y, uint32_t n,
+                           uint32_t k, int out_mode);
+
+/* ---- synthetic inputs, reproducible from (seed, name) alone: splitmix64 counter streams keyed
+ * by seed ^ fnv64a(name) (the role of reference internal/llm/synth.go:12-56). Each element i
+ * reads draw i (normals: draws 2i/2i+1 of pair i/2 through Box-Muller in float64). ---- */
+
+/* n bytes, each the low byte of its draw */
+HWK_API char *hwk_synth_bytes(void *stream, void *out, uint64_t n, uint64_t key);
+/* n ints uniform in [lo, lo+span) (multiply-high of the draw's top 32 bits), stored as bytes
+ * (elem_size 1) or int32 (elem_size 4) */
+HWK_API char *hwk_synth_uniform(void *stream, void *out, uint64_t n, uint64_t key, int32_t lo,
+                                uint32_t span, int elem_size);
+/* n normals N(0, std) as fp16 (f64 -> f32 -> f16, RNE) or fp32; std as float32 bits */
+HWK_API char *hwk_synth_normal(void *stream, void *out, uint64_t n, uint64_t key,
+                               uint32_t std_bits, int out_f16);
+/* rows x k normals N(0, std) encoded to MXFP4 as the reference's Encode does (least-error scale
+ * among OCP's rule and its neighbours, nearest code, ties to even; reference
+ * internal/mxfp4/encode.go:11-78), never materialized in fp32. */
+HWK_API char *hwk_synth_mxfp4(void *stream, void *w, void *e, uint32_t rows, uint32_t k,
+                              uint64_t key, uint32_t std_bits);
+/* Encode an fp32 matrix (rows, k) to MXFP4 (reference internal/mxfp4/encode.go:11-78). */
+HWK_API char *hwk_mxfp4_encode(void *stream, const void *x, void *w, void *e, uint32_t rows,
+                               uint32_t k);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
