@@ -36,6 +36,12 @@ class HwkLibraryError(HwkError):
 P = C.c_void_p
 U32, U64, I32, SZ = C.c_uint32, C.c_uint64, C.c_int32, C.c_size_t
 
+
+class AttnParams(C.Structure):
+    """hwk_attn_params (include/hwk.h)."""
+    _fields_ = [("heads", U32), ("kv_heads", U32), ("head_dim", U32), ("len", U32), ("capacity", U32),
+                ("kv_int8", U32), ("scale_bits", U32), ("out_mode", U32), ("split", U32)]
+
 # name -> (restype, argtypes). ERR marks calls returning an error string (NULL on success).
 ERR = "err"
 SIGNATURES = {
@@ -69,6 +75,10 @@ SIGNATURES = {
     "hwk_mxfp4_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
     "hwk_i8_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
     "hwk_f16_gemv": (ERR, [P, P, P, P, U32, U32, C.c_int]),
+    "hwk_attn_workspace_bytes": (SZ, [C.POINTER(AttnParams)]),
+    "hwk_attn_decode": (ERR, [P, P, P, P, P, P, P, P, SZ, C.POINTER(AttnParams)]),
+    "hwk_kv_quantize_i8": (ERR, [P, P, P, P, U32, U32]),
+    "hwk_attn_merge": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
     "hwk_synth_bytes": (ERR, [P, P, U64, U64]),
     "hwk_synth_uniform": (ERR, [P, P, U64, U64, I32, U32, C.c_int]),
     "hwk_synth_normal": (ERR, [P, P, U64, U64, U32, C.c_int]),

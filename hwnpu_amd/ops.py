@@ -102,3 +102,70 @@ def mxfp4_encode(x: torch.Tensor):
     e = torch.empty((rows, k // 32), dtype=torch.uint8, device=x.device)
     hwk.load().hwk_mxfp4_encode(_stream(), x.data_ptr(), w.data_ptr(), e.data_ptr(), rows, k)
     return w, e
+
+
+def attn_params(heads, kv_heads, length, capacity, kv_int8=False, scale=None, out_mode="f32", split=0,
+                head_dim=128):
+    p = hwk.AttnParams()
+    p.heads, p.kv_heads, p.head_dim = heads, kv_heads, head_dim
+    p.len, p.capacity, p.kv_int8 = length, capacity, 1 if kv_int8 else 0
+    p.scale_bits = f32_bits(head_dim ** -0.5 if scale is None else scale)
+    p.out_mode = OUT_MODES[out_mode]
+    p.split = split
+    return p
+
+
+def attn_workspace(p) -> torch.Tensor:
+    n = hwk.load().hwk_attn_workspace_bytes(p)
+    return torch.empty(n, dtype=torch.uint8, device="cuda")
+
+
+def attn_decode(q, k, v, length, k_scale=None, v_scale=None, out_mode="f32", scale=None, split=0, out=None,
+                workspace=None):
+    """out (heads, d) for one query token per head over caches k, v (kv_heads, capacity, d): fp16, or
+    int8 with fp16 scales (kv_heads, capacity)."""
+    heads, d = q.shape
+    kvh, cap, d2 = k.shape
+    if d2 != d:
+        raise ValueError("head_dim of q and k differ")
+    i8 = k.dtype == torch.int8
+    _need(q, "q", torch.float16, (heads, d))
+    _need(k, "k", torch.int8 if i8 else torch.float16, (kvh, cap, d))
+    _need(v, "v", torch.int8 if i8 else torch.float16, (kvh, cap, d))
+    if i8:
+        _need(k_scale, "k_scale", torch.float16, (kvh, cap))
+        _need(v_scale, "v_scale", torch.float16, (kvh, cap))
+    p = attn_params(heads, kvh, length, cap, i8, scale, out_mode, split, d)
+    ws = attn_workspace(p) if workspace is None else workspace
+    dt = torch.float16 if out_mode == "f16" else torch.float32
+    if out is None:
+        out = torch.empty((heads, d), dtype=dt, device=q.device)
+    else:
+        _need(out, "out", dt, (heads, d))
+    hwk.load().hwk_attn_decode(_stream(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                               k_scale.data_ptr() if i8 else None, v_scale.data_ptr() if i8 else None,
+                               out.data_ptr(), ws.data_ptr(), ws.numel(), p)
+    return out
+
+
+def kv_quantize_i8(x: torch.Tensor):
+    """int8 codes and fp16 scales of fp16 rows x (..., d) by the int8 KV rule."""
+    d = x.shape[-1]
+    _need(x, "x", torch.float16)
+    rows = x.numel() // d
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty(x.shape[:-1], dtype=torch.float16, device=x.device)
+    hwk.load().hwk_kv_quantize_i8(_stream(), x.data_ptr(), q.data_ptr(), s.data_ptr(), rows, d)
+    return q, s
+
+
+def attn_merge(o, m, l, out_mode="f32"):
+    """The reference's Merge over chunks: o (chunks, rows, dim), m and l (chunks, rows), fp32."""
+    chunks, rows, dim = o.shape
+    _need(o, "o", torch.float32, (chunks, rows, dim))
+    _need(m, "m", torch.float32, (chunks, rows))
+    _need(l, "l", torch.float32, (chunks, rows))
+    out = torch.empty((rows, dim), dtype=torch.float16 if out_mode == "f16" else torch.float32, device=o.device)
+    hwk.load().hwk_attn_merge(_stream(), o.data_ptr(), m.data_ptr(), l.data_ptr(), out.data_ptr(), chunks, rows,
+                              dim, OUT_MODES[out_mode])
+    return out

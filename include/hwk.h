@@ -128,6 +128,43 @@ HWK_API char *hwk_i8_gemv(void *stream, const void *q, const void *scale16, cons
 HWK_API char *hwk_f16_gemv(void *stream, const void *w, const void *x, void *y, uint32_t n,
                            uint32_t k, int out_mode);
 
+/* ---- decode attention (K4): one query token per head over a KV cache, split over the context
+ * and merged as Flash-Decoding does (reference internal/llm/paged/paged.go:70-310, the per-chunk
+ * program and Merge, driven by internal/llm/decode/decode.go:1435-1483). ---- */
+typedef struct hwk_attn_params {
+  uint32_t heads;      /* query heads (a multiple of kv_heads; heads/kv_heads in {1, 2, 4, 8}) */
+  uint32_t kv_heads;   /* KV heads */
+  uint32_t head_dim;   /* 128 */
+  uint32_t len;        /* keys in use, positions 0 .. len-1 (all visible to the query) */
+  uint32_t capacity;   /* positions a head's cache holds: K[h] at k + h*capacity*head_dim */
+  uint32_t kv_int8;    /* 0: fp16 K/V; 1: int8 K/V with an fp16 scale per (kv head, position) */
+  uint32_t scale_bits; /* the score scale as float32 bits (1/sqrt(head_dim) for the models here) */
+  uint32_t out_mode;   /* HWK_OUT_F32 or HWK_OUT_F16 */
+  uint32_t split;      /* keys a split takes (a multiple of 16), 0 for the library's choice */
+} hwk_attn_params;
+
+/* Bytes of device workspace hwk_attn_decode needs for these parameters. */
+HWK_API size_t hwk_attn_workspace_bytes(const hwk_attn_params *p);
+/* out (heads, head_dim) = softmax(q k^T * scale) v per head, head h on kv head h/(heads/kv_heads)
+ * (GQA, reference internal/llm/blocks/blocks.go:516-540). q fp16 (heads, head_dim). fp16 caches:
+ * k, v (kv_heads, capacity, head_dim); int8 caches: the same in int8 with k_scale, v_scale fp16
+ * (kv_heads, capacity), value = code * scale (reference internal/probe/kv.go:147-156). Returns an
+ * error for an unsupported shape; there is no CPU path. */
+HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const void *v, const void *k_scale,
+                              const void *v_scale, void *out, void *workspace, size_t workspace_bytes,
+                              const hwk_attn_params *p);
+/* The int8 KV rule, per row of head_dim values (one kv head at one position): scale =
+ * fp16(absmax/127) (1 for a row of zeros), codes = RoundToEven(value/scale) clamped to +-127
+ * (reference internal/llm/experts/weights.go:229-252 with internal/vecops/vecops.go:179-185).
+ * x fp16 (rows, head_dim); q int8 (rows, head_dim); scale fp16 (rows). */
+HWK_API char *hwk_kv_quantize_i8(void *stream, const void *x, void *q, void *scale, uint32_t rows,
+                                 uint32_t head_dim);
+/* Merge chunk outputs as the reference's Merge does (paged.go:227-310): o (chunks, rows, dim)
+ * fp32, each chunk normalized over its own keys, m and l (chunks, rows) fp32 (a chunk whose l is
+ * not positive is skipped); out (rows, dim) per out_mode, zero for a row no chunk saw. */
+HWK_API char *hwk_attn_merge(void *stream, const void *o, const void *m, const void *l, void *out,
+                             uint32_t chunks, uint32_t rows, uint32_t dim, int out_mode);
+
 /* ---- synthetic inputs, reproducible from (seed, name) alone: splitmix64 counter streams keyed
  * by seed ^ fnv64a(name) (the role of reference internal/llm/synth.go:12-56). Each element i
  * reads draw i (normals: draws 2i/2i+1 of pair i/2 through Box-Muller in float64). ---- */
