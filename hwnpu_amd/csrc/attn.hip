@@ -1,15 +1,17 @@
 // GQA decode attention (K4) on gfx950: one query token per head over an fp16 or int8 KV cache.
 //
-// The context is split over waves (split-K). A wave owns one KV head and a run of keys, and walks
-// it in tiles of 16 keys with the next tile's loads in flight:
+// The context is split over workgroups (split-K). A workgroup owns one KV head and a chunk of
+// keys; its four waves take the chunk's 16-key tiles in turn, each with the next tile's loads in
+// flight while it computes the current one:
 //   - scores: the G query heads of the KV head (padded to the MFMA's 16 rows) times the tile's
 //     keys on the fp16 MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulation); a lane loads 16 bytes
 //     of one key row straight from HBM as its B operand, so no cross-lane reduction is needed;
 //   - an online softmax in fp32 (base 2) per head, the running max kept wave-uniform;
 //   - P.V on the vector ALUs in fp32 (P stays fp32; a lane holds 8 dims of one key), so the
 //     weights are never rounded to fp16.
-// The wave writes its unnormalized output, max and sum to a workspace; a merge kernel combines
-// the splits with the rule of the reference's Merge (internal/llm/paged/paged.go:252-310).
+// The waves merge in LDS; with one chunk a head the workgroup writes the output, else one
+// unnormalized output, max and sum per query head to a workspace that a merge kernel combines
+// with the rule of the reference's Merge (internal/llm/paged/paged.go:252-310).
 #include "hwk_common.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -19,6 +21,7 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr uint32_t kMaxChunks = 4096;  // chunks a merge row takes (its weights live in LDS)
 
 __device__ __forceinline__ half8 half8_of(uint4 u) { return __builtin_bit_cast(half8, u); }
 
@@ -38,13 +41,14 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint2 w) {
 
 template <bool I8>
 struct Tile {
-  half8 k[4];     // B operand of the 4 MFMA k-steps: key lane%16, dims t*32 + (lane/16)*8 .. +8
-  half8 v[4];     // V rows: key 4r + lane/16, dims (lane%16)*8 .. +8
-  float kscale;   // int8: the scale of key lane%16
+  half8 k[4];  // B operand of the 4 MFMA k-steps: key lane%16, dims s*32 + (lane/16)*8 .. +8
+  half8 v[4];  // V rows: key 4r + lane/16, dims (lane%16)*8 .. +8
+  float kscale;
   float vscale[4];
 };
 
-// Loads tile keys [key0, key0+16) of kv head h; keys at or past `end` read as zeros.
+// Loads tile keys [key0, key0+16) of the kv head whose rows start at head_base; keys at or past
+// `end` read as zeros (no load is issued for them).
 template <bool I8>
 __device__ __forceinline__ void load_tile(Tile<I8> &t, const void *__restrict__ k, const void *__restrict__ v,
                                           const uint16_t *__restrict__ ks, const uint16_t *__restrict__ vs,
@@ -55,12 +59,11 @@ __device__ __forceinline__ void load_tile(Tile<I8> &t, const void *__restrict__ 
   for (int s = 0; s < 4; s++) {
     const size_t row = head_base + kk;
     if constexpr (I8) {
-      const uint2 z = make_uint2(0, 0);
-      uint2 w = kk < end ? *(const uint2 *)((const uint8_t *)k + row * 128 + s * 32 + grp * 8) : z;
+      uint2 w = kk < end ? *(const uint2 *)((const uint8_t *)k + row * 128 + s * 32 + grp * 8) : make_uint2(0, 0);
       t.k[s] = i8x8_to_half8(w);
     } else {
-      const uint4 z = make_uint4(0, 0, 0, 0);
-      t.k[s] = half8_of(kk < end ? load_stream((const uint4 *)((const f16 *)k + row * 128 + s * 32 + grp * 8)) : z);
+      t.k[s] = half8_of(kk < end ? load_stream((const uint4 *)((const f16 *)k + row * 128 + s * 32 + grp * 8))
+                                 : make_uint4(0, 0, 0, 0));
     }
   }
 #pragma unroll
@@ -91,25 +94,73 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
-// One wave per (kv head, split). G query heads per kv head (G <= 4: the heads are rows 0..G-1 of
-// the MFMA, held by lanes 0..15). Workspace per (kv head, split, g): o[128] unnormalized, m (natural
-// log units), l.
+__device__ __forceinline__ float uniform(float x) {
+  return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(x)));
+}
+
+// One tile into the wave's running softmax state (m, l wave-uniform, base 2; acc per lane).
 template <int G, bool I8>
-__global__ __launch_bounds__(256) void k_attn_split(const uint4 *__restrict__ q, const void *__restrict__ k,
-                                                    const void *__restrict__ v, const uint16_t *__restrict__ ks,
-                                                    const uint16_t *__restrict__ vs, float *__restrict__ ws_o,
-                                                    float *__restrict__ ws_m, float *__restrict__ ws_l,
-                                                    uint32_t kv_heads, uint32_t len, uint32_t cap, uint32_t split,
-                                                    uint32_t nsplit, float scale_log2) {
-  const int lane = threadIdx.x & 63;
-  const uint32_t wid = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (wid >= kv_heads * nsplit) return;
-  const uint32_t h = wid / nsplit, sp = wid % nsplit;
-  const uint32_t begin = sp * split;
-  const uint32_t end = begin + split < len ? begin + split : len;
+__device__ __forceinline__ void attend_tile(const Tile<I8> &t, const half8 (&qa)[4], uint32_t key0, uint32_t end,
+                                            float scale_log2, int lane, float (&m)[G], float (&l)[G],
+                                            float (&acc)[G][8]) {
+  floatx4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < 4; s++) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], t.k[s], sc, 0, 0, 0);
+  const bool valid = key0 + (lane & 15) < end;
+  float p[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float s2 = sc[g] * scale_log2;
+    if constexpr (I8) s2 *= t.kscale;
+    s2 = valid ? s2 : -__builtin_inff();
+    const float mnew = fmaxf(m[g], uniform(max16(s2)));  // lanes 0..15 hold the head rows
+    float alpha = 1.0f;
+    if (mnew == -__builtin_inff()) {
+      p[g] = 0.0f;
+    } else {
+      alpha = exp2f(m[g] - mnew);
+      p[g] = exp2f(s2 - mnew);
+    }
+    l[g] = l[g] * alpha + uniform(sum16(lane < 16 ? p[g] : 0.0f));
+    m[g] = mnew;
+    if (alpha != 1.0f) {
+#pragma unroll
+      for (int d = 0; d < 8; d++) acc[g][d] *= alpha;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int src = 4 * r + (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      float pv = __shfl(p[g], src, 64);
+      if constexpr (I8) pv *= t.vscale[r];
+#pragma unroll
+      for (int d = 0; d < 8; d++) acc[g][d] = fmaf(pv, (float)t.v[r][d], acc[g][d]);
+    }
+  }
+}
+
+// Workgroup (kv head h, chunk c) of W waves over keys [c*chunk, min((c+1)*chunk, len)). With one
+// chunk a head it writes out directly; otherwise its partial (o unnormalized, m in natural log
+// units, l) per query head g of h goes to workspace slot (h*nchunk + c)*G + g for k_attn_merge.
+template <int G, bool I8, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_decode(const uint4 *__restrict__ q, const void *__restrict__ k,
+                                                        const void *__restrict__ v, const uint16_t *__restrict__ ks,
+                                                        const uint16_t *__restrict__ vs, float *__restrict__ ws_o,
+                                                        float *__restrict__ ws_m, float *__restrict__ ws_l,
+                                                        void *__restrict__ out,
+                                                        int mode, uint32_t len, uint32_t cap, uint32_t chunk,
+                                                        uint32_t nchunk, float scale_log2) {
+  __shared__ float sm[W][G], sl[W][G];
+  __shared__ float sacc[W][G][128];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t h = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
+  const uint32_t begin = c * chunk;
+  const uint32_t end = begin + chunk < len ? begin + chunk : len;
   const size_t head_base = (size_t)h * cap;
 
-  // A operand: query head lane%16 (zero past G), dims t*32 + (lane/16)*8 .. +8
+  // A operand: query head lane%16 (zero past G), dims s*32 + (lane/16)*8 .. +8
   half8 qa[4];
   {
     const int g = lane & 15, grp = lane >> 4;
@@ -117,62 +168,27 @@ __global__ __launch_bounds__(256) void k_attn_split(const uint4 *__restrict__ q,
     for (int s = 0; s < 4; s++)
       qa[s] = half8_of(g < G ? q[((size_t)(h * G + g) * 128 + s * 32 + grp * 8) / 8] : make_uint4(0, 0, 0, 0));
   }
-  float acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; g++)
-#pragma unroll
-    for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
-  float m[G], l[G];
+  float acc[G][8], m[G], l[G];
 #pragma unroll
   for (int g = 0; g < G; g++) {
     m[g] = -__builtin_inff();
     l[g] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
   }
-
-  Tile<I8> cur, nxt;
-  if (begin < end) load_tile<I8>(cur, k, v, ks, vs, head_base, begin, end, lane);
-  for (uint32_t key0 = begin; key0 < end; key0 += 16) {
-    if (key0 + 16 < end) load_tile<I8>(nxt, k, v, ks, vs, head_base, key0 + 16, end, lane);
-    floatx4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int s = 0; s < 4; s++) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], cur.k[s], sc, 0, 0, 0);
-    const bool valid = key0 + (lane & 15) < end;
-    float p[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      float s2 = sc[g] * scale_log2;
-      if constexpr (I8) s2 *= cur.kscale;
-      s2 = valid ? s2 : -__builtin_inff();
-      // the tile's largest score, wave-uniform (lanes 0..15 hold the real head rows)
-      const float mt = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(max16(s2))));
-      const float mnew = fmaxf(m[g], mt);
-      float alpha = 1.0f;
-      if (mnew == -__builtin_inff()) {
-        p[g] = 0.0f;
-      } else {
-        alpha = exp2f(m[g] - mnew);
-        p[g] = exp2f(s2 - mnew);
-      }
-      const float lt = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__float_as_uint(sum16(lane < 16 ? p[g] : 0.0f))));
-      l[g] = l[g] * alpha + lt;
-      m[g] = mnew;
-      if (alpha != 1.0f) {
-#pragma unroll
-        for (int d = 0; d < 8; d++) acc[g][d] *= alpha;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int src = 4 * r + (lane >> 4);
-#pragma unroll
-      for (int g = 0; g < G; g++) {
-        float pv = __shfl(p[g], src, 64);
-        if constexpr (I8) pv *= cur.vscale[r];
-#pragma unroll
-        for (int d = 0; d < 8; d++) acc[g][d] = fmaf(pv, (float)cur.v[r][d], acc[g][d]);
-      }
-    }
-    cur = nxt;
+  // this wave's tiles: begin + 16*wave + 16*W*j, two buffers in turn
+  constexpr uint32_t STEP = 16 * W;
+  Tile<I8> ta, tb;
+  uint32_t key = begin + 16 * wave;
+  if (key < end) load_tile<I8>(ta, k, v, ks, vs, head_base, key, end, lane);
+  while (key < end) {
+    if (key + STEP < end) load_tile<I8>(tb, k, v, ks, vs, head_base, key + STEP, end, lane);
+    attend_tile<G, I8>(ta, qa, key, end, scale_log2, lane, m, l, acc);
+    key += STEP;
+    if (key >= end) break;
+    if (key + STEP < end) load_tile<I8>(ta, k, v, ks, vs, head_base, key + STEP, end, lane);
+    attend_tile<G, I8>(tb, qa, key, end, scale_log2, lane, m, l, acc);
+    key += STEP;
   }
   // sum the four key slots of the wave (lanes lane%16 + 16j hold the same dims)
 #pragma unroll
@@ -184,63 +200,117 @@ __global__ __launch_bounds__(256) void k_attn_split(const uint4 *__restrict__ q,
       a += __shfl_xor(a, 32, 64);
       acc[g][d] = a;
     }
-  const size_t base = ((size_t)h * nsplit + sp) * G;
   if (lane < 16) {
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-      float4 *dst = (float4 *)(ws_o + (base + g) * 128 + lane * 8);
-      dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-      dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-    }
+    for (int g = 0; g < G; g++)
+#pragma unroll
+      for (int d = 0; d < 8; d++) sacc[wave][g][lane * 8 + d] = acc[g][d];
   }
   if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < G; g++) {
-      ws_m[base + g] = m[g] * kLn2;  // natural log units
-      ws_l[base + g] = l[g];
+      sm[wave][g] = m[g];
+      sl[wave][g] = l[g];
     }
   }
-}
-
-// Merge of chunks per row (one block of `dim` threads a row): top = the largest m among chunks
-// with l > 0; a chunk weighs exp(m - top), times l when its o is normalized (the reference's
-// Merge); the sum of weights is over l. INTERNAL reads the split workspace of k_attn_split (row
-// = query head, chunk c of kv head row/G at ((row/G)*nsplit + c)*G + row%G).
-template <bool INTERNAL>
-__global__ void k_attn_merge(const float *__restrict__ o, const float *__restrict__ m, const float *__restrict__ l,
-                             void *__restrict__ out, uint32_t chunks, uint32_t rows, uint32_t dim, uint32_t G,
-                             int mode) {
-  const uint32_t row = blockIdx.x, t = threadIdx.x;
-  size_t base, stride;
-  if (INTERNAL) {
-    base = (size_t)(row / G) * chunks * G + row % G;
-    stride = G;
-  } else {
-    base = row;
-    stride = rows;
-  }
-  float top = -__builtin_inff();
-  for (uint32_t c = 0; c < chunks; c++) {
-    const size_t i = base + c * stride;
-    if (l[i] > 0.0f) top = fmaxf(top, m[i]);
-  }
-  float num = 0.0f, den = 0.0f;
-  if (top != -__builtin_inff()) {
-    for (uint32_t c = 0; c < chunks; c++) {
-      const size_t i = base + c * stride;
-      const float lc = l[i];
-      if (!(lc > 0.0f)) continue;
-      const float w = expf(m[i] - top);
-      if (INTERNAL) {
-        den += w * lc;
-        if (t < dim) num += w * o[i * dim + t];
-      } else {
-        den += w * lc;
-        if (t < dim) num += (w * lc) * o[i * dim + t];
+  __syncthreads();
+  // the waves' states merged: weights 2^(m_w - top)
+  const size_t base = ((size_t)h * nchunk + c) * G;
+  for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
+    const uint32_t g = i / 128, d = i % 128;
+    float top = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < W; w++) top = fmaxf(top, sm[w][g]);
+    float o = 0.0f, lsum = 0.0f;
+    if (top != -__builtin_inff()) {
+#pragma unroll
+      for (int w = 0; w < W; w++) {
+        const float wt = exp2f(sm[w][g] - top);
+        o += wt * sacc[w][g][d];
+        lsum += wt * sl[w][g];
+      }
+    }
+    if (nchunk == 1) {
+      store_out(out, (size_t)(h * G + g) * 128 + d, lsum > 0.0f ? o / lsum : 0.0f, mode);
+    } else {
+      ws_o[(base + g) * 128 + d] = o;
+      if (d == 0) {
+        ws_m[base + g] = top * kLn2;
+        ws_l[base + g] = lsum;
       }
     }
   }
-  if (t < dim) store_out(out, (size_t)row * dim + t, den > 0.0f ? num / den : 0.0f, mode);
+}
+// Merge of chunks (the reference's Merge rule, paged.go:252-310): top = the largest m among
+// chunks with l > 0; a chunk weighs exp(m - top), times l when its o is normalized; out = the
+// weighted sum of o over the weighted sum of l. Block (row, slice of 32 dims) of 256 threads: the
+// chunks' weights go to LDS first (one pass of independent loads), then 8 chunk lanes x 32 dims
+// sum o in batches of independent loads. INTERNAL reads the workspace of k_attn_decode (row = query
+// head, chunk c of kv head row/G at slot ((row/G)*chunks + c)*G + row%G, o unnormalized).
+template <bool INTERNAL>
+__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ o, const float *__restrict__ m,
+                                                    const float *__restrict__ l, void *__restrict__ out,
+                                                    uint32_t chunks, uint32_t rows, uint32_t dim, uint32_t G,
+                                                    int mode) {
+  __shared__ float wgt[kMaxChunks];
+  __shared__ float red[256];
+  const uint32_t row = blockIdx.x, t = threadIdx.x;
+  const uint32_t d = blockIdx.y * 32 + (t & 31), cl = t >> 5;
+  const size_t base = INTERNAL ? (size_t)(row / G) * chunks * G + row % G : row;
+  const size_t stride = INTERNAL ? G : rows;
+  float top = -__builtin_inff();
+  for (uint32_t c = t; c < chunks; c += 256) {
+    const size_t i = base + c * stride;
+    const float mc = m[i], lc = l[i];
+    wgt[c] = lc;
+    if (lc > 0.0f) top = fmaxf(top, mc);
+  }
+  red[t] = top;
+  __syncthreads();
+  for (uint32_t s = 128; s > 0; s >>= 1) {
+    if (t < s) red[t] = fmaxf(red[t], red[t + s]);
+    __syncthreads();
+  }
+  top = red[0];
+  __syncthreads();
+  float den = 0.0f;
+  for (uint32_t c = t; c < chunks; c += 256) {
+    const float lc = wgt[c];
+    float w = 0.0f;
+    if (lc > 0.0f && top != -__builtin_inff()) {
+      w = expf(m[base + c * stride] - top);
+      if (!INTERNAL) w *= lc;
+      den += INTERNAL ? w * lc : w;
+    }
+    wgt[c] = w;
+  }
+  red[t] = den;
+  __syncthreads();
+  for (uint32_t s = 128; s > 0; s >>= 1) {
+    if (t < s) red[t] += red[t + s];
+    __syncthreads();
+  }
+  den = red[0];
+  __syncthreads();
+  float num = 0.0f;
+  if (d < dim) {
+    constexpr uint32_t U = 8;
+    uint32_t c = cl;
+    for (; c + 8 * (U - 1) < chunks; c += 8 * U) {
+      float ov[U];
+#pragma unroll
+      for (uint32_t u = 0; u < U; u++) ov[u] = o[(base + (size_t)(c + 8 * u) * stride) * dim + d];
+#pragma unroll
+      for (uint32_t u = 0; u < U; u++) num += wgt[c + 8 * u] * ov[u];
+    }
+    for (; c < chunks; c += 8) num += wgt[c] * o[(base + (size_t)c * stride) * dim + d];
+  }
+  red[t] = num;
+  __syncthreads();
+  if (cl == 0 && d < dim) {
+    for (uint32_t j = 1; j < 8; j++) num += red[t + 32 * j];
+    store_out(out, (size_t)row * dim + d, den > 0.0f ? num / den : 0.0f, mode);
+  }
 }
 
 // One wave a row of head_dim (<= 512) fp16 values: absmax over the row, scale rounded to fp16,
@@ -267,26 +337,33 @@ __global__ void k_kv_quantize_i8(const f16 *__restrict__ x, int8_t *__restrict__
   }
 }
 
-uint32_t pick_split(const hwk_attn_params *p) {
+// Keys per chunk: one chunk a head when the context is short (no merge launch), else about 1024
+// workgroups of 4 waves over the device; a multiple of 64 (a tile per wave), at most kMaxChunks
+// chunks a head.
+uint32_t pick_chunk(const hwk_attn_params *p) {
   if (p->split) return p->split;
-  // about 2048 waves over the device; at least one 16-key tile a wave
-  uint64_t keys = (uint64_t)p->len * p->kv_heads;
-  uint64_t s = (keys + 2047) / 2048;
-  s = (s + 15) / 16 * 16;
-  if (s < 16) s = 16;
+  const uint64_t keys = (uint64_t)p->len * p->kv_heads;
+  if (keys <= 512) return p->len ? (p->len + 63) / 64 * 64 : 64;
+  uint64_t s = (keys + 1023) / 1024;
+  s = (s + 63) / 64 * 64;
+  if (s < 64) s = 64;
+  const uint64_t min_chunk = ((uint64_t)p->len + kMaxChunks - 1) / kMaxChunks;
+  if (s < min_chunk) s = (min_chunk + 63) / 64 * 64;
   return (uint32_t)s;
 }
+
+uint32_t chunks_of(const hwk_attn_params *p, uint32_t chunk) { return p->len ? (p->len + chunk - 1) / chunk : 1; }
 
 }  // namespace
 
 extern "C" {
 
+// Layout: o (slots, 128) | m (slots) | l (slots), slots = heads * chunks.
 HWK_API size_t hwk_attn_workspace_bytes(const hwk_attn_params *p) {
   if (!p || p->kv_heads == 0 || p->heads % p->kv_heads) return 0;
-  const uint32_t split = pick_split(p);
-  const uint64_t nsplit = p->len ? (p->len + split - 1) / split : 1;
-  const uint64_t slots = (uint64_t)p->heads * nsplit;  // kv_heads * nsplit * G
-  return (size_t)(slots * (p->head_dim + 2) * sizeof(float)) + 256;
+  const uint32_t chunk = pick_chunk(p);
+  const uint64_t slots = (uint64_t)p->heads * chunks_of(p, chunk);
+  return (size_t)(slots * (p->head_dim + 2) * sizeof(float));
 }
 
 HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const void *v, const void *k_scale,
@@ -302,30 +379,32 @@ HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const 
   HWK_CHECK(p->len <= p->capacity, "hwk_attn_decode: len %u past capacity %u", p->len, p->capacity);
   HWK_CHECK(!p->kv_int8 || (k_scale && v_scale), "hwk_attn_decode: int8 cache without scales");
   HWK_CHECK(p->out_mode == HWK_OUT_F32 || p->out_mode == HWK_OUT_F16, "hwk_attn_decode: out_mode %u", p->out_mode);
-  HWK_CHECK(p->split % 16 == 0, "hwk_attn_decode: split %u is not a multiple of 16", p->split);
+  HWK_CHECK(p->split % 64 == 0, "hwk_attn_decode: split %u is not a multiple of 64", p->split);
   HWK_CHECK(hwk::aligned(q, 16) && hwk::aligned(workspace, 16), "hwk_attn_decode: q and workspace 16-byte aligned");
   HWK_CHECK(p->kv_int8 ? (hwk::aligned(k, 8) && hwk::aligned(v, 8)) : (hwk::aligned(k, 16) && hwk::aligned(v, 16)),
             "hwk_attn_decode: k, v misaligned");
   const size_t need = hwk_attn_workspace_bytes(p);
   HWK_CHECK(workspace_bytes >= need, "hwk_attn_decode: workspace %zu bytes, %zu needed", workspace_bytes, need);
-  const uint32_t split = pick_split(p);
-  const uint32_t nsplit = p->len ? (p->len + split - 1) / split : 1;
-  const uint64_t slots = (uint64_t)p->heads * nsplit;
+  const uint32_t chunk = pick_chunk(p);
+  const uint32_t nchunk = chunks_of(p, chunk);
+  HWK_CHECK(nchunk <= kMaxChunks, "hwk_attn_decode: %u chunks of %u keys (at most %u)", nchunk, chunk, kMaxChunks);
+  const uint64_t slots = (uint64_t)p->heads * nchunk;
   float *ws_o = (float *)workspace;
   float *ws_m = ws_o + slots * 128;
   float *ws_l = ws_m + slots;
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
-  const uint32_t waves = p->kv_heads * nsplit;
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((waves + 3) / 4), block(256);
+  constexpr int W = 4;
+  const dim3 grid(p->kv_heads * nchunk), block(64 * W);
   const uint16_t *ks = (const uint16_t *)k_scale, *vs = (const uint16_t *)v_scale;
-#define HWK_ATTN_LAUNCH(GG)                                                                                       \
-  if (p->kv_int8)                                                                                                 \
-    hipLaunchKernelGGL((k_attn_split<GG, true>), grid, block, 0, st, (const uint4 *)q, k, v, ks, vs, ws_o, ws_m, \
-                       ws_l, p->kv_heads, p->len, p->capacity, split, nsplit, scale_log2);                       \
-  else                                                                                                            \
-    hipLaunchKernelGGL((k_attn_split<GG, false>), grid, block, 0, st, (const uint4 *)q, k, v, ks, vs, ws_o, ws_m, \
-                       ws_l, p->kv_heads, p->len, p->capacity, split, nsplit, scale_log2);
+  const int mode = (int)p->out_mode;
+#define HWK_ATTN_LAUNCH(GG)                                                                                         \
+  if (p->kv_int8)                                                                                                   \
+    hipLaunchKernelGGL((k_attn_decode<GG, true, W>), grid, block, 0, st, (const uint4 *)q, k, v, ks, vs, ws_o,     \
+                       ws_m, ws_l, out, mode, p->len, p->capacity, chunk, nchunk, scale_log2);                     \
+  else                                                                                                              \
+    hipLaunchKernelGGL((k_attn_decode<GG, false, W>), grid, block, 0, st, (const uint4 *)q, k, v, ks, vs, ws_o,    \
+                       ws_m, ws_l, out, mode, p->len, p->capacity, chunk, nchunk, scale_log2);
   if (G == 1) {
     HWK_ATTN_LAUNCH(1)
   } else if (G == 2) {
@@ -334,9 +413,10 @@ HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const 
     HWK_ATTN_LAUNCH(4)
   }
 #undef HWK_ATTN_LAUNCH
-  if (char *err = hwk::launched("hwk_attn_decode (split)")) return err;
-  hipLaunchKernelGGL((k_attn_merge<true>), dim3(p->heads), dim3(128), 0, st, ws_o, ws_m, ws_l, out, nsplit, p->heads,
-                     128u, G, (int)p->out_mode);
+  if (char *err = hwk::launched("hwk_attn_decode")) return err;
+  if (nchunk == 1) return nullptr;
+  hipLaunchKernelGGL((k_attn_merge<true>), dim3(p->heads, 4), dim3(256), 0, st, ws_o, ws_m, ws_l, out, nchunk,
+                     p->heads, 128u, G, mode);
   return hwk::launched("hwk_attn_decode (merge)");
 }
 
@@ -354,10 +434,10 @@ HWK_API char *hwk_attn_merge(void *stream, const void *o, const void *m, const v
                              uint32_t rows, uint32_t dim, int out_mode) {
   HWK_CHECK(o && m && l && out, "hwk_attn_merge: null pointer");
   HWK_CHECK(dim > 0 && dim <= 1024, "hwk_attn_merge: dim %u (1..1024)", dim);
+  HWK_CHECK(chunks <= kMaxChunks, "hwk_attn_merge: %u chunks (at most %u)", chunks, kMaxChunks);
   HWK_CHECK(out_mode == HWK_OUT_F32 || out_mode == HWK_OUT_F16, "hwk_attn_merge: out_mode %d", out_mode);
   if (rows == 0) return nullptr;
-  const uint32_t threads = (dim + 63) / 64 * 64;
-  hipLaunchKernelGGL((k_attn_merge<false>), dim3(rows), dim3(threads), 0, (hipStream_t)stream, (const float *)o,
+  hipLaunchKernelGGL((k_attn_merge<false>), dim3(rows, (dim + 31) / 32), dim3(256), 0, (hipStream_t)stream, (const float *)o,
                      (const float *)m, (const float *)l, out, chunks, rows, dim, 1u, out_mode);
   return hwk::launched("hwk_attn_merge");
 }

@@ -116,8 +116,9 @@ def attn_params(heads, kv_heads, length, capacity, kv_int8=False, scale=None, ou
 
 
 def attn_workspace(p) -> torch.Tensor:
+    """A workspace for hwk_attn_decode with parameters p (reusable across calls in stream order)."""
     n = hwk.load().hwk_attn_workspace_bytes(p)
-    return torch.empty(n, dtype=torch.uint8, device="cuda")
+    return torch.empty(max(n, 16), dtype=torch.uint8, device="cuda")
 
 
 def attn_decode(q, k, v, length, k_scale=None, v_scale=None, out_mode="f32", scale=None, split=0, out=None,

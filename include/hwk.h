@@ -143,7 +143,8 @@ typedef struct hwk_attn_params {
   uint32_t split;      /* keys a split takes (a multiple of 16), 0 for the library's choice */
 } hwk_attn_params;
 
-/* Bytes of device workspace hwk_attn_decode needs for these parameters. */
+/* Bytes of device workspace hwk_attn_decode needs for these parameters (the chunks' partial
+ * outputs; no initial contents needed). Calls that overlap on one workspace race. */
 HWK_API size_t hwk_attn_workspace_bytes(const hwk_attn_params *p);
 /* out (heads, head_dim) = softmax(q k^T * scale) v per head, head h on kv head h/(heads/kv_heads)
  * (GQA, reference internal/llm/blocks/blocks.go:516-540). q fp16 (heads, head_dim). fp16 caches:

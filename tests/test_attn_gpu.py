@@ -49,13 +49,41 @@ def test_attn_decode_fp16(dev, orc, heads, kvh, L, cap):
     assert np.array_equal(g16.view(np.uint16), orc.f32_to_f16(got))
 
 
-@pytest.mark.parametrize("split", [16, 48, 256, 4096])
+@pytest.mark.parametrize("split", [64, 192, 1024, 4096])
 def test_attn_decode_splits_agree(dev, orc, split):
     q, k, v = case(32, 8, 3000, 3000, "c3.split")
     want = orc.attn_decode(q.cpu().numpy().astype(np.float32), k.cpu().numpy().astype(np.float32),
                            v.cpu().numpy().astype(np.float32), 1 / math.sqrt(128))
     got = ops.attn_decode(q, k, v, 3000, split=split).cpu().numpy()
     check_close(got, want)
+
+
+def test_attn_workspace_reuse_and_graph(dev, orc):
+    """One workspace across calls of several lengths (the chunk counters go back to zero after
+    each call), then the same calls captured in a graph and replayed, each checked."""
+    q, k, v = case(16, 8, 4000, 4000, "c3.reuse")
+    p = ops.attn_params(16, 8, 4000, 4000)
+    ws = ops.attn_workspace(p)
+    lens = [4000, 37, 1153, 4000, 700]
+    want = {L: orc.attn_decode(q.cpu().numpy().astype(np.float32), k[:, :L].cpu().numpy().astype(np.float32),
+                               v[:, :L].cpu().numpy().astype(np.float32), 1 / math.sqrt(128)) for L in set(lens)}
+    for L in lens:
+        check_close(ops.attn_decode(q, k, v, L, workspace=ws).cpu().numpy(), want[L])
+    outs = [torch.empty((16, 128), dtype=torch.float32, device="cuda") for _ in lens]
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for L, o in zip(lens, outs):
+                ops.attn_decode(q, k, v, L, workspace=ws, out=o)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for L, o in zip(lens, outs):
+            check_close(o.cpu().numpy(), want[L])
 
 
 def test_kv_quantize_rule(dev, orc):
