@@ -42,6 +42,15 @@ class AttnParams(C.Structure):
     _fields_ = [("heads", U32), ("kv_heads", U32), ("head_dim", U32), ("len", U32), ("capacity", U32),
                 ("kv_int8", U32), ("scale_bits", U32), ("out_mode", U32), ("split", U32)]
 
+
+class MoeParams(C.Structure):
+    """hwk_moe_params (include/hwk.h)."""
+    _fields_ = [("tokens", U32), ("hidden", U32), ("inter", U32), ("experts", U32), ("k", U32),
+                ("out_mode", U32)]
+
+
+SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+
 # name -> (restype, argtypes). ERR marks calls returning an error string (NULL on success).
 ERR = "err"
 SIGNATURES = {
@@ -79,6 +88,9 @@ SIGNATURES = {
     "hwk_attn_decode": (ERR, [P, P, P, P, P, P, P, P, SZ, C.POINTER(AttnParams)]),
     "hwk_kv_quantize_i8": (ERR, [P, P, P, P, U32, U32]),
     "hwk_attn_merge": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
+    "hwk_moe_route": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int, C.c_int, U32]),
+    "hwk_moe_workspace_bytes": (SZ, [C.POINTER(MoeParams)]),
+    "hwk_moe_experts": (ERR, [P, P, P, P, P, P, P, P, P, P, SZ, C.POINTER(MoeParams)]),
     "hwk_synth_bytes": (ERR, [P, P, U64, U64]),
     "hwk_synth_uniform": (ERR, [P, P, U64, U64, I32, U32, C.c_int]),
     "hwk_synth_normal": (ERR, [P, P, U64, U64, U32, C.c_int]),

@@ -170,3 +170,47 @@ def attn_merge(o, m, l, out_mode="f32"):
     hwk.load().hwk_attn_merge(_stream(), o.data_ptr(), m.data_ptr(), l.data_ptr(), out.data_ptr(), chunks, rows,
                               dim, OUT_MODES[out_mode])
     return out
+
+
+def moe_route(logits, k, score="softmax", norm=True, scale=0.0, bias=None):
+    """idx int32 (rows, k) and w fp32 (rows, k) of router logits fp32 (rows, experts)."""
+    rows, E = logits.shape
+    _need(logits, "logits", torch.float32, (rows, E))
+    if bias is not None:
+        _need(bias, "bias", torch.float32, (E,))
+    idx = torch.empty((rows, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((rows, k), dtype=torch.float32, device=logits.device)
+    hwk.load().hwk_moe_route(_stream(), logits.data_ptr(), None if bias is None else bias.data_ptr(), idx.data_ptr(),
+                             w.data_ptr(), rows, E, k, hwk.SCORE_SOFTMAX if score == "softmax" else hwk.SCORE_SIGMOID,
+                             1 if norm else 0, f32_bits(scale))
+    return idx, w
+
+
+def moe_experts(x, idx, w, gu_w, gu_e, dn_w, dn_e, out=None, out_mode="f32", workspace=None):
+    """The chosen experts' SwiGLU FFNs: x fp16 (T, H); gu_w uint8 (E, 2I, H/32, 16), gu_e (E, 2I, H/32);
+    dn_w (E, H, I/32, 16), dn_e (E, H, I/32); out fp32 (T, H)."""
+    T, H = x.shape
+    E, I2 = gu_e.shape[0], gu_e.shape[1]
+    I = I2 // 2
+    k = idx.shape[1]
+    _need(x, "x", torch.float16, (T, H))
+    _need(idx, "idx", torch.int32, (T, k))
+    _need(w, "w", torch.float32, (T, k))
+    _need(gu_w, "gu_w", torch.uint8, (E, I2, H // 32, 16))
+    _need(gu_e, "gu_e", torch.uint8, (E, I2, H // 32))
+    _need(dn_w, "dn_w", torch.uint8, (E, H, I // 32, 16))
+    _need(dn_e, "dn_e", torch.uint8, (E, H, I // 32))
+    p = hwk.MoeParams()
+    p.tokens, p.hidden, p.inter, p.experts, p.k = T, H, I, E, k
+    p.out_mode = OUT_MODES[out_mode]
+    if out is None:
+        if out_mode == "add":
+            raise ValueError("out_mode 'add' needs out")
+        out = torch.empty((T, H), dtype=torch.float32, device=x.device)
+    else:
+        _need(out, "out", torch.float32, (T, H))
+    n = hwk.load().hwk_moe_workspace_bytes(p)
+    ws = torch.empty(max(n, 16), dtype=torch.uint8, device=x.device) if workspace is None else workspace
+    hwk.load().hwk_moe_experts(_stream(), x.data_ptr(), idx.data_ptr(), w.data_ptr(), gu_w.data_ptr(), gu_e.data_ptr(),
+                               dn_w.data_ptr(), dn_e.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), p)
+    return out

@@ -166,6 +166,41 @@ HWK_API char *hwk_kv_quantize_i8(void *stream, const void *x, void *q, void *sca
 HWK_API char *hwk_attn_merge(void *stream, const void *o, const void *m, const void *l, void *out,
                              uint32_t chunks, uint32_t rows, uint32_t dim, int out_mode);
 
+/* ---- MoE (K5) ---- */
+
+/* Score functions of hwk_moe_route. */
+enum { HWK_SCORE_SOFTMAX = 0, HWK_SCORE_SIGMOID = 1 };
+
+/* K5a: per row of router logits (rows, experts) fp32 (experts <= 64), the k experts of the
+ * largest scores and their weights, as the reference's Routing.Choose computes them
+ * (internal/llm/experts/weights.go:33-81): softmax scores in float32 with exp in float64, or
+ * sigmoid; a stable descending order (ties to the lower index); with norm the chosen scores over
+ * their float32 sum plus 1e-6; times scale (float32 bits) unless 0. bias (experts) fp32 or NULL
+ * moves the choice, not the weights. idx int32 (rows, k); w fp32 (rows, k). */
+HWK_API char *hwk_moe_route(void *stream, const void *logits, const void *bias, void *idx, void *w, uint32_t rows,
+                            uint32_t experts, uint32_t k, int score, int norm, uint32_t scale_bits);
+
+typedef struct hwk_moe_params {
+  uint32_t tokens;   /* rows of x (1..8) */
+  uint32_t hidden;   /* H, a multiple of 32, at most 8192 */
+  uint32_t inter;    /* I, a multiple of 32, at most 8192 */
+  uint32_t experts;  /* E (<= 64) */
+  uint32_t k;        /* experts a token (tokens * k <= 64) */
+  uint32_t out_mode; /* HWK_OUT_F32 (out = the experts' sum) or HWK_OUT_ADD_F32 (out += it) */
+} hwk_moe_params;
+
+/* Device workspace of hwk_moe_experts: the SwiGLU activations, fp32 (tokens*k, I). */
+HWK_API size_t hwk_moe_workspace_bytes(const hwk_moe_params *p);
+/* K5b: the chosen experts of each token (reference experts.Host.Run, host.go:723-882, without
+ * biases, SiLU unit): gate_up MXFP4 (E, 2I, H/32, 16) codes + (E, 2I, H/32) scales with the gate
+ * on the even rows; act = silu(gate x) * (up x) in fp32; down MXFP4 (E, H, I/32, 16) + (E, H,
+ * I/32); out[t] (+)= sum over its experts in ascending expert id of w * (down act). An expert's
+ * rows are read once for all the tokens that chose it. x fp16 (tokens, H); idx int32 and w fp32
+ * (tokens, k) as hwk_moe_route writes them; out fp32 (tokens, H). */
+HWK_API char *hwk_moe_experts(void *stream, const void *x, const void *idx, const void *w, const void *gu_w,
+                              const void *gu_e, const void *dn_w, const void *dn_e, void *out, void *workspace,
+                              size_t workspace_bytes, const hwk_moe_params *p);
+
 /* ---- synthetic inputs, reproducible from (seed, name) alone: splitmix64 counter streams keyed
  * by seed ^ fnv64a(name) (the role of reference internal/llm/synth.go:12-56). Each element i
  * reads draw i (normals: draws 2i/2i+1 of pair i/2 through Box-Muller in float64). ---- */

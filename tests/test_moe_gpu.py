@@ -1,0 +1,111 @@
+"""GPU parity of the MoE path (K5) through libhwk's C ABI against the CPU oracle.
+
+Routing: expert indices bit-exact against the oracle's restatement of Routing.Choose, weights
+equal to within one float32 ulp (the device's float64 exp may differ from glibc's in the last
+place). Experts: fp32 output within max|d| <= 2e-3 * RMS against the dequantized fp32 experts
+(the reference Host.Run's structure with fp32 activations), on the MoE configuration: hidden 2048,
+32 experts, top-4, intermediate 768, T in {1, 5}.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from hwnpu_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def check_close(got, want, tol=TOL):
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))))
+    assert err <= tol * rms(want), f"max|d|={err:.4g} rms={rms(want):.4g} ratio={err / rms(want):.3g}"
+
+
+def ulp_diff(a, b):
+    return np.abs(a.view(np.int32).astype(np.int64) - b.view(np.int32).astype(np.int64))
+
+
+@pytest.mark.parametrize("E,k", [(32, 4), (64, 8), (8, 2), (32, 1)])
+def test_route_softmax_bit_exact(dev, orc, E, k):
+    rows = 4096
+    logits = synth.normal(rows * E, f"route.{E}.{k}", dtype=torch.float32).view(rows, E)
+    lg = logits.cpu().numpy()
+    # planted exact ties: equal logits must go to the lower index
+    lg[:64, 3] = lg[:64, 7]
+    lg[64:128, :] = 0.5
+    logits.copy_(torch.from_numpy(lg))
+    idx, w = ops.moe_route(logits, k)
+    idx, w = idx.cpu().numpy(), w.cpu().numpy()
+    for r in range(rows):
+        oi, ow = orc.choose(lg[r], k)
+        assert np.array_equal(idx[r], oi), (r, idx[r], oi)
+        assert np.all(ulp_diff(w[r], ow) <= 1), (r, w[r], ow)
+    assert np.array_equal(idx[64], np.arange(k))
+
+
+def test_route_sigmoid_bias_kat(dev):
+    """TestChooseSigmoidBias (internal/llm/experts/weights_test.go:11-26)."""
+    logits = torch.tensor([[2, 1, 0, -1]], dtype=torch.float32, device="cuda")
+    bias = torch.tensor([0, 0, 3, 0], dtype=torch.float32, device="cuda")
+    idx, w = ops.moe_route(logits, 2, score="sigmoid", norm=True, bias=bias)
+    assert idx.cpu().tolist() == [[2, 0]]
+    sig = lambda x: 1 / (1 + math.exp(-x))
+    s2, s0 = sig(0), sig(2)
+    got = w.cpu().numpy()[0]
+    assert abs(got[0] - s2 / (s2 + s0)) <= 1e-5 and abs(got[1] - s0 / (s2 + s0)) <= 1e-5
+
+
+def test_route_scale_and_no_norm(dev, orc):
+    logits = synth.normal(64 * 16, "route.scale", dtype=torch.float32).view(64, 16)
+    idx, w = ops.moe_route(logits, 3, norm=False, scale=2.5)
+    lg = logits.cpu().numpy()
+    for r in range(64):
+        oi, ow = orc.choose(lg[r], 3, norm=False, scale=2.5)
+        assert np.array_equal(idx.cpu().numpy()[r], oi)
+        assert np.all(ulp_diff(w.cpu().numpy()[r], ow) <= 1)
+
+
+def experts_case(T, E=32, H=2048, I=768, name="c4"):
+    gw, ge = synth.mxfp4_uniform(E * 2 * I, H, name + ".gate_up")
+    dw, de = synth.mxfp4_uniform(E * H, I, name + ".down")
+    gw, ge = gw.view(E, 2 * I, H // 32, 16), ge.view(E, 2 * I, H // 32)
+    dw, de = dw.view(E, H, I // 32, 16), de.view(E, H, I // 32)
+    x = synth.normal(T * H, name + f".x{T}").view(T, H)
+    logits = synth.normal(T * E, name + f".logits{T}", dtype=torch.float32).view(T, E)
+    return x, logits, gw, ge, dw, de
+
+
+@pytest.mark.parametrize("T", [1, 5, 2, 8])
+def test_experts_parity(dev, orc, T):
+    print(f"moe experts T={T}", flush=True)
+    x, logits, gw, ge, dw, de = experts_case(T)
+    idx, w = ops.moe_route(logits, 4)
+    out = ops.moe_experts(x, idx, w, gw, ge, dw, de)
+    want = orc.experts(x.cpu().numpy().astype(np.float32), idx.cpu().numpy(), w.cpu().numpy(), gw.cpu().numpy(),
+                       ge.cpu().numpy(), dw.cpu().numpy(), de.cpu().numpy())
+    check_close(out.cpu().numpy(), want)
+    # add mode adds the same sums into out
+    base = synth.normal(T * 2048, "c4.base", std=1000.0, dtype=torch.float32).view(T, 2048)
+    b0 = base.cpu().numpy()
+    ops.moe_experts(x, idx, w, gw, ge, dw, de, out=base, out_mode="add")
+    check_close(base.cpu().numpy(), want + b0)
+
+
+def test_experts_small_shapes(dev, orc):
+    """Other widths: H=256 (8 of 64 lanes' blocks), I=96 (3 blocks a row), E=6, k=2, tokens sharing
+    experts."""
+    T, E, H, I = 3, 6, 256, 96
+    x, logits, gw, ge, dw, de = experts_case(T, E, H, I, name="c4s")
+    idx = torch.tensor([[4, 1], [1, 2], [0, 4]], dtype=torch.int32, device="cuda")
+    w = torch.tensor([[0.7, 0.3], [0.5, 0.5], [0.2, 0.8]], dtype=torch.float32, device="cuda")
+    out = ops.moe_experts(x, idx, w, gw, ge, dw, de)
+    want = orc.experts(x.cpu().numpy().astype(np.float32), idx.cpu().numpy(), w.cpu().numpy(), gw.cpu().numpy(),
+                       ge.cpu().numpy(), dw.cpu().numpy(), de.cpu().numpy())
+    check_close(out.cpu().numpy(), want)
