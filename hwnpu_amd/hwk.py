@@ -84,6 +84,8 @@ SIGNATURES = {
     "hwk_mxfp4_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
     "hwk_i8_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
     "hwk_f16_gemv": (ERR, [P, P, P, P, U32, U32, C.c_int]),
+    "hwk_i8_gemm": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
+    "hwk_mxfp4_gemm": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
     "hwk_attn_workspace_bytes": (SZ, [C.POINTER(AttnParams)]),
     "hwk_attn_decode": (ERR, [P, P, P, P, P, P, P, P, SZ, C.POINTER(AttnParams)]),
     "hwk_kv_quantize_i8": (ERR, [P, P, P, P, U32, U32]),

@@ -94,6 +94,42 @@ def f16_gemv(w, x, out_mode="f32", y=None):
     return y
 
 
+def _out2(y, m, n, mode, device):
+    dt = torch.float16 if mode == "f16" else torch.float32
+    if y is None:
+        if mode == "add":
+            raise ValueError("out_mode 'add' needs y")
+        return torch.empty((m, n), dtype=dt, device=device)
+    _need(y, "y", dt, (m, n))
+    return y
+
+
+def i8_gemm(x, q, scale16, out_mode="f32", y=None):
+    """Y (m, n) = X W^T for fp16 X (m, k) and int8 W (n, k) with fp16 per-row scales."""
+    m, k = x.shape
+    n = q.shape[0]
+    _need(x, "x", torch.float16, (m, k))
+    _need(q, "q", torch.int8, (n, k))
+    _need(scale16, "scale", torch.float16, (n,))
+    y = _out2(y, m, n, out_mode, x.device)
+    hwk.load().hwk_i8_gemm(_stream(), x.data_ptr(), q.data_ptr(), scale16.data_ptr(), y.data_ptr(), m, n, k,
+                           OUT_MODES[out_mode])
+    return y
+
+
+def mxfp4_gemm(x, w, e, out_mode="f32", y=None):
+    """Y (m, n) = X W^T for fp16 X (m, k) and MXFP4 W: codes w (n, k/2), scales e (n, k/32)."""
+    m, k = x.shape
+    n = w.shape[0]
+    _need(x, "x", torch.float16, (m, k))
+    _need(w, "w", torch.uint8, (n, k // 2))
+    _need(e, "e", torch.uint8, (n, k // 32))
+    y = _out2(y, m, n, out_mode, x.device)
+    hwk.load().hwk_mxfp4_gemm(_stream(), x.data_ptr(), w.data_ptr(), e.data_ptr(), y.data_ptr(), m, n, k,
+                              OUT_MODES[out_mode])
+    return y
+
+
 def mxfp4_encode(x: torch.Tensor):
     """MXFP4 codes (rows, k/2) and scales (rows, k/32) of fp32 x (rows, k)."""
     rows, k = x.shape

@@ -121,6 +121,20 @@ HWK_API char *hwk_mxfp4_gemv(void *stream, const void *w, const void *e, const v
 HWK_API char *hwk_i8_gemv(void *stream, const void *q, const void *scale16, const void *x,
                           void *y, uint32_t n, uint32_t k, int out_mode);
 
+/* ---- K3: prefill and verify GEMM, Y (m, n) = X (m, k) W^T, X fp16 row-major, fp32 accumulation on
+ * the fp16 MFMA, the weights dequantized to fp16 in LDS; Y per out_mode (fp32, fp16 = RNE of the
+ * fp32 accumulator, or added into fp32 Y). k a multiple of 32. ---- */
+
+/* int8 W (n, k) with fp16 per-row scales (replaces milcpu's shiftScale + linear,
+ * internal/milcpu/ops.go:940-956,1589-1610, over a whole prompt). */
+HWK_API char *hwk_i8_gemm(void *stream, const void *x, const void *q, const void *scale16, void *y, uint32_t m,
+                          uint32_t n, uint32_t k, int out_mode);
+/* MXFP4 W (n, k): codes (n, k/32, 16), scales (n, k/32) (replaces mxfp4.Dequantize + sgemm,
+ * internal/mxfp4/mxfp4.go:120-128 with internal/sgemm/sgemm.go:127-163). The block scale is folded
+ * into the fp16 dequantization: exact for e8m0 exponents in [-23, 13]. */
+HWK_API char *hwk_mxfp4_gemm(void *stream, const void *x, const void *w, const void *e, void *y, uint32_t m,
+                             uint32_t n, uint32_t k, int out_mode);
+
 /* ---- fp16 weights (reference internal/llm/blocks/blocks.go:135-184, format "fp16") ---- */
 
 /* K7: y (n) = W (n, k) x (k), W and x fp16, fp32 accumulation: the tied head (reference

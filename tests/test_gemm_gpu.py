@@ -1,0 +1,69 @@
+"""GPU parity of the prefill/verify GEMM (K3) through libhwk's C ABI against the oracle's
+dequantize + blocked fp32 GEMM (the reference's shiftScale/Dequantize + sgemm.MulAdd).
+
+Bar: max|Y - Y_oracle| <= 2e-3 * RMS(Y_oracle) in fp32; the fp16 output equal to RNE of the fp32
+accumulator, bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+from hwnpu_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def check_close(got, want, tol=TOL):
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))))
+    assert err <= tol * rms(want), f"max|d|={err:.4g} rms={rms(want):.4g} ratio={err / rms(want):.3g}"
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 6144, 2048), (5, 6144, 2048), (1, 128, 32), (130, 200, 96), (7, 1000, 4096),
+                                   (256, 256, 6144)])
+def test_i8_gemm_parity(dev, orc, m, n, k):
+    print(f"i8_gemm m={m} n={n} k={k}", flush=True)
+    name = f"k3i8.{m}.{n}.{k}"
+    x = synth.normal(m * k, name + ".x").view(m, k)
+    q = synth.uniform_int(n * k, -127, 255, name + ".q", dtype=torch.int8).view(n, k)
+    s = synth.uniform_real(n, 0.002, 0.02, name + ".s")
+    wd = orc.i8_dequant(q.cpu().numpy(), s.cpu().numpy().view(np.uint16))
+    want = orc.sgemm(x.cpu().numpy().astype(np.float32), wd, transb=True)
+    y32 = ops.i8_gemm(x, q, s, "f32").cpu().numpy()
+    check_close(y32, want)
+    y16 = ops.i8_gemm(x, q, s, "f16").cpu().numpy()
+    assert np.array_equal(y16.view(np.uint16), orc.f32_to_f16(y32))
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 4096, 2048), (5, 2048, 6144), (1, 96, 64), (200, 12288, 2048), (33, 130, 32)])
+def test_mxfp4_gemm_parity(dev, orc, m, n, k):
+    print(f"mxfp4_gemm m={m} n={n} k={k}", flush=True)
+    name = f"k3mx.{m}.{n}.{k}"
+    x = synth.normal(m * k, name + ".x").view(m, k)
+    w, e = synth.mxfp4_normal(n, k, name + ".w", std=0.02)
+    wd = orc.mxfp4_dequantize(w.cpu().numpy(), e.cpu().numpy())
+    want = orc.sgemm(x.cpu().numpy().astype(np.float32), wd, transb=True)
+    y32 = ops.mxfp4_gemm(x, w, e, "f32").cpu().numpy()
+    check_close(y32, want)
+    y16 = ops.mxfp4_gemm(x, w, e, "f16").cpu().numpy()
+    assert np.array_equal(y16.view(np.uint16), orc.f32_to_f16(y32))
+    # add mode
+    y0 = synth.normal(m * n, name + ".y0", dtype=torch.float32).view(m, n)
+    b0 = y0.cpu().numpy()
+    ops.mxfp4_gemm(x, w, e, "add", y=y0)
+    assert np.array_equal(y0.cpu().numpy(), (b0 + y32).astype(np.float32))
+
+
+def test_mxfp4_gemm_uniform_codes(dev, orc):
+    """The GEMV configuration's weights (every code, exponents -4..2) through the GEMM at m = 5."""
+    m, n, k = 5, 8192, 2048
+    x = synth.normal(m * k, "k3u.x").view(m, k)
+    w, e = synth.mxfp4_uniform(n, k, "k3u.w")
+    wd = orc.mxfp4_dequantize(w.cpu().numpy(), e.cpu().numpy())
+    want = orc.sgemm(x.cpu().numpy().astype(np.float32), wd, transb=True)
+    check_close(ops.mxfp4_gemm(x, w, e, "f32").cpu().numpy(), want)
