@@ -1,13 +1,30 @@
 """Benchmark of the MI355X decode path (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gemv]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|gemv|copy] [--no-cpu]
 
-Prints one JSON line. The roofline object is the batch-1 MXFP4 GEMV of the GEMV configuration
-(W 8192 x 2048 MXFP4, x fp16, y fp16): 8,933,376 algorithmic bytes per launch (codes 8,388,608 +
-scales 524,288 + x 4,096 + y 16,384), timed per launch with HIP events on the launching stream,
-over 64 distinct weight copies (572 MB, past the 256 MB MALL) so that every launch reads HBM.
-The CPU baseline is the oracle's restatement of the reference's CPU MXFP4 GEMV (mxfp4.Run with
-the int8-quantized activation, internal/mxfp4/matvec.go:33-160), on the host's cores.
+Prints one JSON line.
+
+decode (the default, BASELINE's headline): the 28-layer synthetic Qwen3 (hidden 2048, 16/8 heads,
+head_dim 128, SwiGLU 6144, vocab 151936, tied fp16 embeddings, MXFP4 linears of std-0.02 weights,
+seed 0) on one GPU. A 1024-token prompt (ids uniform over the vocabulary) is prefilled, then W
+greedy decode steps run untimed and K timed, each step one replay of the captured step graph
+(W + K = 256 by default). value = K / the timed region's seconds (HIP events on the replay
+stream): decode tokens per second at batch 1. The prefill rate is reported beside it.
+
+roofline: the batch-1 MXFP4 GEMV of the GEMV configuration (W 8192 x 2048 MXFP4, x fp16, y fp16),
+the decode step's dominant kernel kind: 64 back-to-back GEMVs over 64 distinct weight copies (572
+MB, past the 256 MB MALL) in one HIP graph, timed with HIP events on the replay stream; achieved =
+8,933,376 algorithmic bytes a launch (codes 8,388,608 + scales 524,288 + x 4,096 + y 16,384) over
+the average launch time.
+
+gemv: only that GEMV measurement. copy: a plain device copy of the same 8,933,376 bytes timed the
+same way (the calibration run for the FETCH_SIZE / WRITE_SIZE counters).
+
+cpu_baseline (decode): the oracle's restatement of the reference's CPU decode step, timed on the
+host's cores on a bounded sample and scaled to one token: one layer's MXFP4 linears through
+mxfp4.Run with the int8-quantized activation (internal/mxfp4/matvec.go:33-160), one layer's chunked
+attention + Merge at 1152 keys (internal/llm/paged/paged.go:70-310), each times 28, plus the tied
+head as dequantized fp32 sgemm (internal/sgemm/sgemm.go:127-163).
 """
 from __future__ import annotations
 
@@ -21,12 +38,54 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+C5 = dict(layers=28, hidden=2048, heads=16, kv_heads=8, head_dim=128, inter=6144, vocab=151936)
+PROMPT = 1024
+# algorithmic bytes of one decode token at cache position p: MXFP4 linears 28 x 50,331,648 params
+# x 17/32 B, the tied fp16 head, K/V read 114,688 B a position and written once, the embedding row
+LIN_BYTES = 28 * 50331648 * 17 // 32
+HEAD_BYTES = 151936 * 2048 * 2
+KV_POS_BYTES = 28 * 2 * 8 * 128 * 2
 GEMV_N, GEMV_K = 8192, 2048
 GEMV_BYTES = GEMV_N * GEMV_K // 2 + GEMV_N * GEMV_K // 32 + GEMV_K * 2 + GEMV_N * 2  # 8,933,376
 COPIES = 64
 
 
-def gemv_roofline(steps: int, warmup: int):
+def _graph_time(launch_all, steps: int, warmup: int, eager: bool = False):
+    """Per-launch microseconds of COPIES launches captured in one graph, replayed until at least
+    `steps` launches ran, timed with events on the replay stream. eager: the same launches issued
+    one by one without a graph (for counter collection, which profiles dispatches one at a time)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        launch_all()  # eager once: loads the code objects before capture
+    torch.cuda.synchronize()
+    if eager:
+        run = launch_all
+    else:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            launch_all()
+        run = g.replay
+    replays = max(1, -(-steps // COPIES))
+    with torch.cuda.stream(s):
+        for _ in range(-(-warmup // COPIES)):
+            run()
+        s.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        a.record(s)
+        for _ in range(replays):
+            run()
+        b.record(s)
+        b.synchronize()
+        wall = time.perf_counter() - t0
+    launches = replays * COPIES
+    return a.elapsed_time(b) * 1e3 / launches, launches, wall
+
+
+def gemv_roofline(steps: int, warmup: int, eager: bool = False):
     import torch
 
     from hwnpu_amd import ops, synth
@@ -34,28 +93,109 @@ def gemv_roofline(steps: int, warmup: int):
     ws = [synth.mxfp4_uniform(GEMV_N, GEMV_K, f"bench.c1.{i}") for i in range(COPIES)]
     x = synth.normal(GEMV_K, "bench.c1.x", dtype=torch.float16)
     y = torch.empty(GEMV_N, dtype=torch.float16, device="cuda")
-    for i in range(warmup):
-        w, e = ws[i % COPIES]
-        ops.mxfp4_gemv(w, e, x, "f16", y=y)
+
+    def launch_all():
+        for w, e in ws:
+            ops.mxfp4_gemv(w, e, x, "f16", y=y)
+
+    us, launches, wall = _graph_time(launch_all, steps, warmup, eager)
+    return {"us": us, "launches": launches, "wall_s": wall, "gbs": GEMV_BYTES / (us * 1e-6) / 1e9}
+
+
+def copy_roofline(steps: int, warmup: int, eager: bool = False):
+    import torch
+
+    src = [torch.empty(GEMV_BYTES, dtype=torch.uint8, device="cuda") for _ in range(COPIES)]
+    dst = torch.empty(GEMV_BYTES, dtype=torch.uint8, device="cuda")
+
+    def launch_all():
+        for t in src:
+            dst.copy_(t)
+
+    us, launches, wall = _graph_time(launch_all, steps, warmup, eager)
+    return {"us": us, "launches": launches, "wall_s": wall, "gbs": 2 * GEMV_BYTES / (us * 1e-6) / 1e9}
+
+
+def decode_rate(steps: int, warmup: int):
+    """Prefill the C5 prompt, then time `steps` greedy decode steps (graph replays) after `warmup`."""
+    import numpy as np
+    import torch
+
+    from hwnpu_amd import synth
+    from hwnpu_amd.qwen3 import Qwen3
+
+    total = warmup + steps
+    m = Qwen3(**C5, max_ctx=PROMPT + total + 8, max_prompt=PROMPT)
+    m.synth(seed=0, std=0.02)
+    prompt = synth.uniform_int(PROMPT, 0, C5["vocab"], "c5.prompt").cpu().numpy().astype(np.int32)
+    s = torch.cuda.current_stream()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        w, e = ws[i % COPIES]
-        starts[i].record()
-        ops.mxfp4_gemv(w, e, x, "f16", y=y)
-        ends[i].record()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    m.prefill(prompt[:16], 0)  # first use: code objects load outside the timed prefill
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))  # us
-    avg_us = sum(per) / len(per)
-    return {
-        "avg_us": avg_us,
-        "median_us": per[len(per) // 2],
-        "wall_s": wall,
-        "gbs": GEMV_BYTES / (avg_us * 1e-6) / 1e9,
-    }
+    a.record(s)
+    m.prefill(prompt, 0)
+    b.record(s)
+    b.synchronize()
+    prefill_s = a.elapsed_time(b) / 1e3
+    m.decode(max(warmup, 1))  # captures the step graph
+    torch.cuda.synchronize()
+    a.record(s)
+    m.decode(steps)
+    b.record(s)
+    b.synchronize()
+    dec_s = a.elapsed_time(b) / 1e3
+    first = PROMPT + max(warmup, 1)  # position of the first timed step
+    toks = m.history(PROMPT, 8)
+    m.close()
+    p_mean = first + (steps - 1) / 2
+    step_bytes = LIN_BYTES + HEAD_BYTES + KV_POS_BYTES * (p_mean + 1) + KV_POS_BYTES + C5["hidden"] * 2
+    return {"tok_s": steps / dec_s, "ms_per_tok": dec_s / steps * 1e3, "prefill_tok_s": PROMPT / prefill_s,
+            "prefill_ms": prefill_s * 1e3, "step_bytes": step_bytes, "first_tokens": [int(t) for t in toks]}
+
+
+def cpu_decode_baseline():
+    """The reference's CPU decode step restated (oracle, test infrastructure), on a bounded sample
+    scaled to one token: one layer's linears through mxfp4.Run and its attention at 1152 keys, each
+    times 28, plus the head in fp32 sgemm; every host core."""
+    import numpy as np
+
+    from oracle import oracle
+
+    rng = np.random.default_rng(0)
+    H, I, V = C5["hidden"], C5["inter"], C5["vocab"]
+    mats = [(4096, H), (H, 2048), (2 * I, H), (H, I)]  # qkv, o, gate_up, down
+    ws = [(rng.integers(0, 256, (n, k // 2), dtype=np.uint8), rng.integers(120, 125, (n, k // 32), dtype=np.uint8))
+          for n, k in mats]
+    xs = {k: oracle.vec_quantize(rng.standard_normal(k).astype(np.float32)) for _, k in mats}
+    L = 1152
+    q = rng.standard_normal((16, 128)).astype(np.float32)
+    kv = rng.standard_normal((8, L, 128)).astype(np.float32)
+    head = (rng.standard_normal((V, H)) * 0.02).astype(np.float32)
+    xh = rng.standard_normal((1, H)).astype(np.float32)
+    threads = oracle.max_threads()
+
+    def med(fn, n):
+        ts = []
+        for _ in range(n):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return sorted(ts)[len(ts) // 2]
+
+    def lin():
+        for (w, e), (n, k) in zip(ws, mats):
+            qv, sv = xs[k]
+            oracle.mxfp4_run(w, e, qv[None, :], sv[None, :], threads=threads)
+
+    t_lin = med(lin, 7)
+    t_att = med(lambda: oracle.attn_decode(q, kv, kv, 128 ** -0.5, threads=threads), 5)
+    t_head = med(lambda: oracle.sgemm(xh, head, transb=True, threads=threads), 5)
+    per_tok = 28 * (t_lin + t_att) + t_head
+    return {"value": round(1.0 / per_tok, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"one layer's 4 MXFP4 linears via mxfp4.Run (median of 7: {t_lin * 1e3:.2f} ms) and attention "
+                       f"at 1152 keys (median of 5: {t_att * 1e3:.2f} ms), each x28, plus the fp32 head "
+                       f"({t_head * 1e3:.2f} ms): {per_tok * 1e3:.1f} ms a token")}
 
 
 def cpu_gemv_baseline(budget_s: float = 12.0):
@@ -88,10 +228,11 @@ def cpu_gemv_baseline(budget_s: float = 12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="gemv", choices=["gemv"])
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--eager", action="store_true", help="gemv/copy: launch one by one, no graph (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -100,29 +241,48 @@ def main():
     import torch
 
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    r = gemv_roofline(args.steps, args.warmup)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    if args.workload == "copy":
+        r = copy_roofline(args.steps or 3200, args.warmup or 320, args.eager)
+        print(json.dumps({"workload": "copy", "bytes": GEMV_BYTES, "launches": r["launches"],
+                          "us_per_launch": round(r["us"], 3), "gbs_read_plus_write": round(r["gbs"], 1)}))
+        return
+    if args.workload == "gemv":
+        r = gemv_roofline(args.steps or 3200, args.warmup or 320, args.eager)
+        print(json.dumps({"workload": "gemv", "launches": r["launches"], "us_per_launch": round(r["us"], 3),
+                          "gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}))
+        return
+    steps = args.steps if args.steps is not None else 240
+    warmup = args.warmup if args.warmup is not None else 16
+    d = decode_rate(steps, warmup)
+    g = gemv_roofline(3200, 320)
     out = {
-        "metric": "MXFP4 GEMV achieved HBM GB/s (batch-1 decode GEMV, 8192x2048)",
-        "value": round(r["gbs"], 2),
-        "unit": "GB/s",
+        "metric": "decode tok/s at batch 1 (1 GPU); MXFP4 GEMV achieved HBM GB/s vs peak",
+        "value": round(d["tok_s"], 2),
+        "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(r["wall_s"] / args.steps * 1e3, 5),
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(d["ms_per_tok"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "mxfp4*fp16->f32",
-        "data": "synthetic (seeded splitmix64 draws on the GPU)",
-        "config": {"workload": "mxfp4_gemv N=8192 K=2048, 64 rotating weight copies", "n": GEMV_N, "k": GEMV_K},
-        "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel_avg_us": round(r["avg_us"], 3), "bytes_per_launch": GEMV_BYTES},
-        "cpu_baseline": None if args.no_cpu else cpu_gemv_baseline(),
-        "wall_s": round(wall, 3),
+        "data": "synthetic (seed-0 random-init weights and prompt ids drawn on the GPU)",
+        "config": {"workload": "qwen3-shape 28-layer decoder, prompt 1024 then greedy decode at batch 1",
+                   "layers": 28, "hidden": 2048, "heads": 16, "kv_heads": 8, "head_dim": 128, "ffn": 6144,
+                   "vocab": 151936, "prompt": PROMPT, "decode_tokens": steps + warmup, "weights": "MXFP4",
+                   "kv_cache": "fp16", "step": "one HIP graph replay"},
+        "prefill_tok_s": round(d["prefill_tok_s"], 1),
+        "prefill_ms": round(d["prefill_ms"], 3),
+        "decode_step_hbm": {"bytes_per_token": int(d["step_bytes"]),
+                            "achieved_gbs": round(d["step_bytes"] / (d["ms_per_tok"] * 1e-3) / 1e9, 1),
+                            "frac": round(d["step_bytes"] / (d["ms_per_tok"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "first_tokens": d["first_tokens"],
+        "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_mxfp4_gemv_stream (MXFP4 GEMV 8192x2048, 64 distinct copies, graph)",
+                     "us_per_launch": round(g["us"], 3), "bytes_per_launch": GEMV_BYTES},
+        "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(),
     }
     print(json.dumps(out))
 

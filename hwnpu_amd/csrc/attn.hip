@@ -13,6 +13,7 @@
 // unnormalized output, max and sum per query head to a workspace that a merge kernel combines
 // with the rule of the reference's Merge (internal/llm/paged/paged.go:252-310).
 #include "hwk_common.h"
+#include "internal.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -141,7 +142,8 @@ __device__ __forceinline__ void attend_tile(const Tile<I8> &t, const half8 (&qa)
   }
 }
 
-// Workgroup (kv head h, chunk c) of W waves over keys [c*chunk, min((c+1)*chunk, len)). With one
+// Workgroup (kv head h, chunk c) of W waves over keys [c*chunk, min((c+1)*chunk, len)), len plus
+// *pos when pos is given (a chunk past the keys in use leaves l = 0, which the merge skips). With one
 // chunk a head it writes out directly; otherwise its partial (o unnormalized, m in natural log
 // units, l) per query head g of h goes to workspace slot (h*nchunk + c)*G + g for k_attn_merge.
 template <int G, bool I8, int W>
@@ -150,12 +152,14 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const uint4 *__restrict_
                                                         const uint16_t *__restrict__ vs, float *__restrict__ ws_o,
                                                         float *__restrict__ ws_m, float *__restrict__ ws_l,
                                                         void *__restrict__ out,
-                                                        int mode, uint32_t len, uint32_t cap, uint32_t chunk,
-                                                        uint32_t nchunk, float scale_log2) {
+                                                        int mode, const int32_t *__restrict__ pos, uint32_t len,
+                                                        uint32_t cap, uint32_t chunk, uint32_t nchunk,
+                                                        float scale_log2) {
   __shared__ float sm[W][G], sl[W][G];
   __shared__ float sacc[W][G][128];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t h = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
+  if (pos) len += (uint32_t)*pos;  // the keys in use, read on the device (a replayed step graph)
   const uint32_t begin = c * chunk;
   const uint32_t end = begin + chunk < len ? begin + chunk : len;
   const size_t head_base = (size_t)h * cap;
@@ -241,6 +245,127 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const uint4 *__restrict_
     }
   }
 }
+// The model's decode step form of k_attn_decode: q (and, in the chunk holding the new position,
+// the new k and v) made from the fp32 projection in the prologue, written to the cache there
+// before this workgroup reads it. Every workgroup leaves its chunk's partial (o unnormalized, m in
+// natural-log units, l) in the workspace for the consumer's merge, as k_attn_decode does with
+// several chunks. Position p = *pos; keys [0, p] are in use.
+template <int G, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                                      const float *__restrict__ kn, const float *__restrict__ cos_t,
+                                                      const float *__restrict__ sin_t, double eps, f16 *__restrict__ kc,
+                                                      f16 *__restrict__ vc, float *__restrict__ ws_o,
+                                                      float *__restrict__ ws_m, float *__restrict__ ws_l,
+                                                      const int32_t *__restrict__ pos, uint32_t heads, uint32_t kvh,
+                                                      uint32_t cap, uint32_t chunk, uint32_t nchunk, float scale_log2) {
+  __shared__ float sm[W][G], sl[W][G];
+  __shared__ float sacc[W][G][128];
+  __shared__ __attribute__((aligned(16))) f16 qs[G][128];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t h = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
+  const uint32_t p = (uint32_t)*pos, len = p + 1;
+  const uint32_t begin = c * chunk;
+  const uint32_t end = begin + chunk < len ? begin + chunk : len;
+  const size_t head_base = (size_t)h * cap;
+  constexpr uint32_t STEP = 16 * W;
+  // this wave's first tile goes out before the prologue unless it holds p (written below)
+  Tile<false> ta, tb;
+  uint32_t key = begin + 16 * wave;
+  const bool early = key < end && !(key <= p && p < key + 16);
+  if (early) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, end, lane);
+  // prologue: jobs [0, G) the query heads of h; in the chunk holding p also G (k) and G+1 (v)
+  const uint32_t jobs = (p / chunk == c) ? G + 2 : G;
+  for (uint32_t j = wave; j < jobs; j += W) {
+    const uint32_t row = j < G ? h * G + j : j == G ? heads + h : heads + kvh + h;
+    const float x0 = qkv[(size_t)row * 128 + lane], x1 = qkv[(size_t)row * 128 + lane + 64];
+    if (j == G + 1) {
+      vc[(head_base + p) * 128 + lane] = (f16)x0;
+      vc[(head_base + p) * 128 + lane + 64] = (f16)x1;
+      continue;
+    }
+    float o0, o1;
+    head_norm_rope(x0, x1, j < G ? qn : kn, cos_t[(size_t)p * 64 + lane], sin_t[(size_t)p * 64 + lane], eps, lane,
+                   o0, o1);
+    if (j < G) {
+      qs[j][lane] = (f16)o0;
+      qs[j][lane + 64] = (f16)o1;
+    } else {
+      kc[(head_base + p) * 128 + lane] = (f16)o0;
+      kc[(head_base + p) * 128 + lane + 64] = (f16)o1;
+    }
+  }
+  __syncthreads();  // q in LDS; the new cache rows visible to the workgroup's loads
+  if (!early && key < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, end, lane);
+  half8 qa[4];
+  {
+    const int g = lane & 15, grp = lane >> 4;
+#pragma unroll
+    for (int s2 = 0; s2 < 4; s2++)
+      qa[s2] = g < G ? *(const half8 *)&qs[g][s2 * 32 + grp * 8] : half8_of(make_uint4(0, 0, 0, 0));
+  }
+  float acc[G][8], m[G], l[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    m[g] = -__builtin_inff();
+    l[g] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
+  }
+  while (key < end) {
+    if (key + STEP < end) load_tile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + STEP, end, lane);
+    attend_tile<G, false>(ta, qa, key, end, scale_log2, lane, m, l, acc);
+    key += STEP;
+    if (key >= end) break;
+    if (key + STEP < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + STEP, end, lane);
+    attend_tile<G, false>(tb, qa, key, end, scale_log2, lane, m, l, acc);
+    key += STEP;
+  }
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+      float a = acc[g][d];
+      a += __shfl_xor(a, 16, 64);
+      a += __shfl_xor(a, 32, 64);
+      acc[g][d] = a;
+    }
+  if (lane < 16) {
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+      for (int d = 0; d < 8; d++) sacc[wave][g][lane * 8 + d] = acc[g][d];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      sm[wave][g] = m[g];
+      sl[wave][g] = l[g];
+    }
+  }
+  __syncthreads();
+  const size_t base = ((size_t)h * nchunk + c) * G;
+  for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
+    const uint32_t g = i / 128, d = i % 128;
+    float top = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < W; w++) top = fmaxf(top, sm[w][g]);
+    float o = 0.0f, lsum = 0.0f;
+    if (top != -__builtin_inff()) {
+#pragma unroll
+      for (int w = 0; w < W; w++) {
+        const float wt = exp2f(sm[w][g] - top);
+        o += wt * sacc[w][g][d];
+        lsum += wt * sl[w][g];
+      }
+    }
+    ws_o[(base + g) * 128 + d] = o;
+    if (d == 0) {
+      ws_m[base + g] = top * kLn2;
+      ws_l[base + g] = lsum;
+    }
+  }
+}
+
 // Merge of chunks (the reference's Merge rule, paged.go:252-310): top = the largest m among
 // chunks with l > 0; a chunk weighs exp(m - top), times l when its o is normalized; out = the
 // weighted sum of o over the weighted sum of l. Block (row, slice of 32 dims) of 256 threads: the
@@ -369,6 +494,15 @@ HWK_API size_t hwk_attn_workspace_bytes(const hwk_attn_params *p) {
 HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const void *v, const void *k_scale,
                               const void *v_scale, void *out, void *workspace, size_t workspace_bytes,
                               const hwk_attn_params *p) {
+  return hwk::attn_decode_dev((hipStream_t)stream, q, k, v, k_scale, v_scale, out, workspace, workspace_bytes, p,
+                              nullptr, 0);
+}
+
+}  // extern "C"
+
+char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const void *v, const void *k_scale,
+                           const void *v_scale, void *out, void *workspace, size_t workspace_bytes,
+                           const hwk_attn_params *p, const int32_t *pos, uint32_t len_add) {
   HWK_CHECK(p, "hwk_attn_decode: null params");
   HWK_CHECK(q && k && v && out && workspace, "hwk_attn_decode: null pointer");
   HWK_CHECK(p->head_dim == 128, "hwk_attn_decode: head_dim %u (128 only)", p->head_dim);
@@ -393,7 +527,8 @@ HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const 
   float *ws_m = ws_o + slots * 128;
   float *ws_l = ws_m + slots;
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
-  hipStream_t st = (hipStream_t)stream;
+  HWK_CHECK(!pos || p->len == p->capacity, "attn_decode_dev: a device length needs the grid of the capacity");
+  const uint32_t len = pos ? len_add : p->len;
   constexpr int W = 4;
   const dim3 grid(p->kv_heads * nchunk), block(64 * W);
   const uint16_t *ks = (const uint16_t *)k_scale, *vs = (const uint16_t *)v_scale;
@@ -401,10 +536,10 @@ HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const 
 #define HWK_ATTN_LAUNCH(GG)                                                                                         \
   if (p->kv_int8)                                                                                                   \
     hipLaunchKernelGGL((k_attn_decode<GG, true, W>), grid, block, 0, st, (const uint4 *)q, k, v, ks, vs, ws_o,     \
-                       ws_m, ws_l, out, mode, p->len, p->capacity, chunk, nchunk, scale_log2);                     \
+                       ws_m, ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, scale_log2);               \
   else                                                                                                              \
     hipLaunchKernelGGL((k_attn_decode<GG, false, W>), grid, block, 0, st, (const uint4 *)q, k, v, ks, vs, ws_o,    \
-                       ws_m, ws_l, out, mode, p->len, p->capacity, chunk, nchunk, scale_log2);
+                       ws_m, ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, scale_log2);
   if (G == 1) {
     HWK_ATTN_LAUNCH(1)
   } else if (G == 2) {
@@ -419,6 +554,58 @@ HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const 
                      p->heads, 128u, G, mode);
   return hwk::launched("hwk_attn_decode (merge)");
 }
+
+
+uint32_t hwk::attn_step_chunks(const hwk_attn_params *p) {
+  // about 8192 keys a chunk, at least 8 chunks a kv head (at most 64), a multiple of 128 keys
+  uint32_t n = (uint32_t)(((uint64_t)p->capacity * p->kv_heads + 8191) / 8192);
+  n = n < 8 ? 8 : n > 64 ? 64 : n;
+  uint32_t chunk = (p->capacity + n - 1) / n;
+  chunk = (chunk + 127) / 128 * 128;
+  return chunk;
+}
+
+size_t hwk::attn_step_workspace_bytes(const hwk_attn_params *p) {
+  const uint32_t chunk = attn_step_chunks(p), nchunk = (p->capacity + chunk - 1) / chunk;
+  return (size_t)p->heads * nchunk * (128 + 2) * sizeof(float);
+}
+
+char *hwk::attn_decode_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *cos_t,
+                            const float *sin_t, double eps, void *kc, void *vc, void *workspace, size_t workspace_bytes,
+                            const hwk_attn_params *p, const int32_t *pos, uint32_t *nchunk_out) {
+  HWK_CHECK(p && qkv && qn && kn && cos_t && sin_t && kc && vc && workspace && pos, "attn_decode_step: null argument");
+  HWK_CHECK(p->head_dim == 128 && !p->kv_int8, "attn_decode_step: fp16 caches of head_dim 128 only");
+  HWK_CHECK(p->kv_heads > 0 && p->heads % p->kv_heads == 0, "attn_decode_step: %u heads over %u", p->heads, p->kv_heads);
+  const uint32_t G = p->heads / p->kv_heads;
+  HWK_CHECK(G == 1 || G == 2 || G == 4, "attn_decode_step: %u query heads a kv head", G);
+  HWK_CHECK(workspace_bytes >= attn_step_workspace_bytes(p), "attn_decode_step: workspace too small");
+  const uint32_t chunk = attn_step_chunks(p), nchunk = (p->capacity + chunk - 1) / chunk;
+  const uint64_t slots = (uint64_t)p->heads * nchunk;
+  float *ws_o = (float *)workspace, *ws_m = ws_o + slots * 128, *ws_l = ws_m + slots;
+  const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
+  constexpr int W = 8;
+#define HWK_STEP(GG)                                                                                               \
+  hipLaunchKernelGGL((k_attn_step<GG, W>), dim3(p->kv_heads * nchunk), dim3(64 * W), 0, st, qkv, qn, kn, cos_t,   \
+                     sin_t, eps, (f16 *)kc, (f16 *)vc, ws_o, ws_m, ws_l, pos, p->heads, p->kv_heads, p->capacity,  \
+                     chunk, nchunk, scale_log2)
+  if (G == 1) HWK_STEP(1);
+  else if (G == 2) HWK_STEP(2);
+  else HWK_STEP(4);
+#undef HWK_STEP
+  if (nchunk_out) *nchunk_out = nchunk;
+  return hwk::launched("attn_decode_step");
+}
+
+char *hwk::attn_merge_ws(hipStream_t st, const void *workspace, void *out, const hwk_attn_params *p, uint32_t nchunk) {
+  const uint32_t G = p->heads / p->kv_heads;
+  const uint64_t slots = (uint64_t)p->heads * nchunk;
+  const float *ws_o = (const float *)workspace, *ws_m = ws_o + slots * 128, *ws_l = ws_m + slots;
+  hipLaunchKernelGGL((k_attn_merge<true>), dim3(p->heads, 4), dim3(256), 0, st, ws_o, ws_m, ws_l, out, nchunk,
+                     p->heads, 128u, G, HWK_OUT_F16);
+  return hwk::launched("attn_merge_ws");
+}
+
+extern "C" {
 
 HWK_API char *hwk_kv_quantize_i8(void *stream, const void *x, void *q, void *scale, uint32_t rows,
                                  uint32_t head_dim) {

@@ -6,6 +6,7 @@
 // (v_dot2), applies the block's power-of-two scale to the block's fp32 sum (exact), and sums the
 // lanes of a row with cross-lane shuffles. x stays in registers for all of a wave's rows.
 #include "hwk_common.h"
+#include "internal.h"
 #include "synth.h"
 
 namespace {
@@ -174,6 +175,183 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_stream(const uint4 *__restri
   }
 }
 
+// Sum of a float64 over the wave.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Where the decode-step GEMV's x comes from.
+enum XMode { X_F16 = 0, X_NORM = 1, X_MERGE = 2 };
+
+struct XIn {
+  const uint4 *x16;  // X_F16: x itself
+  const float *h;    // X_NORM: the fp32 residual and the norm weights
+  const float *nw;
+  double eps;
+  const float *ws;   // X_MERGE: attention partials, o (slots, 128) | m (slots) | l (slots)
+  uint32_t G, nchunk;
+};
+
+constexpr uint32_t kMergeChunks = 8;  // chunks a kv head the X_MERGE prologue takes
+
+// The decode-step GEMV (64 lanes a row, BPL blocks a lane, nb <= 64*BPL). The workgroup first puts
+// x in LDS, with one round of global loads (issued after the first row set's weight loads, which
+// overlap them): copied (X_F16); made from the fp32 residual h by RMSNorm (X_NORM); or merged from
+// the split attention's chunk partials with the rule of the reference's Merge (X_MERGE). Then its
+// waves stream row sets as k_mxfp4_gemv_stream does, x read from LDS. SWIGLU: a row set holds
+// (gate, up) row pairs and the output is fp16 silu(gate) * up at the pair's index.
+template <int BPL, int RPW, int XM, bool SWIGLU, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restrict__ w, const uint8_t *__restrict__ e,
+                                                           XIn in, void *__restrict__ y, uint32_t n, uint32_t nb,
+                                                           int mode) {
+  static_assert(!SWIGLU || RPW % 2 == 0, "SwiGLU pairs rows");
+  constexpr int NT = 64 * WPB;
+  constexpr int PER = (64 * BPL * 32 + NT - 1) / NT;  // x values a thread makes
+  __shared__ uint4 xs[64 * BPL * 4];
+  __shared__ double red[WPB];
+  const int t = threadIdx.x, lane = t & 63;
+  const uint32_t k = nb * 32;
+  constexpr uint32_t ROWS = RPW;  // 64 lanes a row: a row set is RPW consecutive rows
+  const uint32_t waves = gridDim.x * WPB;
+  uint32_t set = blockIdx.x * WPB + (t >> 6);
+  const uint32_t sets = (n + ROWS - 1) / ROWS;
+  const bool live = set < sets;
+  // the first row set's loads go out before x is made, so that they overlap its latency
+  RowSet<BPL, RPW> cur, nxt;
+  if (live) load_rowset<64, BPL, RPW>(cur, w, e, set * ROWS, n, nb, lane);
+  f16 *xh = (f16 *)xs;
+  if constexpr (XM == X_NORM) {
+    float hv[PER], wv[PER];
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+      const uint32_t i = t + j * NT;
+      hv[j] = i < k ? in.h[i] : 0.0f;
+      wv[j] = i < k ? in.nw[i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < PER; j++) ss += (double)hv[j] * (double)hv[j];
+    ss = wave_sum_f64(ss);
+    if (lane == 0) red[t >> 6] = ss;
+    __syncthreads();
+    ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < WPB; i++) ss += red[i];
+    const float r = (float)(1.0 / sqrt(ss / (double)k + in.eps));
+#pragma unroll
+    for (int j = 0; j < PER; j++)
+      if (t + j * NT < k) xh[t + j * NT] = (f16)((hv[j] * r) * wv[j]);
+  } else if constexpr (XM == X_MERGE) {
+    const uint32_t slots = (k / 128) * in.nchunk;
+    const float *wm = in.ws + (size_t)slots * 128, *wl = wm + slots;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+      const uint32_t i = t + j * NT;
+      if (i >= k) break;
+      const uint32_t hq = i >> 7, d = i & 127, hk = hq / in.G, g = hq % in.G;
+      float mc[kMergeChunks], lc[kMergeChunks], oc[kMergeChunks];
+#pragma unroll
+      for (uint32_t c = 0; c < kMergeChunks; c++) {
+        const size_t slot = ((size_t)hk * in.nchunk + c) * in.G + g;
+        const bool ok = c < in.nchunk;
+        mc[c] = ok ? wm[slot] : 0.0f;
+        lc[c] = ok ? wl[slot] : 0.0f;
+        oc[c] = ok ? in.ws[slot * 128 + d] : 0.0f;
+      }
+      float top = -__builtin_inff();
+#pragma unroll
+      for (uint32_t c = 0; c < kMergeChunks; c++)
+        if (lc[c] > 0.0f) top = fmaxf(top, mc[c]);
+      float num = 0.0f, den = 0.0f;
+      if (top != -__builtin_inff()) {
+#pragma unroll
+        for (uint32_t c = 0; c < kMergeChunks; c++)
+          if (lc[c] > 0.0f) {
+            const float wt = expf(mc[c] - top);
+            num += wt * oc[c];
+            den += wt * lc[c];
+          }
+      }
+      xh[i] = (f16)(den > 0.0f ? num / den : 0.0f);
+    }
+  } else {
+    for (uint32_t i = t; i < nb * 4; i += NT) xs[i] = in.x16[i];
+  }
+  __syncthreads();
+  if (!live) return;
+  uint4 xr[BPL][4];
+#pragma unroll
+  for (int j = 0; j < BPL; j++) {
+    const uint32_t b = j * 64 + lane;
+#pragma unroll
+    for (int q = 0; q < 4; q++) xr[j][q] = b < nb ? xs[b * 4 + q] : make_uint4(0, 0, 0, 0);
+  }
+  for (;;) {
+    const uint32_t next = set + waves;
+    if (next < sets) load_rowset<64, BPL, RPW>(nxt, w, e, next * ROWS, n, nb, lane);
+    float v[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < BPL; j++) {
+        float d0 = 0.0f, d1 = 0.0f;
+        const uint32_t cw[4] = {cur.c[i][j].x, cur.c[i][j].y, cur.c[i][j].z, cur.c[i][j].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<0>(cw[q]), h2_of_bits(xr[j][q].x), d0, false);
+          d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<1>(cw[q]), h2_of_bits(xr[j][q].y), d1, false);
+          d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<2>(cw[q]), h2_of_bits(xr[j][q].z), d0, false);
+          d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<3>(cw[q]), h2_of_bits(xr[j][q].w), d1, false);
+        }
+        acc += (d0 + d1) * e8m0_scale(cur.s[i][j]);
+      }
+      v[i] = group_sum<64>(acc);
+    }
+    if (lane == 0) {
+      const uint32_t r0 = set * ROWS;
+      if constexpr (SWIGLU) {
+#pragma unroll
+        for (int i = 0; i < RPW; i += 2) {
+          if (r0 + i + 1 < n) {
+#pragma clang fp contract(off)
+            const float g = v[i], u = v[i + 1];
+            ((f16 *)y)[(r0 + i) / 2] = (f16)(g / (1.0f + (float)exp(-(double)g)) * u);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < RPW; i++)
+          if (r0 + i < n) store_out(y, r0 + i, v[i], mode);
+      }
+    }
+    if (next >= sets) break;
+    set = next;
+    cur = nxt;
+  }
+}
+
+// RMSNorm of fp32 rows to fp16, one workgroup a row (the rounding of k_mxfp4_gemv_x's NORM).
+__global__ __launch_bounds__(256) void k_rmsnorm_f16(const float *__restrict__ h, const float *__restrict__ nw,
+                                                     double eps, f16 *__restrict__ out, uint32_t k) {
+  __shared__ double red[4];
+  const int t = threadIdx.x, lane = t & 63;
+  const float *hr = h + (size_t)blockIdx.x * k;
+  double ss = 0.0;
+  for (uint32_t i = t; i < k; i += 256) {
+    const double v = (double)hr[i];
+    ss += v * v;
+  }
+  ss = wave_sum_f64(ss);
+  if (lane == 0) red[t >> 6] = ss;
+  __syncthreads();
+  ss = ((red[0] + red[1]) + red[2]) + red[3];
+  const float r = (float)(1.0 / sqrt(ss / (double)k + eps));
+  for (uint32_t i = t; i < k; i += 256) out[(size_t)blockIdx.x * k + i] = (f16)((hr[i] * r) * nw[i]);
+}
+
 // ---- the encoder (reference internal/mxfp4/encode.go:11-78), one thread a block, in float64
 // with every product and sum rounded on its own, as the reference computes it ----
 
@@ -257,14 +435,16 @@ __global__ void k_mxfp4_encode(const float *__restrict__ x, uint8_t *__restrict_
 }
 
 // Block b of a (rows, k) matrix of N(0, std) values: element i = b*32 + j of the normal stream,
-// float32(z * std), then encoded.
+// float32(z * std), then encoded. Row r of the matrix lands at row row0 + r*stride of the output
+// (stride 1, row0 0: in place; stride 2: interleaved with another matrix's rows).
 __global__ void k_synth_mxfp4(uint8_t *__restrict__ w, uint8_t *__restrict__ e, uint64_t nblocks, uint64_t key,
-                              float stdv) {
+                              float stdv, uint32_t nb, uint32_t stride, uint32_t row0) {
   uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= nblocks) return;
   float v[32];
   for (int j = 0; j < 32; j++) v[j] = (float)(hwk::normal_at(key, b * 32 + j) * (double)stdv);
-  encode_block(v, w + b * 16, e + b);
+  const uint64_t r = b / nb, d = ((uint64_t)row0 + r * stride) * nb + b % nb;
+  encode_block(v, w + d * 16, e + d);
 }
 
 // Tuning knobs read once per process: HWK_MXFP4_RPW (row sets of 1, 2, 4 or 8 rows a lane group;
@@ -408,8 +588,88 @@ HWK_API char *hwk_synth_mxfp4(void *stream, void *w, void *e, uint32_t rows, uin
   const uint64_t nblocks = (uint64_t)rows * (k / 32);
   if (nblocks == 0) return nullptr;
   hipLaunchKernelGGL(k_synth_mxfp4, dim3((uint32_t)((nblocks + 127) / 128)), dim3(128), 0, (hipStream_t)stream,
-                     (uint8_t *)w, (uint8_t *)e, nblocks, key, hwk::f32_of_bits(std_bits));
+                     (uint8_t *)w, (uint8_t *)e, nblocks, key, hwk::f32_of_bits(std_bits), k / 32, 1u, 0u);
   return hwk::launched("hwk_synth_mxfp4");
 }
 
 }  // extern "C"
+
+namespace hwk {
+
+namespace {
+
+// 8 waves a workgroup: x is made once for 8 waves' rows, and the model's shapes still give every
+// CU whole workgroups (qkv: 2048 row sets, 256 workgroups; gate_up: 6144, 768).
+template <int BPL, int XM, bool SWIGLU>
+void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb, int mode) {
+  constexpr int WPB = 8, RPW = 2;
+  const uint32_t sets = (n + RPW - 1) / RPW;
+  const uint32_t waves = sets < stream_waves() ? sets : stream_waves();
+  hipLaunchKernelGGL((k_mxfp4_gemv_x<BPL, RPW, XM, SWIGLU, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0,
+                     st, (const uint4 *)w, (const uint8_t *)e, in, y, n, nb, mode);
+}
+
+template <int XM, bool SWIGLU>
+void launch_x_bpl(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb,
+                  int mode) {
+  switch ((nb + 63) / 64) {
+    case 1: launch_x<1, XM, SWIGLU>(st, w, e, in, y, n, nb, mode); break;
+    case 2: launch_x<2, XM, SWIGLU>(st, w, e, in, y, n, nb, mode); break;
+    case 3: launch_x<3, XM, SWIGLU>(st, w, e, in, y, n, nb, mode); break;
+    default: launch_x<4, XM, SWIGLU>(st, w, e, in, y, n, nb, mode); break;
+  }
+}
+
+}  // namespace
+
+char *mxfp4_gemv_x(hipStream_t st, const void *w, const void *e, const void *x16, const float *h, const float *nw,
+                   double eps, void *y, uint32_t n, uint32_t k, int out_mode, bool swiglu) {
+  HWK_CHECK(w && e && y && (h ? nw != nullptr : x16 != nullptr), "mxfp4_gemv_x: null pointer");
+  HWK_CHECK(k % 32 == 0 && k > 0 && k <= 64 * 4 * 32, "mxfp4_gemv_x: k=%u (a multiple of 32 up to 8192)", k);
+  HWK_CHECK(!swiglu || n % 2 == 0, "mxfp4_gemv_x: SwiGLU over %u rows (pairs)", n);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "mxfp4_gemv_x: out_mode %d", out_mode);
+  HWK_CHECK(aligned(w, 16) && (h || aligned(x16, 16)), "mxfp4_gemv_x: w and x must be 16-byte aligned");
+  if (n == 0) return nullptr;
+  XIn in{(const uint4 *)x16, h, nw, eps, nullptr, 0, 0};
+  const uint32_t nb = k / 32;
+  if (swiglu) {
+    if (h) launch_x_bpl<X_NORM, true>(st, w, e, in, y, n, nb, out_mode);
+    else launch_x_bpl<X_F16, true>(st, w, e, in, y, n, nb, out_mode);
+  } else {
+    if (h) launch_x_bpl<X_NORM, false>(st, w, e, in, y, n, nb, out_mode);
+    else launch_x_bpl<X_F16, false>(st, w, e, in, y, n, nb, out_mode);
+  }
+  return launched("mxfp4_gemv_x");
+}
+
+char *mxfp4_gemv_merge(hipStream_t st, const void *w, const void *e, const void *workspace, uint32_t heads,
+                       uint32_t G, uint32_t nchunk, void *y, uint32_t n, int out_mode) {
+  HWK_CHECK(w && e && workspace && y, "mxfp4_gemv_merge: null pointer");
+  HWK_CHECK(nchunk >= 1 && nchunk <= kMergeChunks, "mxfp4_gemv_merge: %u chunks (1..%u)", nchunk, kMergeChunks);
+  HWK_CHECK(G >= 1 && heads % G == 0 && heads * 128 <= 64 * 4 * 32, "mxfp4_gemv_merge: %u heads, G %u", heads, G);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "mxfp4_gemv_merge: out_mode %d", out_mode);
+  HWK_CHECK(aligned(w, 16), "mxfp4_gemv_merge: w must be 16-byte aligned");
+  if (n == 0) return nullptr;
+  XIn in{nullptr, nullptr, nullptr, 0.0, (const float *)workspace, G, nchunk};
+  launch_x_bpl<X_MERGE, false>(st, w, e, in, y, n, heads * 128 / 32, out_mode);
+  return launched("mxfp4_gemv_merge");
+}
+
+char *synth_mxfp4_rows(hipStream_t st, void *w, void *e, uint32_t rows, uint32_t k, uint64_t key, float stdv,
+                       uint32_t stride, uint32_t row0) {
+  HWK_CHECK(w && e && k % 32 == 0 && k > 0 && stride > 0, "synth_mxfp4_rows: bad arguments");
+  const uint64_t nblocks = (uint64_t)rows * (k / 32);
+  if (nblocks == 0) return nullptr;
+  hipLaunchKernelGGL(k_synth_mxfp4, dim3((uint32_t)((nblocks + 127) / 128)), dim3(128), 0, st, (uint8_t *)w,
+                     (uint8_t *)e, nblocks, key, stdv, k / 32, stride, row0);
+  return launched("synth_mxfp4_rows");
+}
+
+char *rmsnorm_f16(hipStream_t st, const float *h, const float *nw, double eps, void *out, uint32_t rows, uint32_t k) {
+  HWK_CHECK(h && nw && out, "rmsnorm_f16: null pointer");
+  if (rows == 0 || k == 0) return nullptr;
+  hipLaunchKernelGGL(k_rmsnorm_f16, dim3(rows), dim3(256), 0, st, h, nw, eps, (f16 *)out, k);
+  return launched("rmsnorm_f16");
+}
+
+}  // namespace hwk

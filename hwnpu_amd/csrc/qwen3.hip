@@ -1,0 +1,546 @@
+// The Qwen3 decoder on gfx950 (the 28-layer synthetic model of the decode benchmark): a
+// device-resident session in the shape of the reference's iron.Model (Step(token, pos) -> logits,
+// internal/llm/iron/model.go:578) over the architecture of internal/llm/qwen3 (build.go:107-311;
+// the float64 forward of qwen3_test.go:77-207 is the semantics restated here).
+//
+// Numerics: the residual stream h is fp32. Values cross kernels in fp16 exactly where noted:
+//   x = fp16((h * r) * w)          RMSNorm into every linear (r = float(1/sqrt(mean h^2 + eps)))
+//   q, k = fp16(rope(norm(q)))     per-head RMSNorm before RoPE (cos/sin tables in float32)
+//   v = fp16(v); K/V cache fp16
+//   attn = fp16(softmax(q k^T / sqrt(d)) v)   (fp32 softmax and P.V)
+//   act = fp16(silu(gate) * up)
+// Linears accumulate in fp32 (MXFP4 weights, the fp16 tied head); h += o_proj(attn) and
+// h += down(act) in fp32. The greedy token is the first index of the largest logit.
+//
+// A decode step is five kernels a layer: the norm-fused qkv GEMV; the split attention with the
+// q/k norm, RoPE and KV append folded in; o_proj, which merges the attention's chunks as it
+// makes its input; the norm- and SwiGLU-fused gate_up GEMV; down. Then four more: embed, final
+// norm, head, argmax. Its token
+// and position are read on the device (hist[pos], pos), and the argmax writes the next token
+// and advances pos, so one captured graph replays for every step.
+#include <math.h>
+#include <string>
+#include <vector>
+
+#include "hwk_common.h"
+#include "internal.h"
+#include "synth.h"
+
+namespace {
+
+// ---- glue kernels (K6) ----
+
+// h[t] = fp32 of embedding row hist[*pos + base + t]
+__global__ __launch_bounds__(256) void k_embed(const int32_t *__restrict__ hist, const int32_t *__restrict__ pos,
+                                               uint32_t base, const f16 *__restrict__ emb, float *__restrict__ h,
+                                               uint32_t hidden, uint32_t vocab) {
+  const uint32_t t = blockIdx.x;
+  uint32_t tok = (uint32_t)hist[(uint32_t)*pos + base + t];
+  if (tok >= vocab) tok = vocab - 1;  // memory safety only: tokens are checked on the host
+  const f16 *row = emb + (size_t)tok * hidden;
+  for (uint32_t i = threadIdx.x; i < hidden; i += 256) h[(size_t)t * hidden + i] = (float)row[i];
+}
+
+// One wave a (token t, head slot): slots [0, heads) are query heads, [heads, heads+kvh) key heads,
+// then value heads. A lane holds dims l and l+64, the pair rotate_half mixes. q and k: per-head
+// RMSNorm with fp32 weights, then RoPE at position *pos + base + t with the float32 tables
+// (reference internal/llm/blocks/blocks.go:412-445), rounded to fp16; q to q16 (t, heads, 128),
+// k to the cache; v rounded to fp16 into the cache.
+__global__ __launch_bounds__(256) void k_qk_rope(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                                 const float *__restrict__ kn, const float *__restrict__ cos_t,
+                                                 const float *__restrict__ sin_t, const int32_t *__restrict__ pos,
+                                                 uint32_t base, f16 *__restrict__ q16, f16 *__restrict__ kc,
+                                                 f16 *__restrict__ vc, uint32_t heads, uint32_t kvh, uint32_t cap,
+                                                 double eps) {
+#pragma clang fp contract(off)
+  const uint32_t slot = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const uint32_t t = blockIdx.y, l = threadIdx.x & 63;
+  const uint32_t slots = heads + 2 * kvh;
+  if (slot >= slots) return;
+  const uint32_t p = (uint32_t)*pos + base + t;
+  const float *x = qkv + (size_t)t * slots * 128 + (size_t)slot * 128;
+  float x0 = x[l], x1 = x[l + 64];
+  if (slot >= heads + kvh) {
+    const uint32_t j = slot - heads - kvh;
+    f16 *dst = vc + ((size_t)j * cap + p) * 128;
+    dst[l] = (f16)x0;
+    dst[l + 64] = (f16)x1;
+    return;
+  }
+  float o0, o1;
+  head_norm_rope(x0, x1, slot < heads ? qn : kn, cos_t[(size_t)p * 64 + l], sin_t[(size_t)p * 64 + l], eps, l, o0, o1);
+  f16 *dst = slot < heads ? q16 + ((size_t)t * heads + slot) * 128
+                          : kc + ((size_t)(slot - heads) * cap + p) * 128;
+  dst[l] = (f16)o0;
+  dst[l + 64] = (f16)o1;
+}
+
+// act (T, inter) fp16 = silu(gate) * up of gu (T, 2*inter) fp32, gate at even columns.
+__global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, f16 *__restrict__ act, uint64_t n) {
+#pragma clang fp contract(off)
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float g = gu[2 * i], u = gu[2 * i + 1];
+  act[i] = (f16)(g / (1.0f + (float)exp(-(double)g)) * u);
+}
+
+__global__ void k_set_i32(int32_t *__restrict__ p, int32_t v) { *p = v; }
+
+constexpr uint32_t kArgBlocks = 64;
+
+__device__ __forceinline__ void better(float &bv, uint32_t &bi, float v, uint32_t i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+// Greedy pick (reference internal/chat/sample.go:80-87: strict >, so the lowest index of the
+// largest value) over kArgBlocks workgroups; the last one to finish reduces their partials in
+// a fixed order, writes the token at hist[*pos + 1], advances *pos and clears the counter for the
+// next call.
+__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uint32_t n, float *__restrict__ part_v,
+                                                uint32_t *__restrict__ part_i, uint32_t *__restrict__ counter,
+                                                int32_t *__restrict__ hist, int32_t *__restrict__ pos) {
+  __shared__ float sv[256];
+  __shared__ uint32_t si[256];
+  __shared__ bool last;
+  const uint32_t t = threadIdx.x;
+  const uint32_t per = (n + kArgBlocks - 1) / kArgBlocks;
+  const uint32_t lo = blockIdx.x * per, hi = lo + per < n ? lo + per : n;
+  float bv = -__builtin_inff();
+  uint32_t bi = 0xffffffffu;
+  for (uint32_t i = lo + t; i < hi; i += 256) better(bv, bi, x[i], i);
+  sv[t] = bv;
+  si[t] = bi;
+  __syncthreads();
+  for (uint32_t s = 128; s > 0; s >>= 1) {
+    if (t < s) better(sv[t], si[t], sv[t + s], si[t + s]);
+    __syncthreads();
+  }
+  if (t == 0) {
+    part_v[blockIdx.x] = sv[0];
+    part_i[blockIdx.x] = si[0];
+    __threadfence();
+    last = atomicAdd(counter, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  if (t < 64) {
+    float v = -__builtin_inff();
+    uint32_t i = 0xffffffffu;
+    if (t < gridDim.x) {
+      v = __builtin_nontemporal_load(&part_v[t]);
+      i = __builtin_nontemporal_load(&part_i[t]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(v, off, 64);
+      const uint32_t oi = __shfl_xor(i, off, 64);
+      better(v, i, ov, oi);
+    }
+    if (t == 0) {
+      const int32_t p = *pos;
+      hist[p + 1] = (int32_t)(i == 0xffffffffu ? 0 : i);
+      *pos = p + 1;
+      *counter = 0;
+    }
+  }
+}
+
+uint64_t fnv64a(const std::string &s) {
+  uint64_t h = 0xCBF29CE484222325ull;
+  for (unsigned char c : s) {
+    h ^= c;
+    h *= 0x100000001B3ull;
+  }
+  return h;
+}
+
+double f64_of_bits(uint64_t b) {
+  double d;
+  memcpy(&d, &b, 8);
+  return d;
+}
+
+__global__ void k_fill_f32(float *__restrict__ p, uint64_t n, float v) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+}  // namespace
+
+struct hwk_qwen3 {
+  hwk_qwen3_config c;
+  double theta, eps;
+  uint32_t qkv_n, att_n;  // rows of the stacked q/k/v projection; width of the attention output
+  size_t bytes = 0;
+  uint8_t *base = nullptr;  // one allocation for weights, cache, state and scratch
+  struct Lin {
+    uint8_t *w, *e;
+    uint32_t rows, cols;
+  };
+  struct Layer {
+    Lin qkv, o, gu, down;
+    float *in_norm, *post_norm, *q_norm, *k_norm;
+    f16 *kc, *vc;
+  };
+  std::vector<Layer> L;
+  float *norm;
+  f16 *embed;
+  float *cos_t, *sin_t;
+  int32_t *hist, *pos;
+  uint32_t *counter, *part_i;
+  float *part_v, *logits;
+  float *h, *qkv, *gu;
+  f16 *x16, *q16, *att16, *a16;
+  void *ws;
+  size_t ws_bytes;
+  hwk_attn_params ap;  // decode attention: len = capacity (the grid), the length read on the device
+  uint32_t host_pos = 0;  // mirror of *pos: where the next step writes
+  bool started = false;
+  hipStream_t cap = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+};
+
+namespace {
+
+struct Carver {
+  size_t off = 0;
+  template <typename T>
+  T *take(uint8_t *base, size_t bytes) {
+    off = (off + 255) / 256 * 256;
+    T *p = base ? (T *)(base + off) : nullptr;
+    off += bytes;
+    return p;
+  }
+};
+
+// Lays the model out in one allocation (base null: only counts the bytes).
+void layout(hwk_qwen3 *m, uint8_t *base) {
+  const hwk_qwen3_config &c = m->c;
+  Carver cv;
+  auto lin = [&](uint32_t rows, uint32_t cols) {
+    hwk_qwen3::Lin l;
+    l.rows = rows;
+    l.cols = cols;
+    l.w = cv.take<uint8_t>(base, (size_t)rows * cols / 2);
+    l.e = cv.take<uint8_t>(base, (size_t)rows * cols / 32);
+    return l;
+  };
+  m->L.resize(c.layers);
+  for (auto &ly : m->L) {
+    ly.qkv = lin(m->qkv_n, c.hidden);
+    ly.o = lin(c.hidden, m->att_n);
+    ly.gu = lin(2 * c.inter, c.hidden);
+    ly.down = lin(c.hidden, c.inter);
+    ly.in_norm = cv.take<float>(base, 4ull * c.hidden);
+    ly.post_norm = cv.take<float>(base, 4ull * c.hidden);
+    ly.q_norm = cv.take<float>(base, 4ull * c.head_dim);
+    ly.k_norm = cv.take<float>(base, 4ull * c.head_dim);
+    ly.kc = cv.take<f16>(base, 2ull * c.kv_heads * c.max_ctx * c.head_dim);
+    ly.vc = cv.take<f16>(base, 2ull * c.kv_heads * c.max_ctx * c.head_dim);
+  }
+  m->norm = cv.take<float>(base, 4ull * c.hidden);
+  m->embed = cv.take<f16>(base, 2ull * c.vocab * c.hidden);
+  m->cos_t = cv.take<float>(base, 4ull * c.max_ctx * (c.head_dim / 2));
+  m->sin_t = cv.take<float>(base, 4ull * c.max_ctx * (c.head_dim / 2));
+  m->hist = cv.take<int32_t>(base, 4ull * (c.max_ctx + 1));
+  m->pos = cv.take<int32_t>(base, 4);
+  m->counter = cv.take<uint32_t>(base, 4);
+  m->part_i = cv.take<uint32_t>(base, 4 * kArgBlocks);
+  m->part_v = cv.take<float>(base, 4 * kArgBlocks);
+  m->logits = cv.take<float>(base, 4ull * c.vocab);
+  const size_t T = c.max_prompt;
+  m->h = cv.take<float>(base, 4 * T * c.hidden);
+  m->qkv = cv.take<float>(base, 4 * T * m->qkv_n);
+  m->gu = cv.take<float>(base, 8 * T * c.inter);
+  m->x16 = cv.take<f16>(base, 2 * T * (c.hidden > c.inter ? c.hidden : c.inter));
+  m->q16 = cv.take<f16>(base, 2 * T * m->att_n);
+  m->att16 = cv.take<f16>(base, 2 * T * m->att_n);
+  m->a16 = cv.take<f16>(base, 2 * T * c.inter);
+  m->ws = cv.take<uint8_t>(base, m->ws_bytes);
+  m->bytes = cv.off;
+}
+
+#define HWK_Q(call)                  \
+  do {                               \
+    if (char *e_ = (call)) return e_; \
+  } while (0)
+
+// The decode step on stream st: the token hist[*pos] at position *pos.
+char *step(hwk_qwen3 *m, hipStream_t st) {
+  const hwk_qwen3_config &c = m->c;
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed, m->h, c.hidden, c.vocab);
+  HWK_Q(hwk::launched("qwen3 embed"));
+  for (auto &ly : m->L) {
+    HWK_Q(hwk::mxfp4_gemv_x(st, ly.qkv.w, ly.qkv.e, nullptr, m->h, ly.in_norm, m->eps, m->qkv, m->qkv_n, c.hidden,
+                            HWK_OUT_F32, false));
+    uint32_t nchunk = 0;
+    HWK_Q(hwk::attn_decode_step(st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t, m->sin_t, m->eps, ly.kc, ly.vc, m->ws,
+                                m->ws_bytes, &m->ap, m->pos, &nchunk));
+    if (nchunk <= 8) {  // the o_proj GEMV merges the chunks itself
+      HWK_Q(hwk::mxfp4_gemv_merge(st, ly.o.w, ly.o.e, m->ws, c.heads, c.heads / c.kv_heads, nchunk, m->h, c.hidden,
+                                  HWK_OUT_ADD_F32));
+    } else {
+      HWK_Q(hwk::attn_merge_ws(st, m->ws, m->att16, &m->ap, nchunk));
+      HWK_Q(hwk_mxfp4_gemv(st, ly.o.w, ly.o.e, m->att16, m->h, c.hidden, m->att_n, HWK_OUT_ADD_F32));
+    }
+    HWK_Q(hwk::mxfp4_gemv_x(st, ly.gu.w, ly.gu.e, nullptr, m->h, ly.post_norm, m->eps, m->a16, 2 * c.inter, c.hidden,
+                            HWK_OUT_F16, true));
+    HWK_Q(hwk_mxfp4_gemv(st, ly.down.w, ly.down.e, m->a16, m->h, c.hidden, c.inter, HWK_OUT_ADD_F32));
+  }
+  HWK_Q(hwk::rmsnorm_f16(st, m->h, m->norm, m->eps, m->x16, 1, c.hidden));
+  HWK_Q(hwk_f16_gemv(st, m->embed, m->x16, m->logits, c.vocab, c.hidden, HWK_OUT_F32));
+  hipLaunchKernelGGL(k_argmax, dim3(kArgBlocks), dim3(256), 0, st, m->logits, c.vocab, m->part_v, m->part_i,
+                     m->counter, m->hist, m->pos);
+  return hwk::launched("qwen3 argmax");
+}
+
+// Rows [0, T) of a prompt piece at positions start .. start+T-1, whose tokens are in hist.
+char *prefill_piece(hwk_qwen3 *m, hipStream_t st, uint32_t T, uint32_t start, bool last_piece) {
+  const hwk_qwen3_config &c = m->c;
+  hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(1), 0, st, m->pos, (int32_t)start);
+  hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed, m->h, c.hidden, c.vocab);
+  HWK_Q(hwk::launched("qwen3 embed"));
+  const uint32_t slots = c.heads + 2 * c.kv_heads;
+  hwk_attn_params pp = m->ap;
+  pp.len = start + T;
+  pp.out_mode = HWK_OUT_F16;
+  for (auto &ly : m->L) {
+    HWK_Q(hwk::rmsnorm_f16(st, m->h, ly.in_norm, m->eps, m->x16, T, c.hidden));
+    HWK_Q(hwk_mxfp4_gemm(st, m->x16, ly.qkv.w, ly.qkv.e, m->qkv, T, m->qkv_n, c.hidden, HWK_OUT_F32));
+    hipLaunchKernelGGL(k_qk_rope, dim3((slots + 3) / 4, T), dim3(256), 0, st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t,
+                       m->sin_t, m->pos, 0u, m->q16, ly.kc, ly.vc, c.heads, c.kv_heads, c.max_ctx, m->eps);
+    HWK_Q(hwk::launched("qwen3 qk_rope"));
+    HWK_Q(hwk_attn_prefill(st, m->q16, ly.kc, ly.vc, m->att16, T, start, &pp));
+    HWK_Q(hwk_mxfp4_gemm(st, m->att16, ly.o.w, ly.o.e, m->h, T, c.hidden, m->att_n, HWK_OUT_ADD_F32));
+    HWK_Q(hwk::rmsnorm_f16(st, m->h, ly.post_norm, m->eps, m->x16, T, c.hidden));
+    HWK_Q(hwk_mxfp4_gemm(st, m->x16, ly.gu.w, ly.gu.e, m->gu, T, 2 * c.inter, c.hidden, HWK_OUT_F32));
+    const uint64_t n = (uint64_t)T * c.inter;
+    hipLaunchKernelGGL(k_swiglu, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, m->gu, m->a16, n);
+    HWK_Q(hwk::launched("qwen3 swiglu"));
+    HWK_Q(hwk_mxfp4_gemm(st, m->a16, ly.down.w, ly.down.e, m->h, T, c.hidden, c.inter, HWK_OUT_ADD_F32));
+  }
+  if (!last_piece) return nullptr;
+  // the head on the last row; the argmax writes hist[start+T] and sets pos = start+T
+  hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(1), 0, st, m->pos, (int32_t)(start + T - 1));
+  HWK_Q(hwk::rmsnorm_f16(st, m->h + (size_t)(T - 1) * c.hidden, m->norm, m->eps, m->x16, 1, c.hidden));
+  HWK_Q(hwk_f16_gemv(st, m->embed, m->x16, m->logits, c.vocab, c.hidden, HWK_OUT_F32));
+  hipLaunchKernelGGL(k_argmax, dim3(kArgBlocks), dim3(256), 0, st, m->logits, c.vocab, m->part_v, m->part_i,
+                     m->counter, m->hist, m->pos);
+  return hwk::launched("qwen3 argmax");
+}
+
+}  // namespace
+
+extern "C" {
+
+HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
+  HWK_CHECK(cfg && out, "hwk_qwen3_new: null argument");
+  const hwk_qwen3_config &c = *cfg;
+  HWK_CHECK(c.layers >= 1 && c.layers <= 256, "hwk_qwen3_new: %u layers", c.layers);
+  HWK_CHECK(c.head_dim == 128, "hwk_qwen3_new: head_dim %u (128 only)", c.head_dim);
+  HWK_CHECK(c.kv_heads > 0 && c.heads % c.kv_heads == 0 && (c.heads / c.kv_heads == 1 || c.heads / c.kv_heads == 2 ||
+                                                           c.heads / c.kv_heads == 4),
+            "hwk_qwen3_new: %u heads over %u kv heads", c.heads, c.kv_heads);
+  HWK_CHECK(c.hidden % 32 == 0 && c.hidden > 0 && c.hidden <= 8192, "hwk_qwen3_new: hidden %u", c.hidden);
+  HWK_CHECK(c.inter % 32 == 0 && c.inter > 0 && c.inter <= 8192, "hwk_qwen3_new: inter %u", c.inter);
+  HWK_CHECK(c.heads * c.head_dim <= 8192, "hwk_qwen3_new: heads*head_dim %u past 8192", c.heads * c.head_dim);
+  HWK_CHECK(c.vocab >= 1 && c.max_ctx >= 2 && c.max_prompt >= 1 && c.max_prompt <= c.max_ctx,
+            "hwk_qwen3_new: vocab %u, max_ctx %u, max_prompt %u", c.vocab, c.max_ctx, c.max_prompt);
+  hwk_qwen3 *m = new hwk_qwen3();
+  m->c = c;
+  m->theta = f64_of_bits(c.theta_bits);
+  m->eps = f64_of_bits(c.eps_bits);
+  m->qkv_n = (c.heads + 2 * c.kv_heads) * c.head_dim;
+  m->att_n = c.heads * c.head_dim;
+  hwk_attn_params &ap = m->ap;
+  ap.heads = c.heads;
+  ap.kv_heads = c.kv_heads;
+  ap.head_dim = c.head_dim;
+  ap.len = c.max_ctx;
+  ap.capacity = c.max_ctx;
+  ap.kv_int8 = 0;
+  const float sc = (float)(1.0 / sqrt((double)c.head_dim));
+  memcpy(&ap.scale_bits, &sc, 4);
+  ap.out_mode = HWK_OUT_F16;
+  ap.split = 0;
+  m->ws_bytes = hwk::attn_step_workspace_bytes(&ap);
+  layout(m, nullptr);
+  hipError_t e = hipMalloc((void **)&m->base, m->bytes);
+  if (e != hipSuccess) {
+    char *err = hwk::errf("hwk_qwen3_new: hipMalloc of %zu bytes: %s", m->bytes, hipGetErrorString(e));
+    delete m;
+    return err;
+  }
+  layout(m, m->base);
+  // RoPE tables in float32 of float64 cos/sin (reference blocks.go:412-425, config.go:152-159)
+  const uint32_t half = c.head_dim / 2;
+  std::vector<float> ct((size_t)c.max_ctx * half), stb((size_t)c.max_ctx * half);
+  for (uint32_t p = 0; p < c.max_ctx; p++)
+    for (uint32_t j = 0; j < half; j++) {
+      const double inv = 1.0 / pow(m->theta, (double)(2 * j) / (double)c.head_dim);
+      const double a = (double)p * inv;
+      ct[(size_t)p * half + j] = (float)cos(a);
+      stb[(size_t)p * half + j] = (float)sin(a);
+    }
+  char *err = nullptr;
+  if ((e = hipMemcpy(m->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
+      (e = hipMemcpy(m->sin_t, stb.data(), stb.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
+      (e = hipMemset(m->hist, 0, 4ull * (c.max_ctx + 1))) != hipSuccess || (e = hipMemset(m->pos, 0, 4)) != hipSuccess ||
+      (e = hipMemset(m->counter, 0, 4)) != hipSuccess ||
+      (e = hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking)) != hipSuccess ||
+      (e = hipDeviceSynchronize()) != hipSuccess)
+    err = hwk::hip_err("hwk_qwen3_new", e);
+  if (err) {
+    hwk_qwen3_free(m);
+    return err;
+  }
+  *out = m;
+  return nullptr;
+}
+
+HWK_API void hwk_qwen3_free(hwk_qwen3 *m) {
+  if (!m) return;
+  if (m->exec) (void)hipGraphExecDestroy(m->exec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  if (m->cap) (void)hipStreamDestroy(m->cap);
+  if (m->base) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(m->base);
+  }
+  delete m;
+}
+
+HWK_API char *hwk_qwen3_synth(hwk_qwen3 *m, void *stream, uint64_t seed, uint32_t std_bits) {
+  HWK_CHECK(m, "hwk_qwen3_synth: null model");
+  hipStream_t st = (hipStream_t)stream;
+  const hwk_qwen3_config &c = m->c;
+  const float sd = hwk::f32_of_bits(std_bits);
+  const uint32_t hd = c.head_dim, qn = c.heads * hd, kn = c.kv_heads * hd;
+  for (uint32_t i = 0; i < c.layers; i++) {
+    hwk_qwen3::Layer &ly = m->L[i];
+    const std::string p = "model.layers." + std::to_string(i) + ".";
+    auto key = [&](const char *name) { return seed ^ fnv64a(p + name); };
+    // q, k, v stacked; rows of one projection are one stream
+    const uint32_t nb = c.hidden / 32;
+    HWK_Q(hwk::synth_mxfp4_rows(st, ly.qkv.w, ly.qkv.e, qn, c.hidden, key("self_attn.q_proj.weight"), sd, 1, 0));
+    HWK_Q(hwk::synth_mxfp4_rows(st, ly.qkv.w, ly.qkv.e, kn, c.hidden, key("self_attn.k_proj.weight"), sd, 1, qn));
+    HWK_Q(hwk::synth_mxfp4_rows(st, ly.qkv.w, ly.qkv.e, kn, c.hidden, key("self_attn.v_proj.weight"), sd, 1, qn + kn));
+    (void)nb;
+    HWK_Q(hwk::synth_mxfp4_rows(st, ly.o.w, ly.o.e, c.hidden, qn, key("self_attn.o_proj.weight"), sd, 1, 0));
+    HWK_Q(hwk::synth_mxfp4_rows(st, ly.gu.w, ly.gu.e, c.inter, c.hidden, key("mlp.gate_proj.weight"), sd, 2, 0));
+    HWK_Q(hwk::synth_mxfp4_rows(st, ly.gu.w, ly.gu.e, c.inter, c.hidden, key("mlp.up_proj.weight"), sd, 2, 1));
+    HWK_Q(hwk::synth_mxfp4_rows(st, ly.down.w, ly.down.e, c.hidden, c.inter, key("mlp.down_proj.weight"), sd, 1, 0));
+    float *ones[4] = {ly.in_norm, ly.post_norm, ly.q_norm, ly.k_norm};
+    const uint32_t lens[4] = {c.hidden, c.hidden, hd, hd};
+    for (int j = 0; j < 4; j++)
+      hipLaunchKernelGGL(k_fill_f32, dim3((lens[j] + 255) / 256), dim3(256), 0, st, ones[j], (uint64_t)lens[j], 1.0f);
+  }
+  hipLaunchKernelGGL(k_fill_f32, dim3((c.hidden + 255) / 256), dim3(256), 0, st, m->norm, (uint64_t)c.hidden, 1.0f);
+  HWK_Q(hwk::launched("hwk_qwen3_synth (norms)"));
+  return hwk_synth_normal(stream, m->embed, (uint64_t)c.vocab * c.hidden, seed ^ fnv64a("model.embed_tokens.weight"),
+                          std_bits, 1);
+}
+
+HWK_API char *hwk_qwen3_tensor(hwk_qwen3 *m, const char *name, void **ptr, size_t *bytes) {
+  HWK_CHECK(m && name && ptr && bytes, "hwk_qwen3_tensor: null argument");
+  const hwk_qwen3_config &c = m->c;
+  std::string n(name);
+  auto put = [&](void *p, size_t b) {
+    *ptr = p;
+    *bytes = b;
+    return (char *)nullptr;
+  };
+  if (n == "norm") return put(m->norm, 4ull * c.hidden);
+  if (n == "embed") return put(m->embed, 2ull * c.vocab * c.hidden);
+  unsigned li = 0;
+  char rest[64] = {0};
+  if (sscanf(name, "layers.%u.%63s", &li, rest) == 2 && li < c.layers) {
+    hwk_qwen3::Layer &ly = m->L[li];
+    std::string r(rest);
+    hwk_qwen3::Lin *lin = nullptr;
+    std::string part;
+    const size_t dot = r.find('.');
+    std::string head = dot == std::string::npos ? r : r.substr(0, dot);
+    part = dot == std::string::npos ? "" : r.substr(dot + 1);
+    if (head == "qkv") lin = &ly.qkv;
+    else if (head == "o") lin = &ly.o;
+    else if (head == "gate_up") lin = &ly.gu;
+    else if (head == "down") lin = &ly.down;
+    if (lin && part == "blocks") return put(lin->w, (size_t)lin->rows * lin->cols / 2);
+    if (lin && part == "scales") return put(lin->e, (size_t)lin->rows * lin->cols / 32);
+    if (r == "input_norm") return put(ly.in_norm, 4ull * c.hidden);
+    if (r == "post_norm") return put(ly.post_norm, 4ull * c.hidden);
+    if (r == "q_norm") return put(ly.q_norm, 4ull * c.head_dim);
+    if (r == "k_norm") return put(ly.k_norm, 4ull * c.head_dim);
+  }
+  return hwk::errf("hwk_qwen3_tensor: no tensor %s", name);
+}
+
+HWK_API char *hwk_qwen3_state(hwk_qwen3 *m, void **logits, void **hist, void **pos) {
+  HWK_CHECK(m, "hwk_qwen3_state: null model");
+  if (logits) *logits = m->logits;
+  if (hist) *hist = m->hist;
+  if (pos) *pos = m->pos;
+  return nullptr;
+}
+
+HWK_API char *hwk_qwen3_prefill(hwk_qwen3 *m, void *stream, const int32_t *tokens, uint32_t n, uint32_t start) {
+  HWK_CHECK(m && tokens, "hwk_qwen3_prefill: null argument");
+  HWK_CHECK(n >= 1, "hwk_qwen3_prefill: empty prompt");
+  HWK_CHECK((uint64_t)start + n < m->c.max_ctx, "hwk_qwen3_prefill: positions %u+%u leave no room in %u", start, n,
+            m->c.max_ctx);
+  HWK_CHECK(start <= m->host_pos, "hwk_qwen3_prefill: start %u past the cached positions (%u)", start, m->host_pos);
+  for (uint32_t i = 0; i < n; i++)
+    HWK_CHECK(tokens[i] >= 0 && (uint32_t)tokens[i] < m->c.vocab, "hwk_qwen3_prefill: token %d at %u out of vocab %u",
+              tokens[i], i, m->c.vocab);
+  hipStream_t st = (hipStream_t)stream;
+  HWK_TRY("hipStreamSynchronize", hipStreamSynchronize(st));
+  HWK_TRY("hipMemcpy", hipMemcpy(m->hist + start, tokens, 4ull * n, hipMemcpyHostToDevice));
+  for (uint32_t done = 0; done < n;) {
+    const uint32_t T = n - done < m->c.max_prompt ? n - done : m->c.max_prompt;
+    HWK_Q(prefill_piece(m, st, T, start + done, done + T == n));
+    done += T;
+  }
+  m->host_pos = start + n;
+  m->started = true;
+  return nullptr;
+}
+
+HWK_API char *hwk_qwen3_step(hwk_qwen3 *m, void *stream) {
+  HWK_CHECK(m, "hwk_qwen3_step: null model");
+  HWK_CHECK(m->started, "hwk_qwen3_step: no prompt yet");
+  HWK_CHECK(m->host_pos + 1 < m->c.max_ctx, "hwk_qwen3_step: position %u is the last of %u", m->host_pos, m->c.max_ctx);
+  HWK_Q(step(m, (hipStream_t)stream));
+  m->host_pos++;
+  return nullptr;
+}
+
+HWK_API char *hwk_qwen3_decode(hwk_qwen3 *m, void *stream, uint32_t steps) {
+  HWK_CHECK(m, "hwk_qwen3_decode: null model");
+  HWK_CHECK(m->started, "hwk_qwen3_decode: no prompt yet");
+  HWK_CHECK((uint64_t)m->host_pos + steps < m->c.max_ctx, "hwk_qwen3_decode: %u steps from %u pass %u", steps,
+            m->host_pos, m->c.max_ctx);
+  if (!m->exec) {
+    HWK_TRY("hipStreamBeginCapture", hipStreamBeginCapture(m->cap, hipStreamCaptureModeRelaxed));
+    char *err = step(m, m->cap);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(m->cap, &g);
+    if (err) {
+      if (g) (void)hipGraphDestroy(g);
+      return err;
+    }
+    if (e != hipSuccess) return hwk::hip_err("hipStreamEndCapture", e);
+    m->graph = g;
+    HWK_TRY("hipGraphInstantiate", hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+  }
+  for (uint32_t i = 0; i < steps; i++) HWK_TRY("hipGraphLaunch", hipGraphLaunch(m->exec, (hipStream_t)stream));
+  m->host_pos += steps;
+  return nullptr;
+}
+
+}  // extern "C"

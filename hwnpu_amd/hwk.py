@@ -51,6 +51,13 @@ class MoeParams(C.Structure):
 
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 
+
+class Qwen3Config(C.Structure):
+    """hwk_qwen3_config (include/hwk.h)."""
+    _fields_ = [("layers", U32), ("hidden", U32), ("heads", U32), ("kv_heads", U32), ("head_dim", U32),
+                ("inter", U32), ("vocab", U32), ("max_ctx", U32), ("max_prompt", U32), ("pad", U32),
+                ("theta_bits", U64), ("eps_bits", U64)]
+
 # name -> (restype, argtypes). ERR marks calls returning an error string (NULL on success).
 ERR = "err"
 SIGNATURES = {
@@ -90,6 +97,15 @@ SIGNATURES = {
     "hwk_attn_decode": (ERR, [P, P, P, P, P, P, P, P, SZ, C.POINTER(AttnParams)]),
     "hwk_kv_quantize_i8": (ERR, [P, P, P, P, U32, U32]),
     "hwk_attn_merge": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
+    "hwk_attn_prefill": (ERR, [P, P, P, P, P, U32, U32, C.POINTER(AttnParams)]),
+    "hwk_qwen3_new": (ERR, [C.POINTER(Qwen3Config), C.POINTER(P)]),
+    "hwk_qwen3_free": (None, [P]),
+    "hwk_qwen3_synth": (ERR, [P, P, U64, U32]),
+    "hwk_qwen3_tensor": (ERR, [P, C.c_char_p, C.POINTER(P), C.POINTER(SZ)]),
+    "hwk_qwen3_state": (ERR, [P, C.POINTER(P), C.POINTER(P), C.POINTER(P)]),
+    "hwk_qwen3_prefill": (ERR, [P, P, C.POINTER(I32), U32, U32]),
+    "hwk_qwen3_step": (ERR, [P, P]),
+    "hwk_qwen3_decode": (ERR, [P, P, U32]),
     "hwk_moe_route": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int, C.c_int, U32]),
     "hwk_moe_workspace_bytes": (SZ, [C.POINTER(MoeParams)]),
     "hwk_moe_experts": (ERR, [P, P, P, P, P, P, P, P, P, P, SZ, C.POINTER(MoeParams)]),

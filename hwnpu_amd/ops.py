@@ -185,6 +185,26 @@ def attn_decode(q, k, v, length, k_scale=None, v_scale=None, out_mode="f32", sca
     return out
 
 
+def attn_prefill(q, k, v, start, out_mode="f32", scale=None, out=None):
+    """Causal attention of tokens query rows q (tokens, heads, d) at positions start .. start+tokens-1
+    over fp16 caches k, v (kv_heads, capacity, d) that hold their keys: out (tokens, heads, d)."""
+    tokens, heads, d = q.shape
+    kvh, cap, d2 = k.shape
+    if d2 != d:
+        raise ValueError("head_dim of q and k differ")
+    _need(q, "q", torch.float16, (tokens, heads, d))
+    _need(k, "k", torch.float16, (kvh, cap, d))
+    _need(v, "v", torch.float16, (kvh, cap, d))
+    p = attn_params(heads, kvh, start + tokens, cap, False, scale, out_mode, 0, d)
+    dt = torch.float16 if out_mode == "f16" else torch.float32
+    if out is None:
+        out = torch.empty((tokens, heads, d), dtype=dt, device=q.device)
+    else:
+        _need(out, "out", dt, (tokens, heads, d))
+    hwk.load().hwk_attn_prefill(_stream(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), tokens, start, p)
+    return out
+
+
 def kv_quantize_i8(x: torch.Tensor):
     """int8 codes and fp16 scales of fp16 rows x (..., d) by the int8 KV rule."""
     d = x.shape[-1]

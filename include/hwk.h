@@ -174,6 +174,14 @@ HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const 
  * x fp16 (rows, head_dim); q int8 (rows, head_dim); scale fp16 (rows). */
 HWK_API char *hwk_kv_quantize_i8(void *stream, const void *x, void *q, void *scale, uint32_t rows,
                                  uint32_t head_dim);
+/* Causal attention of a prompt: tokens query rows at positions start .. start+tokens-1, q fp16
+ * (tokens, heads, head_dim), each seeing the keys at or before its own position in fp16 caches k,
+ * v (kv_heads, capacity, head_dim) that already hold them; p->len = start + tokens. out (tokens,
+ * heads, head_dim) per p->out_mode (replaces the prompt form of the reference's chunk program with
+ * its causal mask, internal/llm/paged/paged.go:70-203 at tokens > 1, as decode.Session.Step runs a
+ * prompt through it, internal/llm/decode/decode.go:1391-1483). */
+HWK_API char *hwk_attn_prefill(void *stream, const void *q, const void *k, const void *v, void *out,
+                               uint32_t tokens, uint32_t start, const hwk_attn_params *p);
 /* Merge chunk outputs as the reference's Merge does (paged.go:227-310): o (chunks, rows, dim)
  * fp32, each chunk normalized over its own keys, m and l (chunks, rows) fp32 (a chunk whose l is
  * not positive is skipped); out (rows, dim) per out_mode, zero for a row no chunk saw. */
@@ -214,6 +222,57 @@ HWK_API size_t hwk_moe_workspace_bytes(const hwk_moe_params *p);
 HWK_API char *hwk_moe_experts(void *stream, const void *x, const void *idx, const void *w, const void *gu_w,
                               const void *gu_e, const void *dn_w, const void *dn_e, void *out, void *workspace,
                               size_t workspace_bytes, const hwk_moe_params *p);
+
+/* ---- the Qwen3 decoder on the device (the shape of reference internal/llm/qwen3, build.go:107-311,
+ * driven the way internal/llm/iron/model.go:578 Step(token, pos) -> logits drives a device-resident
+ * model). Weights, KV cache, token history and position live on the device; a decode step is one
+ * captured HIP graph that reads its token and position on the device and writes the greedy next
+ * token there, so that steps replay without the host. ---- */
+typedef struct hwk_qwen3 hwk_qwen3;
+
+typedef struct hwk_qwen3_config {
+  uint32_t layers;       /* 28 */
+  uint32_t hidden;       /* 2048: a multiple of 32, at most 8192 */
+  uint32_t heads;        /* 16 query heads */
+  uint32_t kv_heads;     /* 8 (heads/kv_heads in {1, 2, 4}) */
+  uint32_t head_dim;     /* 128 only */
+  uint32_t inter;        /* 6144: the SwiGLU width, a multiple of 32, at most 8192 */
+  uint32_t vocab;        /* 151936: rows of the tied fp16 embedding / head */
+  uint32_t max_ctx;      /* positions the KV cache holds */
+  uint32_t max_prompt;   /* rows a prefill call takes at once (longer prompts go in pieces) */
+  uint32_t pad;
+  uint64_t theta_bits;   /* RoPE theta as float64 bits (1e6) */
+  uint64_t eps_bits;     /* RMSNorm epsilon as float64 bits (1e-6) */
+} hwk_qwen3_config;
+
+/* Allocates the model on the current device (weights uninitialized). */
+HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out);
+HWK_API void hwk_qwen3_free(hwk_qwen3 *m);
+/* Fills every weight with the synthetic checkpoint: each linear N(0, std) drawn under its Hugging
+ * Face name (model.layers.{i}.self_attn.q_proj.weight, ...) and encoded to MXFP4, the embedding
+ * fp16(N(0, std)) under model.embed_tokens.weight, every norm weight 1. std as float32 bits. */
+HWK_API char *hwk_qwen3_synth(hwk_qwen3 *m, void *stream, uint64_t seed, uint32_t std_bits);
+/* A weight's device memory by its name in this layout, for a loader:
+ *   layers.{i}.qkv.blocks/.scales      MXFP4 (q, k, v rows stacked: heads*hd + 2*kv_heads*hd, hidden)
+ *   layers.{i}.o.blocks/.scales        MXFP4 (hidden, heads*hd)
+ *   layers.{i}.gate_up.blocks/.scales  MXFP4 (2*inter, hidden), gate row j at 2j, up row j at 2j+1
+ *   layers.{i}.down.blocks/.scales     MXFP4 (hidden, inter)
+ *   layers.{i}.input_norm, .post_norm  fp32 (hidden); layers.{i}.q_norm, .k_norm fp32 (head_dim)
+ *   norm fp32 (hidden); embed fp16 (vocab, hidden)
+ * blocks are (rows, cols/32, 16) bytes, scales (rows, cols/32) e8m0. */
+HWK_API char *hwk_qwen3_tensor(hwk_qwen3 *m, const char *name, void **ptr, size_t *bytes);
+/* The device state: logits fp32 (vocab) of the last processed row; the token history int32
+ * (max_ctx + 1), hist[p] the token at position p; pos int32, the position the next step takes. */
+HWK_API char *hwk_qwen3_state(hwk_qwen3 *m, void **logits, void **hist, void **pos);
+/* Runs a prompt of n host token ids at positions start .. start+n-1 (KV written there), then the
+ * head on its last row: logits, and the greedy next token into hist[start+n]; pos = start+n.
+ * Synchronous on the host for the token copy, asynchronous for the compute. */
+HWK_API char *hwk_qwen3_prefill(hwk_qwen3 *m, void *stream, const int32_t *tokens, uint32_t n, uint32_t start);
+/* One decode step, eagerly: the token hist[pos] at position pos -> logits, hist[pos+1] = the
+ * greedy token (strict >, ties to the lowest id, reference internal/chat/sample.go:80-87), pos+1. */
+HWK_API char *hwk_qwen3_step(hwk_qwen3 *m, void *stream);
+/* steps decode steps as replays of the captured step graph (captured on the first call). */
+HWK_API char *hwk_qwen3_decode(hwk_qwen3 *m, void *stream, uint32_t steps);
 
 /* ---- synthetic inputs, reproducible from (seed, name) alone: splitmix64 counter streams keyed
  * by seed ^ fnv64a(name) (the role of reference internal/llm/synth.go:12-56). Each element i

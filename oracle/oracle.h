@@ -128,6 +128,25 @@ void or_silu_mul(float *out, const float *g, const float *u, size_t n);
 /* greedy pick: the first index of the largest value (strict >) */
 int32_t or_argmax(const float *x, size_t n);
 
+/* ---- the Qwen3 decoder (internal/llm/qwen3/qwen3_test.go:77-207 with the decode session's
+ *      chunked attention and fp16 storage points; see qwen3.c) ---- */
+typedef struct or_qwen3_cfg {
+  int layers, hidden, heads, kv_heads, head_dim, inter, vocab, max_ctx;
+  double theta, eps;
+} or_qwen3_cfg;
+typedef struct or_qwen3 or_qwen3;
+/* element i of the normal stream keyed by key (splitmix64 + Box-Muller in float64) */
+double or_normal_at(uint64_t key, uint64_t i);
+uint64_t or_fnv64a(const char *s);
+/* the synthetic checkpoint of seed with weight std sd */
+or_qwen3 *or_qwen3_new(const or_qwen3_cfg *cfg, uint64_t seed, float sd, int threads);
+void or_qwen3_free(or_qwen3 *m);
+/* sums of every linear's code bytes, of their scale bytes, and of the embedding's fp16 bits */
+void or_qwen3_checksums(const or_qwen3 *m, uint64_t out[3]);
+/* T tokens at positions start .. start+T-1 (KV cache written there; earlier positions must be
+ * cached): logits (vocab) of the last row, returns the greedy token */
+int32_t or_qwen3_run(or_qwen3 *m, const int32_t *tokens, int T, int start, float *logits);
+
 /* ---- threads ---- */
 int or_max_threads(void);
 

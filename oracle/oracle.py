@@ -65,6 +65,12 @@ def lib():
             "or_silu_mul": (None, [P, P, P, sz]),
             "or_argmax": (C.c_int32, [P, sz]),
             "or_max_threads": (C.c_int, []),
+            "or_normal_at": (C.c_double, [C.c_uint64, C.c_uint64]),
+            "or_fnv64a": (C.c_uint64, [C.c_char_p]),
+            "or_qwen3_new": (P, [P, C.c_uint64, C.c_float, C.c_int]),
+            "or_qwen3_free": (None, [P]),
+            "or_qwen3_checksums": (None, [P, P]),
+            "or_qwen3_run": (C.c_int32, [P, P, C.c_int, C.c_int, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -308,3 +314,44 @@ def silu_mul(g, u):
 def argmax(x) -> int:
     x = _c(x, np.float32)
     return int(lib().or_argmax(_p(x), x.size))
+
+
+# ---- the Qwen3 decoder ----
+class Qwen3Cfg(C.Structure):
+    _fields_ = [("layers", C.c_int), ("hidden", C.c_int), ("heads", C.c_int), ("kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("inter", C.c_int), ("vocab", C.c_int), ("max_ctx", C.c_int),
+                ("theta", C.c_double), ("eps", C.c_double)]
+
+
+class Qwen3:
+    """The oracle's synthetic Qwen3 (qwen3.c): run(tokens, start) -> (greedy token, logits)."""
+
+    def __init__(self, layers, hidden, heads, kv_heads, head_dim, inter, vocab, max_ctx, theta=1e6, eps=1e-6,
+                 seed=0, std=0.02, threads=0):
+        self.cfg = Qwen3Cfg(layers, hidden, heads, kv_heads, head_dim, inter, vocab, max_ctx, theta, eps)
+        self.vocab = vocab
+        self._h = lib().or_qwen3_new(C.byref(self.cfg), seed, std, threads)
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().or_qwen3_free(self._h)
+            self._h = None
+
+    def checksums(self):
+        out = np.zeros(3, np.uint64)
+        lib().or_qwen3_checksums(self._h, _p(out))
+        return [int(v) for v in out]
+
+    def run(self, tokens, start):
+        toks = _c(tokens, np.int32)
+        logits = np.empty(self.vocab, np.float32)
+        tok = lib().or_qwen3_run(self._h, _p(toks), toks.size, int(start), _p(logits))
+        return int(tok), logits
+
+
+def normal_at(key: int, i: int) -> float:
+    return lib().or_normal_at(key, i)
+
+
+def fnv64a(name: str) -> int:
+    return lib().or_fnv64a(name.encode())

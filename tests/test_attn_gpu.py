@@ -151,3 +151,37 @@ def test_attn_merge_vs_oracle(dev, orc):
     want = mg.result()
     got = ops.attn_merge(*(torch.from_numpy(a).cuda() for a in (o, m, l))).cpu().numpy()
     assert np.max(np.abs(got - want)) <= 1e-5 * max(1.0, float(np.max(np.abs(want))))
+
+
+def oracle_prefill(orc, q, k, v, start, scale):
+    """The reference's chunk program over the whole cache with the causal mask (0 / -1e4), as the
+    session runs a prompt (one chunk: every case here is under DefaultChunk = 8192 keys)."""
+    T, H, d = q.shape
+    kvh = k.shape[0]
+    L = start + T
+    mask = np.where(np.arange(L)[None, :] <= start + np.arange(T)[:, None], 0.0, -1e4).astype(np.float32)
+    qh = np.ascontiguousarray(q.transpose(1, 0, 2))  # (heads, tokens, d)
+    o, m, l = orc.paged_chunk(qh, k[:, :L], v[:, :L], mask, scale)
+    return o.transpose(1, 0, 2)
+
+
+@pytest.mark.parametrize("heads,kvh,T,start,cap", [
+    (16, 8, 1024, 0, 1280),  # the model's prompt
+    (32, 8, 200, 0, 256), (16, 8, 37, 100, 160), (8, 8, 70, 5, 80), (16, 16, 1, 0, 8), (16, 8, 33, 31, 64)])
+def test_attn_prefill_causal(dev, orc, heads, kvh, T, start, cap):
+    print(f"attn prefill heads={heads} kv={kvh} T={T} start={start} cap={cap}", flush=True)
+    name = f"c3p.{heads}.{T}.{start}"
+    q = synth.normal(T * heads * 128, name + ".q").view(T, heads, 128)
+    k = synth.normal(kvh * cap * 128, name + ".k").view(kvh, cap, 128)
+    v = synth.normal(kvh * cap * 128, name + ".v").view(kvh, cap, 128)
+    scale = 1 / math.sqrt(128)
+    want = oracle_prefill(orc, q.cpu().numpy().astype(np.float32), k.cpu().numpy().astype(np.float32),
+                          v.cpu().numpy().astype(np.float32), start, scale)
+    got = ops.attn_prefill(q, k, v, start, out_mode="f32").cpu().numpy()
+    for t in range(T):  # every row against its own scale
+        check_close(got[t], want[t])
+    g16 = ops.attn_prefill(q, k, v, start, out_mode="f16").cpu().numpy()
+    assert np.array_equal(g16.view(np.uint16), orc.f32_to_f16(got))
+    # the last row equals decode attention at that position
+    dec = ops.attn_decode(q[T - 1].contiguous(), k, v, start + T).cpu().numpy()
+    check_close(got[T - 1], dec)
