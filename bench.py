@@ -48,6 +48,10 @@ KV_POS_BYTES = 28 * 2 * 8 * 128 * 2
 GEMV_N, GEMV_K = 8192, 2048
 GEMV_BYTES = GEMV_N * GEMV_K // 2 + GEMV_N * GEMV_K // 32 + GEMV_K * 2 + GEMV_N * 2  # 8,933,376
 COPIES = 64
+# HBM bytes a K1 launch moves, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on the same launches
+# scaled by the counters' reading of a plain copy of known size (profiles/k1_mxfp4_gemv_8192x2048.md):
+# 8,759 KiB read + 32 KiB written
+GEMV_TRAFFIC = (8759 + 32) * 1024
 
 
 def _graph_time(launch_all, steps: int, warmup: int, eager: bool = False):
@@ -279,7 +283,7 @@ def main():
                             "frac": round(d["step_bytes"] / (d["ms_per_tok"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "first_tokens": d["first_tokens"],
         "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC,
                      "kernel": "k_mxfp4_gemv_stream (MXFP4 GEMV 8192x2048, 64 distinct copies, graph)",
                      "us_per_launch": round(g["us"], 3), "bytes_per_launch": GEMV_BYTES},
         "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(),

@@ -86,3 +86,30 @@ FAKE = 0x10000  # never dereferenced: every case below is refused before a launc
 def test_bad_arguments_rejected(call, match):
     with pytest.raises(hwk.HwkError, match=match):
         call(hwk.load())
+
+
+def test_attn_prefill_rejects_bad_params():
+    L = hwk.load()
+    p = hwk.AttnParams()
+    p.heads, p.kv_heads, p.head_dim, p.len, p.capacity, p.out_mode = 16, 8, 128, 10, 64, 0
+    with pytest.raises(hwk.HwkError, match="start \\+ tokens"):
+        L.hwk_attn_prefill(None, FAKE, FAKE, FAKE, FAKE, 8, 0, C.byref(p))  # len 10 != 0 + 8
+    p.len = 70
+    with pytest.raises(hwk.HwkError, match="past capacity"):
+        L.hwk_attn_prefill(None, FAKE, FAKE, FAKE, FAKE, 70, 0, C.byref(p))
+    p.len, p.kv_heads = 8, 3
+    with pytest.raises(hwk.HwkError, match="kv heads"):
+        L.hwk_attn_prefill(None, FAKE, FAKE, FAKE, FAKE, 8, 0, C.byref(p))
+
+
+@pytest.mark.parametrize("field,value,match", [
+    ("head_dim", 64, "head_dim"), ("kv_heads", 3, "kv heads"), ("hidden", 100, "hidden"),
+    ("inter", 0, "inter"), ("max_prompt", 5000, "max_prompt"), ("layers", 0, "layers")])
+def test_qwen3_new_rejects_bad_config(field, value, match):
+    c = hwk.Qwen3Config()
+    c.layers, c.hidden, c.heads, c.kv_heads, c.head_dim = 2, 2048, 16, 8, 128
+    c.inter, c.vocab, c.max_ctx, c.max_prompt = 6144, 1000, 4096, 64
+    setattr(c, field, value)
+    out = C.c_void_p()
+    with pytest.raises(hwk.HwkError, match=match):
+        hwk.load().hwk_qwen3_new(C.byref(c), C.byref(out))
