@@ -366,6 +366,188 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
   }
 }
 
+// The model's decode attention for the token at position p = *pos. NSPLIT workgroups of W waves a
+// kv head each take a contiguous share of the keys [0, p]. Prologue: q for the kv head's G query
+// heads comes from the fp32 projection qkv (heads + 2 * kvh rows of 128) through the per-head
+// RMSNorm and RoPE; the workgroup whose share holds p also writes the new k (normed, rotated) and v
+// into the caches there and reads them after a workgroup barrier. Every workgroup merges its waves
+// in LDS and leaves its partial (o unnormalized, m in natural-log units, l) in the workspace; the
+// last of a kv head's workgroups to arrive (a counter a kv head, a single thread's release and
+// acquire fences) merges them with the rule of the reference's Merge into out (fp16) and clears
+// the counter for the next call.
+constexpr uint32_t kHeadSplit = 8;  // most workgroups a kv head
+
+template <int G, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                                      const float *__restrict__ kn, const float *__restrict__ cos_t,
+                                                      const float *__restrict__ sin_t, double eps,
+                                                      f16 *__restrict__ kc, f16 *__restrict__ vc,
+                                                      f16 *__restrict__ out, float *__restrict__ ws_o,
+                                                      float *__restrict__ ws_m, float *__restrict__ ws_l,
+                                                      uint32_t *__restrict__ counters, const int32_t *__restrict__ pos,
+                                                      uint32_t heads, uint32_t kvh, uint32_t cap, uint32_t chunk,
+                                                      uint32_t nsplit, float scale_log2) {
+  __shared__ float sm[W][G], sl[W][G];
+  __shared__ float sacc[W][G][128];
+  __shared__ __attribute__((aligned(16))) f16 qs[G][128];
+  __shared__ float pw[G][kHeadSplit], pden[G];
+  __shared__ bool last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t h = blockIdx.x / nsplit, c = blockIdx.x % nsplit;
+  const uint32_t p = (uint32_t)*pos, len = p + 1;
+  const uint32_t begin = c * chunk;
+  const uint32_t end = begin + chunk < len ? begin + chunk : len;
+  const size_t head_base = (size_t)h * cap;
+  constexpr uint32_t STEP = 16 * W;
+  // this wave's first tile goes out before the prologue unless it holds p (written below)
+  Tile<false> ta, tb;
+  uint32_t key = begin + 16 * wave;
+  const bool early = key < end && !(key <= p && p < key + 16);
+  if (early) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, end, lane);
+  const uint32_t jobs = (p / chunk == c) ? G + 2 : G;
+  for (uint32_t j = wave; j < jobs; j += W) {
+    const uint32_t row = j < G ? h * G + j : j == G ? heads + h : heads + kvh + h;
+    const float x0 = qkv[(size_t)row * 128 + lane], x1 = qkv[(size_t)row * 128 + lane + 64];
+    if (j == G + 1) {
+      vc[(head_base + p) * 128 + lane] = (f16)x0;
+      vc[(head_base + p) * 128 + lane + 64] = (f16)x1;
+      continue;
+    }
+    float o0, o1;
+    head_norm_rope(x0, x1, j < G ? qn : kn, cos_t[(size_t)p * 64 + lane], sin_t[(size_t)p * 64 + lane], eps, lane,
+                   o0, o1);
+    if (j < G) {
+      qs[j][lane] = (f16)o0;
+      qs[j][lane + 64] = (f16)o1;
+    } else {
+      kc[(head_base + p) * 128 + lane] = (f16)o0;
+      kc[(head_base + p) * 128 + lane + 64] = (f16)o1;
+    }
+  }
+  __syncthreads();  // q in LDS; the new cache rows visible to the workgroup's loads
+  if (!early && key < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, end, lane);
+  half8 qa[4];
+  {
+    const int g = lane & 15, grp = lane >> 4;
+#pragma unroll
+    for (int s2 = 0; s2 < 4; s2++)
+      qa[s2] = g < G ? *(const half8 *)&qs[g][s2 * 32 + grp * 8] : half8_of(make_uint4(0, 0, 0, 0));
+  }
+  float acc[G][8], m[G], l[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    m[g] = -__builtin_inff();
+    l[g] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
+  }
+  while (key < end) {
+    if (key + STEP < end) load_tile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + STEP, end, lane);
+    attend_tile<G, false>(ta, qa, key, end, scale_log2, lane, m, l, acc);
+    key += STEP;
+    if (key >= end) break;
+    if (key + STEP < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + STEP, end, lane);
+    attend_tile<G, false>(tb, qa, key, end, scale_log2, lane, m, l, acc);
+    key += STEP;
+  }
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+      float a = acc[g][d];
+      a += __shfl_xor(a, 16, 64);
+      a += __shfl_xor(a, 32, 64);
+      acc[g][d] = a;
+    }
+  if (lane < 16) {
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+      for (int d = 0; d < 8; d++) sacc[wave][g][lane * 8 + d] = acc[g][d];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      sm[wave][g] = m[g];
+      sl[wave][g] = l[g];
+    }
+  }
+  __syncthreads();
+  const size_t base = ((size_t)h * nsplit + c) * G;
+  for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
+    const uint32_t g = i / 128, d = i % 128;
+    float top = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < W; w++) top = fmaxf(top, sm[w][g]);
+    float o = 0.0f, lsum = 0.0f;
+    if (top != -__builtin_inff()) {
+#pragma unroll
+      for (int w = 0; w < W; w++) {
+        const float wt = exp2f(sm[w][g] - top);
+        o += wt * sacc[w][g][d];
+        lsum += wt * sl[w][g];
+      }
+    }
+    if (nsplit == 1) {
+      out[(size_t)(h * G + g) * 128 + d] = (f16)(lsum > 0.0f ? o / lsum : 0.0f);
+    } else {
+      ws_o[(base + g) * 128 + d] = o;
+      if (d == 0) {
+        ws_m[base + g] = top * kLn2;
+        ws_l[base + g] = lsum;
+      }
+    }
+  }
+  if (nsplit == 1) return;
+  __syncthreads();  // the workgroup's partial is written (every wave's stores complete)
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const bool lst = __hip_atomic_fetch_add(&counters[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+    if (lst) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    last = lst;
+  }
+  __syncthreads();
+  if (!last) return;
+  // the kv head's partials: weights exp(m - top) for the parts with l > 0, then o over l
+  const size_t b0 = (size_t)h * nsplit * G;
+  if (threadIdx.x < G) {
+    const uint32_t g = threadIdx.x;
+    float mv[kHeadSplit], lv[kHeadSplit];
+    float top = -__builtin_inff();
+#pragma unroll
+    for (uint32_t cc = 0; cc < kHeadSplit; cc++) {
+      mv[cc] = cc < nsplit ? ws_m[b0 + cc * G + g] : 0.0f;
+      lv[cc] = cc < nsplit ? ws_l[b0 + cc * G + g] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t cc = 0; cc < kHeadSplit; cc++)
+      if (lv[cc] > 0.0f) top = fmaxf(top, mv[cc]);
+    float den = 0.0f;
+#pragma unroll
+    for (uint32_t cc = 0; cc < kHeadSplit; cc++) {
+      const float wt = (lv[cc] > 0.0f && top != -__builtin_inff()) ? expf(mv[cc] - top) : 0.0f;
+      pw[g][cc] = wt;
+      den += wt * lv[cc];
+    }
+    pden[g] = den;
+  }
+  float ov[kHeadSplit];
+  const uint32_t g0 = threadIdx.x / 128, d0 = threadIdx.x % 128;
+  if (threadIdx.x < (uint32_t)G * 128) {
+#pragma unroll
+    for (uint32_t cc = 0; cc < kHeadSplit; cc++) ov[cc] = cc < nsplit ? ws_o[(b0 + cc * G + g0) * 128 + d0] : 0.0f;
+  }
+  __syncthreads();
+  if (threadIdx.x < (uint32_t)G * 128) {
+    float num = 0.0f;
+#pragma unroll
+    for (uint32_t cc = 0; cc < kHeadSplit; cc++) num += pw[g0][cc] * ov[cc];
+    const float den = pden[g0];
+    out[(size_t)(h * G + g0) * 128 + d0] = (f16)(den > 0.0f ? num / den : 0.0f);
+  }
+  if (threadIdx.x == 0) counters[h] = 0;
+}
+
 // Merge of chunks (the reference's Merge rule, paged.go:252-310): top = the largest m among
 // chunks with l > 0; a chunk weighs exp(m - top), times l when its o is normalized; out = the
 // weighted sum of o over the weighted sum of l. Block (row, slice of 32 dims) of 256 threads: the
@@ -555,6 +737,42 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
   return hwk::launched("hwk_attn_decode (merge)");
 }
 
+
+uint32_t hwk::attn_head_split(const hwk_attn_params *p) {
+  // about 256 keys a workgroup at the cache's capacity, at most kHeadSplit a kv head
+  const uint32_t n = (p->capacity + 255) / 256;
+  return n < 1 ? 1 : n > kHeadSplit ? kHeadSplit : n;
+}
+
+size_t hwk::attn_head_workspace_bytes(const hwk_attn_params *p) {
+  return (size_t)p->heads * attn_head_split(p) * (128 + 2) * sizeof(float);
+}
+
+char *hwk::attn_head(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *cos_t,
+                     const float *sin_t, double eps, void *kc, void *vc, void *out, void *workspace,
+                     size_t workspace_bytes, uint32_t *counters, const hwk_attn_params *p, const int32_t *pos) {
+  HWK_CHECK(p && qkv && qn && kn && cos_t && sin_t && kc && vc && out && workspace && counters && pos,
+            "attn_head: null argument");
+  HWK_CHECK(p->head_dim == 128 && !p->kv_int8, "attn_head: fp16 caches of head_dim 128 only");
+  HWK_CHECK(p->kv_heads > 0 && p->heads % p->kv_heads == 0, "attn_head: %u heads over %u", p->heads, p->kv_heads);
+  const uint32_t G = p->heads / p->kv_heads;
+  HWK_CHECK(G == 1 || G == 2 || G == 4, "attn_head: %u query heads a kv head", G);
+  HWK_CHECK(workspace_bytes >= attn_head_workspace_bytes(p), "attn_head: workspace too small");
+  const uint32_t nsplit = attn_head_split(p), chunk = (p->capacity + nsplit - 1) / nsplit;
+  const uint64_t slots = (uint64_t)p->heads * nsplit;
+  float *ws_o = (float *)workspace, *ws_m = ws_o + slots * 128, *ws_l = ws_m + slots;
+  const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
+  constexpr int W = 8;
+#define HWK_AH(GG)                                                                                                \
+  hipLaunchKernelGGL((k_attn_head<GG, W>), dim3(p->kv_heads * nsplit), dim3(64 * W), 0, st, qkv, qn, kn, cos_t,  \
+                     sin_t, eps, (f16 *)kc, (f16 *)vc, (f16 *)out, ws_o, ws_m, ws_l, counters, pos, p->heads,     \
+                     p->kv_heads, p->capacity, chunk, nsplit, scale_log2)
+  if (G == 1) HWK_AH(1);
+  else if (G == 2) HWK_AH(2);
+  else HWK_AH(4);
+#undef HWK_AH
+  return hwk::launched("attn_head");
+}
 
 uint32_t hwk::attn_step_chunks(const hwk_attn_params *p) {
   // about 8192 keys a chunk, at least 8 chunks a kv head (at most 64), a multiple of 128 keys

@@ -34,20 +34,26 @@ char *attn_decode_dev(hipStream_t st, const void *q, const void *k, const void *
 // qkv (fp32, heads + 2 * kv_heads rows of 128); the workgroup whose chunk holds *pos writes the new
 // k (normed, rotated) and v into the caches before it reads them. The chunks' partials go to the
 // workspace (o (slots, 128) | m (slots) | l (slots), slot = (kv head * nchunk + chunk) * G + g) for
-// a consumer to merge: mxfp4_gemv_x with merge input (nchunk <= 8) or attn_merge_ws. p: the decode
+// a consumer to merge (attn_merge_ws). p: the decode
 // grid (its capacity sizes the chunks), fp16 caches. *nchunk_out: the chunks a kv head.
 uint32_t attn_step_chunks(const hwk_attn_params *p);
 size_t attn_step_workspace_bytes(const hwk_attn_params *p);
 char *attn_decode_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *cos_t,
                        const float *sin_t, double eps, void *kc, void *vc, void *workspace, size_t workspace_bytes,
                        const hwk_attn_params *p, const int32_t *pos, uint32_t *nchunk_out);
+// The model's decode attention for the token at *pos (k_attn_head): the per-head q/k RMSNorm, RoPE
+// and the KV append folded into its prologue (q, k, v from the stacked fp32 projection qkv), a few
+// workgroups a kv head over the keys [0, *pos], the last of them to arrive merging the partials
+// into out (heads, 128) fp16. counters (kv_heads) start at zero and are left at zero; workspace:
+// attn_head_workspace_bytes.
+uint32_t attn_head_split(const hwk_attn_params *p);
+size_t attn_head_workspace_bytes(const hwk_attn_params *p);
+char *attn_head(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *cos_t,
+                const float *sin_t, double eps, void *kc, void *vc, void *out, void *workspace, size_t workspace_bytes,
+                uint32_t *counters, const hwk_attn_params *p, const int32_t *pos);
+
 // The merge of attn_decode_step's partials into out (heads, 128) fp16.
 char *attn_merge_ws(hipStream_t st, const void *workspace, void *out, const hwk_attn_params *p, uint32_t nchunk);
-
-// mxfp4_gemv_x with x made by merging attn_decode_step's partials (x = the attention output, heads *
-// 128 values, fp16-rounded): G query heads a kv head, nchunk <= 8 chunks a kv head.
-char *mxfp4_gemv_merge(hipStream_t st, const void *w, const void *e, const void *workspace, uint32_t heads,
-                       uint32_t G, uint32_t nchunk, void *y, uint32_t n, int out_mode);
 
 }  // namespace hwk
 

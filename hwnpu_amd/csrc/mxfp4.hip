@@ -183,23 +183,18 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 }
 
 // Where the decode-step GEMV's x comes from.
-enum XMode { X_F16 = 0, X_NORM = 1, X_MERGE = 2 };
+enum XMode { X_F16 = 0, X_NORM = 1 };
 
 struct XIn {
   const uint4 *x16;  // X_F16: x itself
   const float *h;    // X_NORM: the fp32 residual and the norm weights
   const float *nw;
   double eps;
-  const float *ws;   // X_MERGE: attention partials, o (slots, 128) | m (slots) | l (slots)
-  uint32_t G, nchunk;
 };
-
-constexpr uint32_t kMergeChunks = 8;  // chunks a kv head the X_MERGE prologue takes
 
 // The decode-step GEMV (64 lanes a row, BPL blocks a lane, nb <= 64*BPL). The workgroup first puts
 // x in LDS, with one round of global loads (issued after the first row set's weight loads, which
-// overlap them): copied (X_F16); made from the fp32 residual h by RMSNorm (X_NORM); or merged from
-// the split attention's chunk partials with the rule of the reference's Merge (X_MERGE). Then its
+// overlap them): copied (X_F16) or made from the fp32 residual h by RMSNorm (X_NORM). Then its
 // waves stream row sets as k_mxfp4_gemv_stream does, x read from LDS. SWIGLU: a row set holds
 // (gate, up) row pairs and the output is fp16 silu(gate) * up at the pair's index.
 template <int BPL, int RPW, int XM, bool SWIGLU, int WPB>
@@ -243,39 +238,6 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
 #pragma unroll
     for (int j = 0; j < PER; j++)
       if (t + j * NT < k) xh[t + j * NT] = (f16)((hv[j] * r) * wv[j]);
-  } else if constexpr (XM == X_MERGE) {
-    const uint32_t slots = (k / 128) * in.nchunk;
-    const float *wm = in.ws + (size_t)slots * 128, *wl = wm + slots;
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-      const uint32_t i = t + j * NT;
-      if (i >= k) break;
-      const uint32_t hq = i >> 7, d = i & 127, hk = hq / in.G, g = hq % in.G;
-      float mc[kMergeChunks], lc[kMergeChunks], oc[kMergeChunks];
-#pragma unroll
-      for (uint32_t c = 0; c < kMergeChunks; c++) {
-        const size_t slot = ((size_t)hk * in.nchunk + c) * in.G + g;
-        const bool ok = c < in.nchunk;
-        mc[c] = ok ? wm[slot] : 0.0f;
-        lc[c] = ok ? wl[slot] : 0.0f;
-        oc[c] = ok ? in.ws[slot * 128 + d] : 0.0f;
-      }
-      float top = -__builtin_inff();
-#pragma unroll
-      for (uint32_t c = 0; c < kMergeChunks; c++)
-        if (lc[c] > 0.0f) top = fmaxf(top, mc[c]);
-      float num = 0.0f, den = 0.0f;
-      if (top != -__builtin_inff()) {
-#pragma unroll
-        for (uint32_t c = 0; c < kMergeChunks; c++)
-          if (lc[c] > 0.0f) {
-            const float wt = expf(mc[c] - top);
-            num += wt * oc[c];
-            den += wt * lc[c];
-          }
-      }
-      xh[i] = (f16)(den > 0.0f ? num / den : 0.0f);
-    }
   } else {
     for (uint32_t i = t; i < nb * 4; i += NT) xs[i] = in.x16[i];
   }
@@ -630,7 +592,7 @@ char *mxfp4_gemv_x(hipStream_t st, const void *w, const void *e, const void *x16
   HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "mxfp4_gemv_x: out_mode %d", out_mode);
   HWK_CHECK(aligned(w, 16) && (h || aligned(x16, 16)), "mxfp4_gemv_x: w and x must be 16-byte aligned");
   if (n == 0) return nullptr;
-  XIn in{(const uint4 *)x16, h, nw, eps, nullptr, 0, 0};
+  XIn in{(const uint4 *)x16, h, nw, eps};
   const uint32_t nb = k / 32;
   if (swiglu) {
     if (h) launch_x_bpl<X_NORM, true>(st, w, e, in, y, n, nb, out_mode);
@@ -640,19 +602,6 @@ char *mxfp4_gemv_x(hipStream_t st, const void *w, const void *e, const void *x16
     else launch_x_bpl<X_F16, false>(st, w, e, in, y, n, nb, out_mode);
   }
   return launched("mxfp4_gemv_x");
-}
-
-char *mxfp4_gemv_merge(hipStream_t st, const void *w, const void *e, const void *workspace, uint32_t heads,
-                       uint32_t G, uint32_t nchunk, void *y, uint32_t n, int out_mode) {
-  HWK_CHECK(w && e && workspace && y, "mxfp4_gemv_merge: null pointer");
-  HWK_CHECK(nchunk >= 1 && nchunk <= kMergeChunks, "mxfp4_gemv_merge: %u chunks (1..%u)", nchunk, kMergeChunks);
-  HWK_CHECK(G >= 1 && heads % G == 0 && heads * 128 <= 64 * 4 * 32, "mxfp4_gemv_merge: %u heads, G %u", heads, G);
-  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "mxfp4_gemv_merge: out_mode %d", out_mode);
-  HWK_CHECK(aligned(w, 16), "mxfp4_gemv_merge: w must be 16-byte aligned");
-  if (n == 0) return nullptr;
-  XIn in{nullptr, nullptr, nullptr, 0.0, (const float *)workspace, G, nchunk};
-  launch_x_bpl<X_MERGE, false>(st, w, e, in, y, n, heads * 128 / 32, out_mode);
-  return launched("mxfp4_gemv_merge");
 }
 
 char *synth_mxfp4_rows(hipStream_t st, void *w, void *e, uint32_t rows, uint32_t k, uint64_t key, float stdv,

@@ -12,10 +12,10 @@
 // Linears accumulate in fp32 (MXFP4 weights, the fp16 tied head); h += o_proj(attn) and
 // h += down(act) in fp32. The greedy token is the first index of the largest logit.
 //
-// A decode step is five kernels a layer: the norm-fused qkv GEMV; the split attention with the
-// q/k norm, RoPE and KV append folded in; o_proj, which merges the attention's chunks as it
-// makes its input; the norm- and SwiGLU-fused gate_up GEMV; down. Then four more: embed, final
-// norm, head, argmax. Its token
+// A decode step is five kernels a layer: the norm-fused qkv GEMV; the attention with the q/k norm,
+// RoPE and KV append in its prologue (a few workgroups a kv head, merged by the last to finish);
+// o_proj; the norm- and SwiGLU-fused gate_up GEMV; down. Then four more: embed, final norm, head,
+// argmax. Its token
 // and position are read on the device (hist[pos], pos), and the argmax writes the next token
 // and advances pos, so one captured graph replays for every step.
 #include <math.h>
@@ -191,7 +191,8 @@ struct hwk_qwen3 {
   f16 *embed;
   float *cos_t, *sin_t;
   int32_t *hist, *pos;
-  uint32_t *counter, *part_i;
+  uint32_t *counter, *part_i, *counters;
+  bool head_attn = true;  // short caches: attn_head; long ones: the split attention and its merge
   float *part_v, *logits;
   float *h, *qkv, *gu;
   f16 *x16, *q16, *att16, *a16;
@@ -250,6 +251,7 @@ void layout(hwk_qwen3 *m, uint8_t *base) {
   m->hist = cv.take<int32_t>(base, 4ull * (c.max_ctx + 1));
   m->pos = cv.take<int32_t>(base, 4);
   m->counter = cv.take<uint32_t>(base, 4);
+  m->counters = cv.take<uint32_t>(base, 4ull * c.kv_heads);
   m->part_i = cv.take<uint32_t>(base, 4 * kArgBlocks);
   m->part_v = cv.take<float>(base, 4 * kArgBlocks);
   m->logits = cv.take<float>(base, 4ull * c.vocab);
@@ -278,16 +280,16 @@ char *step(hwk_qwen3 *m, hipStream_t st) {
   for (auto &ly : m->L) {
     HWK_Q(hwk::mxfp4_gemv_x(st, ly.qkv.w, ly.qkv.e, nullptr, m->h, ly.in_norm, m->eps, m->qkv, m->qkv_n, c.hidden,
                             HWK_OUT_F32, false));
-    uint32_t nchunk = 0;
-    HWK_Q(hwk::attn_decode_step(st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t, m->sin_t, m->eps, ly.kc, ly.vc, m->ws,
-                                m->ws_bytes, &m->ap, m->pos, &nchunk));
-    if (nchunk <= 8) {  // the o_proj GEMV merges the chunks itself
-      HWK_Q(hwk::mxfp4_gemv_merge(st, ly.o.w, ly.o.e, m->ws, c.heads, c.heads / c.kv_heads, nchunk, m->h, c.hidden,
-                                  HWK_OUT_ADD_F32));
-    } else {
+    if (m->head_attn) {
+      HWK_Q(hwk::attn_head(st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t, m->sin_t, m->eps, ly.kc, ly.vc, m->att16, m->ws,
+                           m->ws_bytes, m->counters, &m->ap, m->pos));
+    } else {  // long caches: the split attention and its merge kernel
+      uint32_t nchunk = 0;
+      HWK_Q(hwk::attn_decode_step(st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t, m->sin_t, m->eps, ly.kc, ly.vc, m->ws,
+                                  m->ws_bytes, &m->ap, m->pos, &nchunk));
       HWK_Q(hwk::attn_merge_ws(st, m->ws, m->att16, &m->ap, nchunk));
-      HWK_Q(hwk_mxfp4_gemv(st, ly.o.w, ly.o.e, m->att16, m->h, c.hidden, m->att_n, HWK_OUT_ADD_F32));
     }
+    HWK_Q(hwk_mxfp4_gemv(st, ly.o.w, ly.o.e, m->att16, m->h, c.hidden, m->att_n, HWK_OUT_ADD_F32));
     HWK_Q(hwk::mxfp4_gemv_x(st, ly.gu.w, ly.gu.e, nullptr, m->h, ly.post_norm, m->eps, m->a16, 2 * c.inter, c.hidden,
                             HWK_OUT_F16, true));
     HWK_Q(hwk_mxfp4_gemv(st, ly.down.w, ly.down.e, m->a16, m->h, c.hidden, c.inter, HWK_OUT_ADD_F32));
@@ -368,7 +370,9 @@ HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
   memcpy(&ap.scale_bits, &sc, 4);
   ap.out_mode = HWK_OUT_F16;
   ap.split = 0;
-  m->ws_bytes = hwk::attn_step_workspace_bytes(&ap);
+  // attn_head while its workgroups take at most 2048 keys each; past that the split attention
+  m->head_attn = c.max_ctx <= 2048 * 8;
+  m->ws_bytes = m->head_attn ? hwk::attn_head_workspace_bytes(&ap) : hwk::attn_step_workspace_bytes(&ap);
   layout(m, nullptr);
   hipError_t e = hipMalloc((void **)&m->base, m->bytes);
   if (e != hipSuccess) {
@@ -391,7 +395,7 @@ HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
   if ((e = hipMemcpy(m->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
       (e = hipMemcpy(m->sin_t, stb.data(), stb.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
       (e = hipMemset(m->hist, 0, 4ull * (c.max_ctx + 1))) != hipSuccess || (e = hipMemset(m->pos, 0, 4)) != hipSuccess ||
-      (e = hipMemset(m->counter, 0, 4)) != hipSuccess ||
+      (e = hipMemset(m->counter, 0, 4)) != hipSuccess || (e = hipMemset(m->counters, 0, 4ull * c.kv_heads)) != hipSuccess ||
       (e = hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking)) != hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess)
     err = hwk::hip_err("hwk_qwen3_new", e);

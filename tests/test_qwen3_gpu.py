@@ -41,11 +41,12 @@ def check_close(got, want, what):
 SMALL = dict(layers=2, hidden=2048, heads=16, kv_heads=8, head_dim=128, inter=6144, vocab=4096)
 
 
-@pytest.mark.parametrize("heads,kv_heads,max_prompt", [(16, 8, 64), (8, 8, 128), (16, 4, 48)])
-def test_qwen3_small_matches_oracle(dev, orc, heads, kv_heads, max_prompt):
+# max_ctx past 16384 takes the split attention with a separate merge instead of attn_head
+@pytest.mark.parametrize("heads,kv_heads,max_prompt,max_ctx", [(16, 8, 64, 192), (8, 8, 128, 192), (16, 4, 48, 192),
+                                                               (16, 8, 64, 16500)])
+def test_qwen3_small_matches_oracle(dev, orc, heads, kv_heads, max_prompt, max_ctx):
     cfg = dict(SMALL, heads=heads, kv_heads=kv_heads)
-    print(f"qwen3 small {cfg} max_prompt={max_prompt}", flush=True)
-    max_ctx = 192
+    print(f"qwen3 small {cfg} max_prompt={max_prompt} max_ctx={max_ctx}", flush=True)
     m = Qwen3(**cfg, max_ctx=max_ctx, max_prompt=max_prompt)
     m.synth(seed=0, std=0.02)
     ref = orc.Qwen3(**cfg, max_ctx=max_ctx, seed=0, std=0.02)
