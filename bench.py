@@ -1,6 +1,6 @@
 """Benchmark of the MI355X decode path (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|gemv|copy] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|gemv|copy|gemm|attn|moe] [--no-cpu]
 
 Prints one JSON line.
 
@@ -19,6 +19,21 @@ the average launch time.
 
 gemv: only that GEMV measurement. copy: a plain device copy of the same 8,933,376 bytes timed the
 same way (the calibration run for the FETCH_SIZE / WRITE_SIZE counters).
+
+The other configurations (each a graph of back-to-back launches over distinct input copies, timed
+with HIP events; the decode line carries them under "configs" without CPU baselines, and the
+workloads below print them with theirs):
+- gemm: the int8 weight-only prefill GEMM, M=512 K=2048 N=6144 (fp16 X, int8 W, fp16 per-row
+  scale, fp16 Y): 12.88 GFLOP a launch, TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak; CPU:
+  the oracle's shiftScale dequant (cached, as milcpu caches constants) + blocked fp32 sgemm on 64
+  rows of X, scaled.
+- attn: GQA decode attention, 32 query / 8 KV heads, head_dim 128, L in {512, 2048, 8192, 32768},
+  fp16 KV (4,096 L + 16,384 B) and int8 KV with per-(head, token) scales (2,080 L + 16,384 B):
+  GB/s against 8 TB/s; CPU: the oracle's chunk attention + Merge (runner.attentionCPU's form).
+- moe: the MoE decode layer, hidden 2048, 32 experts, top-4 softmax routing, SwiGLU 768, MXFP4:
+  route + experts at T = 1 and 5; bytes = unique experts x 2,506,752 + activations; GB/s; CPU: the
+  oracle's Routing.Choose + Host.Run with int8-quantized activations (the reference's production
+  numerics).
 
 cpu_baseline (decode): the oracle's restatement of the reference's CPU decode step, timed on the
 host's cores on a bounded sample and scaled to one token: one layer's MXFP4 linears through
@@ -118,6 +133,207 @@ def copy_roofline(steps: int, warmup: int, eager: bool = False):
 
     us, launches, wall = _graph_time(launch_all, steps, warmup, eager)
     return {"us": us, "launches": launches, "wall_s": wall, "gbs": 2 * GEMV_BYTES / (us * 1e-6) / 1e9}
+
+
+def _graph_us(launch_all, copies: int, replays: int = 20):
+    """Microseconds a launch of `copies` launches captured in one graph, replayed `replays` times."""
+    import torch
+
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        launch_all()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        launch_all()
+    with torch.cuda.stream(st):
+        g.replay()
+        st.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(replays):
+            g.replay()
+        b.record(st)
+        b.synchronize()
+    return a.elapsed_time(b) * 1e3 / (replays * copies)
+
+
+GEMM_M, GEMM_N, GEMM_K = 512, 6144, 2048
+GEMM_FLOP = 2 * GEMM_M * GEMM_N * GEMM_K
+GEMM_BYTES = GEMM_N * GEMM_K + GEMM_N * 2 + GEMM_M * GEMM_K * 2 + GEMM_M * GEMM_N * 2
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def gemm_rate(copies: int = 8):
+    import torch
+
+    from hwnpu_amd import ops, synth
+
+    x = synth.normal(GEMM_M * GEMM_K, "bench.c2.x").view(GEMM_M, GEMM_K)
+    ws = [(synth.uniform_int(GEMM_N * GEMM_K, -127, 255, f"bench.c2.q.{i}", dtype=torch.int8).view(GEMM_N, GEMM_K),
+           synth.uniform_real(GEMM_N, 0.002, 0.02, f"bench.c2.s.{i}")) for i in range(copies)]
+    y = torch.empty((GEMM_M, GEMM_N), dtype=torch.float16, device="cuda")
+
+    def launch_all():
+        for q, sc in ws:
+            ops.i8_gemm(x, q, sc, "f16", y=y)
+
+    us = _graph_us(launch_all, copies)
+    tf = GEMM_FLOP / (us * 1e-6) / 1e12
+    return {"config": "int8 GEMM M=512 K=2048 N=6144, fp16 out", "us": round(us, 2), "tflops": round(tf, 1),
+            "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4), "gbs": round(GEMM_BYTES / (us * 1e-6) / 1e9, 1)}
+
+
+def gemm_cpu(rows: int = 64):
+    import numpy as np
+
+    from oracle import oracle
+
+    rng = np.random.default_rng(0)
+    q = rng.integers(-127, 128, (GEMM_N, GEMM_K), dtype=np.int8)
+    sc = (rng.uniform(0.002, 0.02, GEMM_N).astype(np.float16)).view(np.uint16)
+    wd = oracle.i8_dequant(q, sc)  # once: milcpu caches the dequantized constant
+    x = rng.standard_normal((rows, GEMM_K)).astype(np.float16).astype(np.float32)
+    oracle.sgemm(x[:8], wd, transb=True)
+    ts = []
+    for _ in range(3):
+        t = time.perf_counter()
+        oracle.sgemm(x, wd, transb=True)
+        ts.append(time.perf_counter() - t)
+    t = sorted(ts)[1] * GEMM_M / rows
+    return {"value": round(GEMM_FLOP / t / 1e12, 4), "unit": "TFLOP/s", "cores": oracle.max_threads(), "kind": "port",
+            "sample": f"sgemm of {rows} of the 512 rows against the dequantized weights, median of 3, scaled"}
+
+
+ATTN_LENS = (512, 2048, 8192, 32768)
+
+
+def attn_rate(L: int, int8: bool):
+    import math
+
+    import torch
+
+    from hwnpu_amd import ops, synth
+
+    kv_bytes = (2080 if int8 else 4096) * L + 16384
+    copies = max(2, min(160, -(-(320 << 20) // kv_bytes)))
+    q = synth.normal(32 * 128, f"bench.c3.q.{L}").view(32, 128)
+    caches = []
+    for i in range(copies):
+        k = synth.normal(8 * L * 128, f"bench.c3.k.{L}.{i}").view(8, L, 128)
+        v = synth.normal(8 * L * 128, f"bench.c3.v.{L}.{i}").view(8, L, 128)
+        if int8:
+            kq, ks = ops.kv_quantize_i8(k)
+            vq, vs = ops.kv_quantize_i8(v)
+            caches.append((kq, vq, ks, vs))
+        else:
+            caches.append((k, v, None, None))
+    torch.cuda.synchronize()
+    out = torch.empty((32, 128), dtype=torch.float16, device="cuda")
+    p = ops.attn_params(32, 8, L, L, int8, 1 / math.sqrt(128), "f16")
+    ws = ops.attn_workspace(p)
+
+    def launch_all():
+        for k, v, ks, vs in caches:
+            ops.attn_decode(q, k, v, L, ks, vs, out_mode="f16", out=out, workspace=ws)
+
+    us = _graph_us(launch_all, copies, 10)
+    gbs = kv_bytes / (us * 1e-6) / 1e9
+    return {"L": L, "kv": "int8" if int8 else "fp16", "us": round(us, 2), "gbs": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
+
+
+def attn_cpu(L: int):
+    import numpy as np
+
+    from oracle import oracle
+
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((32, 128)).astype(np.float32)
+    k = rng.standard_normal((8, L, 128)).astype(np.float32)
+    v = rng.standard_normal((8, L, 128)).astype(np.float32)
+    oracle.attn_decode(q, k[:, :64], v[:, :64], 128 ** -0.5)
+    ts = []
+    for _ in range(3):
+        t = time.perf_counter()
+        oracle.attn_decode(q, k, v, 128 ** -0.5)
+        ts.append(time.perf_counter() - t)
+    t = sorted(ts)[1]
+    return {"value": round((4096 * L + 16384) / t / 1e9, 3), "unit": "GB/s (fp16-KV bytes)",
+            "cores": oracle.max_threads(), "kind": "port", "sample": f"L={L}, median of 3"}
+
+
+MOE_E, MOE_H, MOE_I, MOE_K = 32, 2048, 768, 4
+MOE_EXPERT_BYTES = 2 * MOE_I * MOE_H // 2 + 2 * MOE_I * MOE_H // 32 + MOE_H * MOE_I // 2 + MOE_H * MOE_I // 32
+
+
+def moe_rate(T: int, copies: int = 4):
+    import torch
+
+    from hwnpu_amd import ops, synth
+
+    layers = []
+    uniq = []
+    for i in range(copies):
+        gw, ge = synth.mxfp4_uniform(MOE_E * 2 * MOE_I, MOE_H, f"bench.c4.gu.{i}")
+        dw, de = synth.mxfp4_uniform(MOE_E * MOE_H, MOE_I, f"bench.c4.dn.{i}")
+        gw = gw.view(MOE_E, 2 * MOE_I, MOE_H // 32, 16)
+        ge = ge.view(MOE_E, 2 * MOE_I, MOE_H // 32)
+        dw = dw.view(MOE_E, MOE_H, MOE_I // 32, 16)
+        de = de.view(MOE_E, MOE_H, MOE_I // 32)
+        logits = synth.normal(T * MOE_E, f"bench.c4.logits.{T}.{i}", dtype=torch.float32).view(T, MOE_E)
+        x = synth.normal(T * MOE_H, f"bench.c4.x.{T}.{i}").view(T, MOE_H)
+        idx, _ = ops.moe_route(logits, MOE_K)
+        uniq.append(len(set(idx.cpu().numpy().ravel().tolist())))
+        layers.append((gw, ge, dw, de, logits, x))
+    out = torch.empty((T, MOE_H), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, MOE_K), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, MOE_K), dtype=torch.float32, device="cuda")
+    ws = torch.empty(T * MOE_K * (MOE_I + MOE_H) * 4, dtype=torch.uint8, device="cuda")
+
+    def launch_all():
+        for gw, ge, dw, de, logits, x in layers:
+            i2, w2 = ops.moe_route(logits, MOE_K)
+            ops.moe_experts(x, i2, w2, gw, ge, dw, de, out=out, workspace=ws)
+
+    us = _graph_us(launch_all, copies, 20)
+    u = sum(uniq) / len(uniq)
+    nbytes = u * MOE_EXPERT_BYTES + T * MOE_H * 2 + T * MOE_H * 4 + T * MOE_E * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"T": T, "unique_experts": u, "us": round(us, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def moe_cpu(T: int):
+    import numpy as np
+
+    from oracle import oracle
+
+    rng = np.random.default_rng(0)
+    gw = rng.integers(0, 256, (MOE_E, 2 * MOE_I, MOE_H // 32, 16), dtype=np.uint8)
+    ge = rng.integers(123, 130, (MOE_E, 2 * MOE_I, MOE_H // 32), dtype=np.uint8)
+    dw = rng.integers(0, 256, (MOE_E, MOE_H, MOE_I // 32, 16), dtype=np.uint8)
+    de = rng.integers(123, 130, (MOE_E, MOE_H, MOE_I // 32), dtype=np.uint8)
+    logits = rng.standard_normal((T, MOE_E)).astype(np.float32)
+    x = rng.standard_normal((T, MOE_H)).astype(np.float16).astype(np.float32)
+
+    def run():
+        idx = np.empty((T, MOE_K), np.int32)
+        w = np.empty((T, MOE_K), np.float32)
+        for t in range(T):
+            idx[t], w[t] = oracle.choose(logits[t], MOE_K)
+        oracle.experts(x, idx, w, gw, ge, dw, de, quantized=True)
+        return len(set(idx.ravel().tolist()))
+
+    u = run()
+    ts = []
+    for _ in range(5):
+        t = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t)
+    t = sorted(ts)[2]
+    nbytes = u * MOE_EXPERT_BYTES + T * MOE_H * 6 + T * MOE_E * 4
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": oracle.max_threads(), "kind": "port",
+            "sample": f"T={T}: Choose + Host.Run (int8 activations, mxfp4.Run), median of 5, {u} unique experts"}
 
 
 def decode_rate(steps: int, warmup: int):
@@ -234,7 +450,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "copy"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "copy", "gemm", "attn", "moe"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager", action="store_true", help="gemv/copy: launch one by one, no graph (counter runs)")
     args = ap.parse_args()
@@ -250,6 +466,23 @@ def main():
         print(json.dumps({"workload": "copy", "bytes": GEMV_BYTES, "launches": r["launches"],
                           "us_per_launch": round(r["us"], 3), "gbs_read_plus_write": round(r["gbs"], 1)}))
         return
+    if args.workload == "gemm":
+        r = gemm_rate()
+        r["roofline"] = {"bound": "mfma", "achieved": r["tflops"], "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": r["frac_mfma"]}
+        r["cpu_baseline"] = None if args.no_cpu else gemm_cpu()
+        print(json.dumps(r))
+        return
+    if args.workload == "attn":
+        rows = [attn_rate(L, i8) for L in ATTN_LENS for i8 in (False, True)]
+        cpu = None if args.no_cpu else [attn_cpu(L) for L in ATTN_LENS]
+        print(json.dumps({"workload": "attn", "results": rows, "cpu_baseline": cpu}))
+        return
+    if args.workload == "moe":
+        rows = [moe_rate(T) for T in (1, 5)]
+        cpu = None if args.no_cpu else [moe_cpu(T) for T in (1, 5)]
+        print(json.dumps({"workload": "moe", "results": rows, "cpu_baseline": cpu}))
+        return
     if args.workload == "gemv":
         r = gemv_roofline(args.steps or 3200, args.warmup or 320, args.eager)
         print(json.dumps({"workload": "gemv", "launches": r["launches"], "us_per_launch": round(r["us"], 3),
@@ -259,6 +492,9 @@ def main():
     warmup = args.warmup if args.warmup is not None else 16
     d = decode_rate(steps, warmup)
     g = gemv_roofline(3200, 320)
+    configs = {"c2_int8_gemm": gemm_rate(4),
+               "c3_attention": [attn_rate(L, i8) for L in (2048, 32768) for i8 in (False, True)],
+               "c4_moe": [moe_rate(T, 2) for T in (1, 5)]}
     out = {
         "metric": "decode tok/s at batch 1 (1 GPU); MXFP4 GEMV achieved HBM GB/s vs peak",
         "value": round(d["tok_s"], 2),
@@ -287,6 +523,7 @@ def main():
                      "kernel": "k_mxfp4_gemv_stream (MXFP4 GEMV 8192x2048, 64 distinct copies, graph)",
                      "us_per_launch": round(g["us"], 3), "bytes_per_launch": GEMV_BYTES},
         "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(),
+        "configs": configs,
     }
     print(json.dumps(out))
 

@@ -375,7 +375,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
 // last of a kv head's workgroups to arrive (a counter a kv head, a single thread's release and
 // acquire fences) merges them with the rule of the reference's Merge into out (fp16) and clears
 // the counter for the next call.
-constexpr uint32_t kHeadSplit = 8;  // most workgroups a kv head
+constexpr uint32_t kHeadSplit = 64;  // most workgroups a kv head
 
 template <int G, int W>
 __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ qkv, const float *__restrict__ qn,
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
   __shared__ float sm[W][G], sl[W][G];
   __shared__ float sacc[W][G][128];
   __shared__ __attribute__((aligned(16))) f16 qs[G][128];
-  __shared__ float pw[G][kHeadSplit], pden[G];
+  __shared__ float pw[G][kHeadSplit], pl[G][kHeadSplit], pden[G];
   __shared__ bool last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t h = blockIdx.x / nsplit, c = blockIdx.x % nsplit;
@@ -508,40 +508,39 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
   }
   __syncthreads();
   if (!last) return;
-  // the kv head's partials: weights exp(m - top) for the parts with l > 0, then o over l
+  // the kv head's partials: m and l into LDS in one pass, the weights exp(m - top) of the parts
+  // with l > 0 there, then o over l with U loads in flight a thread
   const size_t b0 = (size_t)h * nsplit * G;
+  for (uint32_t i = threadIdx.x; i < nsplit * G; i += 64 * W) {
+    pw[i % G][i / G] = ws_m[b0 + i];
+    pl[i % G][i / G] = ws_l[b0 + i];
+  }
+  __syncthreads();
   if (threadIdx.x < G) {
     const uint32_t g = threadIdx.x;
-    float mv[kHeadSplit], lv[kHeadSplit];
     float top = -__builtin_inff();
-#pragma unroll
-    for (uint32_t cc = 0; cc < kHeadSplit; cc++) {
-      mv[cc] = cc < nsplit ? ws_m[b0 + cc * G + g] : 0.0f;
-      lv[cc] = cc < nsplit ? ws_l[b0 + cc * G + g] : 0.0f;
-    }
-#pragma unroll
-    for (uint32_t cc = 0; cc < kHeadSplit; cc++)
-      if (lv[cc] > 0.0f) top = fmaxf(top, mv[cc]);
+    for (uint32_t cc = 0; cc < nsplit; cc++)
+      if (pl[g][cc] > 0.0f) top = fmaxf(top, pw[g][cc]);
     float den = 0.0f;
-#pragma unroll
-    for (uint32_t cc = 0; cc < kHeadSplit; cc++) {
-      const float wt = (lv[cc] > 0.0f && top != -__builtin_inff()) ? expf(mv[cc] - top) : 0.0f;
+    for (uint32_t cc = 0; cc < nsplit; cc++) {
+      const float wt = (pl[g][cc] > 0.0f && top != -__builtin_inff()) ? expf(pw[g][cc] - top) : 0.0f;
       pw[g][cc] = wt;
-      den += wt * lv[cc];
+      den += wt * pl[g][cc];
     }
     pden[g] = den;
   }
-  float ov[kHeadSplit];
-  const uint32_t g0 = threadIdx.x / 128, d0 = threadIdx.x % 128;
-  if (threadIdx.x < (uint32_t)G * 128) {
-#pragma unroll
-    for (uint32_t cc = 0; cc < kHeadSplit; cc++) ov[cc] = cc < nsplit ? ws_o[(b0 + cc * G + g0) * 128 + d0] : 0.0f;
-  }
   __syncthreads();
-  if (threadIdx.x < (uint32_t)G * 128) {
+  constexpr uint32_t U = 8;  // o loads in flight a thread
+  for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
+    const uint32_t g0 = i / 128, d0 = i % 128;
     float num = 0.0f;
+    for (uint32_t cc = 0; cc < nsplit; cc += U) {
+      float ov[U];
 #pragma unroll
-    for (uint32_t cc = 0; cc < kHeadSplit; cc++) num += pw[g0][cc] * ov[cc];
+      for (uint32_t u = 0; u < U; u++) ov[u] = cc + u < nsplit ? ws_o[(b0 + (cc + u) * G + g0) * 128 + d0] : 0.0f;
+#pragma unroll
+      for (uint32_t u = 0; u < U; u++) num += (cc + u < nsplit ? pw[g0][cc + u] : 0.0f) * ov[u];
+    }
     const float den = pden[g0];
     out[(size_t)(h * G + g0) * 128 + d0] = (f16)(den > 0.0f ? num / den : 0.0f);
   }
@@ -738,9 +737,31 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
 }
 
 
+// Tuning knobs read once a process: HWK_ATTN_KEYS, the keys a workgroup takes at the cache's capacity
+// (default 256); HWK_ATTN_W, waves a workgroup (2, 4, 8 or 16; default 8).
+static int attn_env(const char *name, int dflt) {
+  const char *v = getenv(name);
+  return v ? atoi(v) : dflt;
+}
+
+static uint32_t attn_keys() {
+  static uint32_t k = [] {
+    const int v = attn_env("HWK_ATTN_KEYS", 256);
+    return (uint32_t)(v < 16 ? 16 : v > 65536 ? 65536 : v);
+  }();
+  return k;
+}
+
+static int attn_waves() {
+  static int w = [] {
+    const int v = attn_env("HWK_ATTN_W", 8);
+    return v == 2 || v == 4 || v == 16 ? v : 8;
+  }();
+  return w;
+}
+
 uint32_t hwk::attn_head_split(const hwk_attn_params *p) {
-  // about 256 keys a workgroup at the cache's capacity, at most kHeadSplit a kv head
-  const uint32_t n = (p->capacity + 255) / 256;
+  const uint32_t n = (p->capacity + attn_keys() - 1) / attn_keys();
   return n < 1 ? 1 : n > kHeadSplit ? kHeadSplit : n;
 }
 
@@ -762,14 +783,25 @@ char *hwk::attn_head(hipStream_t st, const float *qkv, const float *qn, const fl
   const uint64_t slots = (uint64_t)p->heads * nsplit;
   float *ws_o = (float *)workspace, *ws_m = ws_o + slots * 128, *ws_l = ws_m + slots;
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
-  constexpr int W = 8;
-#define HWK_AH(GG)                                                                                                \
+#define HWK_AH(GG, W)                                                                                             \
   hipLaunchKernelGGL((k_attn_head<GG, W>), dim3(p->kv_heads * nsplit), dim3(64 * W), 0, st, qkv, qn, kn, cos_t,  \
                      sin_t, eps, (f16 *)kc, (f16 *)vc, (f16 *)out, ws_o, ws_m, ws_l, counters, pos, p->heads,     \
                      p->kv_heads, p->capacity, chunk, nsplit, scale_log2)
-  if (G == 1) HWK_AH(1);
-  else if (G == 2) HWK_AH(2);
-  else HWK_AH(4);
+#define HWK_AHW(GG)                  \
+  switch (attn_waves()) {            \
+    case 2: HWK_AH(GG, 2); break;    \
+    case 4: HWK_AH(GG, 4); break;    \
+    case 16: HWK_AH(GG, 16); break;  \
+    default: HWK_AH(GG, 8); break;   \
+  }
+  if (G == 1) {
+    HWK_AHW(1)
+  } else if (G == 2) {
+    HWK_AHW(2)
+  } else {
+    HWK_AHW(4)
+  }
+#undef HWK_AHW
 #undef HWK_AH
   return hwk::launched("attn_head");
 }

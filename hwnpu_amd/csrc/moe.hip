@@ -4,14 +4,14 @@
 // (float64 exp rounded to float32, a sequential float32 sum, a stable descending order), so that
 // the chosen expert ids are the reference's bit for bit.
 //
-// K5b is two launches and needs nothing from the host between them: every workgroup derives the
+// K5b is three launches and needs nothing from the host between them: every workgroup derives the
 // sorted set of chosen experts from idx itself (a 64-bit ballot of the expert ids). The gate_up
 // kernel gives each (chosen expert, row-pair tile) to a workgroup, reads the expert's rows once
 // for all tokens that chose it, and writes silu(gate)*up in fp32 (it overflows fp16 at the
-// benchmark's scales). The down kernel gives each output row to a lane group that walks the
-// chosen experts in ascending id, reads each row once for all its tokens and adds w * y into a
-// per-token accumulator in that order: the reference's summation order (host.go:566-578,866-881),
-// with no atomics and no further launch.
+// benchmark's scales). The down kernel does the same for (chosen expert, row tile), so that every
+// expert's rows stream in parallel, and leaves each token's per-expert outputs in fp32; the combine
+// adds w * y for each token in ascending expert id, the reference's summation order
+// (host.go:566-578,866-881), with no atomics.
 #include "hwk_common.h"
 
 namespace {
@@ -192,71 +192,90 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x
   }
 }
 
-// ---- K5b stage 2: down + the ordered combine ----
-// LPR lanes a row (RS = 64/LPR rows a wave), BPL blocks a lane (nb = I/32 <= LPR*BPL).
+// ---- K5b stage 2: down, one chosen expert a workgroup column ----
+// Workgroup (row tile blockIdx.x, chosen expert number blockIdx.y in ascending id), one wave: LPR
+// lanes a row (RS = 64/LPR rows), BPL blocks a lane (nb = I/32 <= LPR*BPL). The expert's rows are
+// read once for all the tokens that chose it; y = down(act) goes unweighted to ydown (tokens, k, H)
+// at the token's slot of that expert.
 template <int LPR, int BPL>
-__global__ __launch_bounds__(256) void k_moe_down(const float *__restrict__ act, const int32_t *__restrict__ idx,
-                                                  const float *__restrict__ w, const uint4 *__restrict__ dw,
-                                                  const uint8_t *__restrict__ de, float *__restrict__ out, uint32_t T,
-                                                  uint32_t H, uint32_t I, uint32_t k, int mode) {
+__global__ __launch_bounds__(64) void k_moe_down(const float *__restrict__ act, const int32_t *__restrict__ idx,
+                                                 const uint4 *__restrict__ dw, const uint8_t *__restrict__ de,
+                                                 float *__restrict__ ydown, uint32_t T, uint32_t H, uint32_t I,
+                                                 uint32_t k) {
   constexpr int RS = 64 / LPR;
   const int lane = threadIdx.x & 63, l = lane % LPR;
-  const uint32_t row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RS + lane / LPR;
+  const uint32_t row = blockIdx.x * RS + lane / LPR;
   uint64_t mask = chosen_mask(idx, T * k);
+  const uint32_t u = blockIdx.y;
+  if (u >= (uint32_t)__builtin_popcountll(mask)) return;
+  for (uint32_t i = 0; i < u; i++) mask &= mask - 1;
+  const int e = __builtin_ctzll(mask);
   const uint32_t nb = I / 32;
-  float acc[8];
+  uint4 c[BPL];
+  uint32_t sc[BPL];
 #pragma unroll
-  for (int t = 0; t < 8; t++) acc[t] = (mode == HWK_OUT_ADD_F32 && t < (int)T && row < H) ? out[(size_t)t * H + row] : 0.0f;
-  while (mask) {
-    const int e = __builtin_ctzll(mask);
-    mask &= mask - 1;
-    uint4 c[BPL];
-    uint32_t s[BPL];
+  for (int j = 0; j < BPL; j++) {
+    const uint32_t b = j * LPR + l;
+    if (row < H && b < nb) {
+      const size_t blk = ((size_t)e * H + row) * nb + b;
+      c[j] = load_stream(&dw[blk]);
+      sc[j] = de[blk];
+    } else {
+      c[j] = make_uint4(0, 0, 0, 0);
+      sc[j] = 0;
+    }
+  }
+  for (uint32_t t = 0; t < T; t++) {
+    const int slot = slot_of(idx, t, k, e);
+    if (slot < 0) continue;
+    const float *ar = act + ((size_t)t * k + slot) * I;
+    float a = 0.0f;
 #pragma unroll
     for (int j = 0; j < BPL; j++) {
       const uint32_t b = j * LPR + l;
-      if (row < H && b < nb) {
-        const size_t blk = ((size_t)e * H + row) * nb + b;
-        c[j] = load_stream(&dw[blk]);
-        s[j] = de[blk];
-      } else {
-        c[j] = make_uint4(0, 0, 0, 0);
-        s[j] = 0;
-      }
+      float4 av[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) av[q] = b < nb ? ((const float4 *)(ar + b * 32))[q] : make_float4(0, 0, 0, 0);
+      a += dot_block_f32(c[j], av) * e8m0_scale(sc[j]);
     }
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      if (t >= (int)T) break;
-      const int slot = slot_of(idx, t, k, e);
-      if (slot < 0) continue;
-      const float *ar = act + ((size_t)t * k + slot) * I;
-      float a = 0.0f;
-#pragma unroll
-      for (int j = 0; j < BPL; j++) {
-        const uint32_t b = j * LPR + l;
-        float4 av[8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) av[q] = b < nb ? ((const float4 *)(ar + b * 32))[q] : make_float4(0, 0, 0, 0);
-        a += dot_block_f32(c[j], av) * e8m0_scale(s[j]);
-      }
-      const float y = group_sum<LPR>(a);
-      acc[t] += w[(size_t)t * k + slot] * y;
-    }
-  }
-  if (l == 0 && row < H) {
-#pragma unroll
-    for (int t = 0; t < 8; t++)
-      if (t < (int)T) out[(size_t)t * H + row] = acc[t];
+    const float y = group_sum<LPR>(a);
+    if (l == 0 && row < H) ydown[((size_t)t * k + slot) * H + row] = y;
   }
 }
 
+// ---- K5b stage 3: the ordered combine ----
+// out[t][r] (+)= sum over token t's experts in ascending expert id of w * y (the reference's order,
+// host.go:566-578,866-881), one thread an output.
+__global__ __launch_bounds__(256) void k_moe_combine(const float *__restrict__ ydown, const int32_t *__restrict__ idx,
+                                                     const float *__restrict__ w, float *__restrict__ out, uint32_t T,
+                                                     uint32_t H, uint32_t k, int mode) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= T * H) return;
+  const uint32_t t = i / H, r = i % H;
+  float acc = mode == HWK_OUT_ADD_F32 ? out[i] : 0.0f;
+  int prev = -1;
+  for (uint32_t n = 0; n < k; n++) {
+    int best = 1 << 30;
+    uint32_t bs = 0;
+    for (uint32_t j = 0; j < k; j++) {
+      const int e = idx[t * k + j];
+      if (e > prev && e < best) {
+        best = e;
+        bs = j;
+      }
+    }
+    acc += w[t * k + bs] * ydown[((size_t)t * k + bs) * H + r];
+    prev = best;
+  }
+  out[i] = acc;
+}
+
 template <int LPR, int BPL>
-void launch_down(hipStream_t st, const float *act, const int32_t *idx, const float *w, const void *dw, const void *de,
-                 float *out, const hwk_moe_params *p) {
-  constexpr uint32_t rows_per_block = 4 * (64 / LPR);
-  hipLaunchKernelGGL((k_moe_down<LPR, BPL>), dim3((p->hidden + rows_per_block - 1) / rows_per_block), dim3(256), 0,
-                     st, act, idx, w, (const uint4 *)dw, (const uint8_t *)de, out, p->tokens, p->hidden, p->inter,
-                     p->k, (int)p->out_mode);
+void launch_down(hipStream_t st, const float *act, const int32_t *idx, const void *dw, const void *de, float *ydown,
+                 const hwk_moe_params *p, uint32_t unique_max) {
+  constexpr uint32_t rows = 64 / LPR;
+  hipLaunchKernelGGL((k_moe_down<LPR, BPL>), dim3((p->hidden + rows - 1) / rows, unique_max), dim3(64), 0, st, act,
+                     idx, (const uint4 *)dw, (const uint8_t *)de, ydown, p->tokens, p->hidden, p->inter, p->k);
 }
 
 }  // namespace
@@ -276,9 +295,10 @@ HWK_API char *hwk_moe_route(void *stream, const void *logits, const void *bias, 
   return hwk::launched("hwk_moe_route");
 }
 
+// Layout: act (tokens, k, I) fp32 | ydown (tokens, k, H) fp32.
 HWK_API size_t hwk_moe_workspace_bytes(const hwk_moe_params *p) {
   if (!p) return 0;
-  return (size_t)p->tokens * p->k * p->inter * sizeof(float);
+  return (size_t)p->tokens * p->k * (p->inter + p->hidden) * sizeof(float);
 }
 
 HWK_API char *hwk_moe_experts(void *stream, const void *x, const void *idx, const void *w, const void *gu_w,
@@ -317,17 +337,20 @@ HWK_API char *hwk_moe_experts(void *stream, const void *x, const void *idx, cons
   if (char *err = hwk::launched("hwk_moe_experts (gate_up)")) return err;
   // down: lanes a row by I/32 blocks, the fewest idle slots (8 lanes x 3 blocks for I = 768)
   const uint32_t nbi = p->inter / 32;
-  const float *wt = (const float *)w;
-  float *o = (float *)out;
-  if (nbi <= 8) launch_down<8, 1>(st, act, id, wt, dn_w, dn_e, o, p);
-  else if (nbi <= 16) launch_down<16, 1>(st, act, id, wt, dn_w, dn_e, o, p);
-  else if (nbi <= 24) launch_down<8, 3>(st, act, id, wt, dn_w, dn_e, o, p);
-  else if (nbi <= 32) launch_down<32, 1>(st, act, id, wt, dn_w, dn_e, o, p);
-  else if (nbi <= 64) launch_down<64, 1>(st, act, id, wt, dn_w, dn_e, o, p);
-  else if (nbi <= 128) launch_down<64, 2>(st, act, id, wt, dn_w, dn_e, o, p);
-  else if (nbi <= 192) launch_down<64, 3>(st, act, id, wt, dn_w, dn_e, o, p);
-  else launch_down<64, 4>(st, act, id, wt, dn_w, dn_e, o, p);
-  return hwk::launched("hwk_moe_experts (down)");
+  float *yd = act + (size_t)p->tokens * p->k * p->inter;
+  if (nbi <= 8) launch_down<8, 1>(st, act, id, dn_w, dn_e, yd, p, unique_max);
+  else if (nbi <= 16) launch_down<16, 1>(st, act, id, dn_w, dn_e, yd, p, unique_max);
+  else if (nbi <= 24) launch_down<8, 3>(st, act, id, dn_w, dn_e, yd, p, unique_max);
+  else if (nbi <= 32) launch_down<32, 1>(st, act, id, dn_w, dn_e, yd, p, unique_max);
+  else if (nbi <= 64) launch_down<64, 1>(st, act, id, dn_w, dn_e, yd, p, unique_max);
+  else if (nbi <= 128) launch_down<64, 2>(st, act, id, dn_w, dn_e, yd, p, unique_max);
+  else if (nbi <= 192) launch_down<64, 3>(st, act, id, dn_w, dn_e, yd, p, unique_max);
+  else launch_down<64, 4>(st, act, id, dn_w, dn_e, yd, p, unique_max);
+  if (char *err = hwk::launched("hwk_moe_experts (down)")) return err;
+  const uint32_t n = p->tokens * p->hidden;
+  hipLaunchKernelGGL(k_moe_combine, dim3((n + 255) / 256), dim3(256), 0, st, yd, id, (const float *)w, (float *)out,
+                     p->tokens, p->hidden, p->k, (int)p->out_mode);
+  return hwk::launched("hwk_moe_experts (combine)");
 }
 
 }  // extern "C"

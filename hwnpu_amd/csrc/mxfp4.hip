@@ -560,15 +560,34 @@ namespace hwk {
 
 namespace {
 
-// 8 waves a workgroup: x is made once for 8 waves' rows, and the model's shapes still give every
-// CU whole workgroups (qkv: 2048 row sets, 256 workgroups; gate_up: 6144, 768).
-template <int BPL, int XM, bool SWIGLU>
-void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb, int mode) {
-  constexpr int WPB = 8, RPW = 2;
+// Tuning knob read once a process: HWK_GEMVX_WPB, waves a workgroup of the decode-step GEMV (4, 8 or
+// 16; default 8: x is made once for 8 waves' rows, and the model's shapes still give every CU whole
+// workgroups: qkv 2048 row sets, 256 workgroups; gate_up 6144, 768).
+int gemvx_wpb() {
+  static int v = [] {
+    const int w = env_int("HWK_GEMVX_WPB", 8);
+    return w == 4 || w == 16 ? w : 8;
+  }();
+  return v;
+}
+
+template <int BPL, int XM, bool SWIGLU, int WPB>
+void launch_x_w(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb,
+                int mode) {
+  constexpr int RPW = 2;
   const uint32_t sets = (n + RPW - 1) / RPW;
   const uint32_t waves = sets < stream_waves() ? sets : stream_waves();
   hipLaunchKernelGGL((k_mxfp4_gemv_x<BPL, RPW, XM, SWIGLU, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0,
                      st, (const uint4 *)w, (const uint8_t *)e, in, y, n, nb, mode);
+}
+
+template <int BPL, int XM, bool SWIGLU>
+void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb, int mode) {
+  switch (gemvx_wpb()) {
+    case 4: launch_x_w<BPL, XM, SWIGLU, 4>(st, w, e, in, y, n, nb, mode); break;
+    case 16: launch_x_w<BPL, XM, SWIGLU, 16>(st, w, e, in, y, n, nb, mode); break;
+    default: launch_x_w<BPL, XM, SWIGLU, 8>(st, w, e, in, y, n, nb, mode); break;
+  }
 }
 
 template <int XM, bool SWIGLU>

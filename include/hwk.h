@@ -211,7 +211,8 @@ typedef struct hwk_moe_params {
   uint32_t out_mode; /* HWK_OUT_F32 (out = the experts' sum) or HWK_OUT_ADD_F32 (out += it) */
 } hwk_moe_params;
 
-/* Device workspace of hwk_moe_experts: the SwiGLU activations, fp32 (tokens*k, I). */
+/* Device workspace of hwk_moe_experts: the SwiGLU activations, fp32 (tokens*k, I), then the
+ * experts' unweighted down outputs, fp32 (tokens*k, H). */
 HWK_API size_t hwk_moe_workspace_bytes(const hwk_moe_params *p);
 /* K5b: the chosen experts of each token (reference experts.Host.Run, host.go:723-882, without
  * biases, SiLU unit): gate_up MXFP4 (E, 2I, H/32, 16) codes + (E, 2I, H/32) scales with the gate
