@@ -25,7 +25,7 @@ def check_close(got, want, tol=TOL):
 
 
 @pytest.mark.parametrize("m,n,k", [(512, 6144, 2048), (5, 6144, 2048), (1, 128, 32), (130, 200, 96), (7, 1000, 4096),
-                                   (256, 256, 6144)])
+                                   (256, 256, 6144), (300, 130, 2880)])
 def test_i8_gemm_parity(dev, orc, m, n, k):
     print(f"i8_gemm m={m} n={n} k={k}", flush=True)
     name = f"k3i8.{m}.{n}.{k}"
