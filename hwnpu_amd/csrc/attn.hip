@@ -367,15 +367,30 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
 }
 
 // The model's decode attention for the token at position p = *pos. NSPLIT workgroups of W waves a
-// kv head each take a contiguous share of the keys [0, p]. Prologue: q for the kv head's G query
-// heads comes from the fp32 projection qkv (heads + 2 * kvh rows of 128) through the per-head
-// RMSNorm and RoPE; the workgroup whose share holds p also writes the new k (normed, rotated) and v
-// into the caches there and reads them after a workgroup barrier. Every workgroup merges its waves
-// in LDS and leaves its partial (o unnormalized, m in natural-log units, l) in the workspace; the
-// last of a kv head's workgroups to arrive (a counter a kv head, a single thread's release and
-// acquire fences) merges them with the rule of the reference's Merge into out (fp16) and clears
+// kv head each take a contiguous share of the capacity; those whose share starts past p leave at
+// once. Prologue: q for the kv head's G query heads comes from the fp32 projection qkv (heads + 2 *
+// kvh rows of 128) through the per-head RMSNorm and RoPE; the workgroup whose share holds p (the
+// owner) also makes the new k (normed, rotated) and v, writes them to the caches at p for later
+// steps and keeps them in LDS: the tile holding p never reads row p from memory but takes it from
+// LDS, so the owner's keys wait on no store. Every workgroup merges its waves in LDS and leaves its
+// partial (o unnormalized, m in natural-log units, l) in the workspace; the last of the kv head's
+// live workgroups to arrive (a counter a kv head, a single thread's release and acquire fences)
+// merges them with the rule of the reference's Merge into out (fp16), one wave reduction a query
+// head over the partials (a lane a partial) with every partial's o already in flight, and clears
 // the counter for the next call.
-constexpr uint32_t kHeadSplit = 64;  // most workgroups a kv head
+constexpr uint32_t kHeadSplit = 64;  // most workgroups a kv head (a lane each in the merge)
+
+// Row p = key0 + j of a tile from LDS (k as the MFMA B operand layout, v as the P.V layout).
+__device__ __forceinline__ void patch_row(Tile<false> &t, uint32_t j, const f16 *kn16, const f16 *vn16, int lane) {
+  const int grp = lane >> 4;
+  if ((uint32_t)(lane & 15) == j) {
+#pragma unroll
+    for (int s2 = 0; s2 < 4; s2++) t.k[s2] = *(const half8 *)&kn16[s2 * 32 + grp * 8];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+    if ((uint32_t)(4 * r + grp) == j) t.v[r] = *(const half8 *)&vn16[(lane & 15) * 8];
+}
 
 template <int G, int W>
 __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ qkv, const float *__restrict__ qn,
@@ -390,25 +405,28 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
   __shared__ float sm[W][G], sl[W][G];
   __shared__ float sacc[W][G][128];
   __shared__ __attribute__((aligned(16))) f16 qs[G][128];
-  __shared__ float pw[G][kHeadSplit], pl[G][kHeadSplit], pden[G];
+  __shared__ __attribute__((aligned(16))) f16 knew[128], vnew[128];
   __shared__ bool last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t h = blockIdx.x / nsplit, c = blockIdx.x % nsplit;
   const uint32_t p = (uint32_t)*pos, len = p + 1;
   const uint32_t begin = c * chunk;
-  const uint32_t end = begin + chunk < len ? begin + chunk : len;
+  if (begin >= len) return;  // no keys in use here: no partial, no arrival
+  const bool owner = p - begin < chunk;  // the share holds p (begin <= p)
+  const uint32_t end = owner ? len : begin + chunk;
+  const uint32_t lim = owner ? p : end;  // rows loaded from memory: row p comes from LDS
   const size_t head_base = (size_t)h * cap;
   constexpr uint32_t STEP = 16 * W;
-  // this wave's first tile goes out before the prologue unless it holds p (written below)
   Tile<false> ta, tb;
   uint32_t key = begin + 16 * wave;
-  const bool early = key < end && !(key <= p && p < key + 16);
-  if (early) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, end, lane);
-  const uint32_t jobs = (p / chunk == c) ? G + 2 : G;
+  if (key < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, lim, lane);
+  const uint32_t jobs = owner ? G + 2 : G;
   for (uint32_t j = wave; j < jobs; j += W) {
     const uint32_t row = j < G ? h * G + j : j == G ? heads + h : heads + kvh + h;
     const float x0 = qkv[(size_t)row * 128 + lane], x1 = qkv[(size_t)row * 128 + lane + 64];
     if (j == G + 1) {
+      vnew[lane] = (f16)x0;
+      vnew[lane + 64] = (f16)x1;
       vc[(head_base + p) * 128 + lane] = (f16)x0;
       vc[(head_base + p) * 128 + lane + 64] = (f16)x1;
       continue;
@@ -420,12 +438,13 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
       qs[j][lane] = (f16)o0;
       qs[j][lane + 64] = (f16)o1;
     } else {
+      knew[lane] = (f16)o0;
+      knew[lane + 64] = (f16)o1;
       kc[(head_base + p) * 128 + lane] = (f16)o0;
       kc[(head_base + p) * 128 + lane + 64] = (f16)o1;
     }
   }
-  __syncthreads();  // q in LDS; the new cache rows visible to the workgroup's loads
-  if (!early && key < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, end, lane);
+  __syncthreads();  // q, and the owner's new k/v, in LDS
   half8 qa[4];
   {
     const int g = lane & 15, grp = lane >> 4;
@@ -442,11 +461,13 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
     for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
   }
   while (key < end) {
-    if (key + STEP < end) load_tile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + STEP, end, lane);
+    if (key + STEP < end) load_tile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + STEP, lim, lane);
+    if (owner && p - key < 16) patch_row(ta, p - key, knew, vnew, lane);
     attend_tile<G, false>(ta, qa, key, end, scale_log2, lane, m, l, acc);
     key += STEP;
     if (key >= end) break;
-    if (key + STEP < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + STEP, end, lane);
+    if (key + STEP < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + STEP, lim, lane);
+    if (owner && p - key < 16) patch_row(tb, p - key, knew, vnew, lane);
     attend_tile<G, false>(tb, qa, key, end, scale_log2, lane, m, l, acc);
     key += STEP;
   }
@@ -499,49 +520,40 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
     }
   }
   if (nsplit == 1) return;
+  const uint32_t live = p / chunk + 1;  // workgroups of this kv head that hold keys
   __syncthreads();  // the workgroup's partial is written (every wave's stores complete)
   if (threadIdx.x == 0) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const bool lst = __hip_atomic_fetch_add(&counters[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+    const bool lst = __hip_atomic_fetch_add(&counters[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == live - 1;
     if (lst) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     last = lst;
   }
   __syncthreads();
   if (!last) return;
-  // the kv head's partials: m and l into LDS in one pass, the weights exp(m - top) of the parts
-  // with l > 0 there, then o over l with U loads in flight a thread
+  // A wave's 64 outputs share one query head g0: lane cc holds partial cc's m and l, and the wave's
+  // outputs load every partial's o (U at a time) while the weights exp(m - top) are reduced.
   const size_t b0 = (size_t)h * nsplit * G;
-  for (uint32_t i = threadIdx.x; i < nsplit * G; i += 64 * W) {
-    pw[i % G][i / G] = ws_m[b0 + i];
-    pl[i % G][i / G] = ws_l[b0 + i];
-  }
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const uint32_t g = threadIdx.x;
-    float top = -__builtin_inff();
-    for (uint32_t cc = 0; cc < nsplit; cc++)
-      if (pl[g][cc] > 0.0f) top = fmaxf(top, pw[g][cc]);
-    float den = 0.0f;
-    for (uint32_t cc = 0; cc < nsplit; cc++) {
-      const float wt = (pl[g][cc] > 0.0f && top != -__builtin_inff()) ? expf(pw[g][cc] - top) : 0.0f;
-      pw[g][cc] = wt;
-      den += wt * pl[g][cc];
-    }
-    pden[g] = den;
-  }
-  __syncthreads();
-  constexpr uint32_t U = 8;  // o loads in flight a thread
+  constexpr uint32_t U = 16;
   for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
     const uint32_t g0 = i / 128, d0 = i % 128;
+    float ov[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) ov[u] = u < live ? ws_o[(b0 + u * G + g0) * 128 + d0] : 0.0f;
+    const bool mine = (uint32_t)lane < live;
+    const float mc = mine ? ws_m[b0 + lane * G + g0] : -__builtin_inff();
+    const float lc = mine ? ws_l[b0 + lane * G + g0] : 0.0f;
+    const float top = wave_max(lc > 0.0f ? mc : -__builtin_inff());
+    const float wc = (lc > 0.0f && top != -__builtin_inff()) ? expf(mc - top) : 0.0f;
+    const float den = group_sum<64>(wc * lc);
     float num = 0.0f;
-    for (uint32_t cc = 0; cc < nsplit; cc += U) {
-      float ov[U];
 #pragma unroll
-      for (uint32_t u = 0; u < U; u++) ov[u] = cc + u < nsplit ? ws_o[(b0 + (cc + u) * G + g0) * 128 + d0] : 0.0f;
+    for (uint32_t u = 0; u < U; u++) num += __shfl(wc, u, 64) * ov[u];
+    for (uint32_t cc = U; cc < live; cc += U) {
 #pragma unroll
-      for (uint32_t u = 0; u < U; u++) num += (cc + u < nsplit ? pw[g0][cc + u] : 0.0f) * ov[u];
+      for (uint32_t u = 0; u < U; u++) ov[u] = cc + u < live ? ws_o[(b0 + (cc + u) * G + g0) * 128 + d0] : 0.0f;
+#pragma unroll
+      for (uint32_t u = 0; u < U; u++) num += __shfl(wc, (cc + u) & 63, 64) * ov[u];
     }
-    const float den = pden[g0];
     out[(size_t)(h * G + g0) * 128 + d0] = (f16)(den > 0.0f ? num / den : 0.0f);
   }
   if (threadIdx.x == 0) counters[h] = 0;

@@ -152,7 +152,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const f16 *__restrict__ q,
     if (mode == HWK_OUT_F16) {
       half4 o;
 #pragma unroll
-      for (int r = 0; r < 4; r++) o[r] = (f16)(acc[d][r] * inv);
+      for (int r = 0; r < 4; r++) o[r] = (f16)f32_value(acc[d][r] * inv);
       *(half4 *)((f16 *)out + o0 + dim) = o;
     } else {
 #pragma unroll

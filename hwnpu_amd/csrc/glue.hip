@@ -1,0 +1,323 @@
+// The decoder's small ops as C-ABI entry points (K6): RMSNorm, the per-head norm + RoPE, KV append,
+// SiLU(gate)*up, the residual add, the embedding gather and the greedy argmax. The fused decode
+// step runs the same arithmetic inside its GEMV prologues/epilogues and the attention prologue;
+// these are the standalone forms a caller composes (prefill pieces, other models, tests).
+//
+// Numerics, identical to the fused forms:
+//   RMSNorm   r = float(1 / sqrt(sum(x^2) / n + eps)), the sum of squares in float64; y = (x * r) * w
+//             (reference internal/llm/blocks/blocks.go:351-395)
+//   RoPE      rotate_half over cat(freqs, freqs) tables: y[j] = x[j] c[j] - x[j+h] s[j] for j < h,
+//             y[j+h] = x[j+h] c[j] + x[j] s[j] (blocks.go:412-445), no fused multiply-add
+//   SiLU*up   g / (1 + float(exp(-g))) * u with exp in float64 (blocks.go:395-401; the reference's
+//             expert act, internal/llm/experts/host.go:45-57)
+//   argmax    strict > from index 0 (internal/chat/sample.go:80-87): the lowest index of the
+//             largest value; NaNs never win except at index 0, where the reference keeps it.
+#include <math.h>
+
+#include "hwk_common.h"
+
+namespace {
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// One workgroup a row.
+template <bool F16OUT>
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, double eps,
+                                                 void *__restrict__ out, uint32_t n) {
+#pragma clang fp contract(off)
+  __shared__ double red[4];
+  const int t = threadIdx.x, lane = t & 63;
+  const float *xr = x + (size_t)blockIdx.x * n;
+  double ss = 0.0;
+  for (uint32_t i = t; i < n; i += 256) {
+    const double v = (double)xr[i];
+    ss += v * v;
+  }
+  ss = wave_sum_d(ss);
+  if (lane == 0) red[t >> 6] = ss;
+  __syncthreads();
+  ss = ((red[0] + red[1]) + red[2]) + red[3];
+  const float r = (float)(1.0 / sqrt(ss / (double)n + eps));
+  for (uint32_t i = t; i < n; i += 256) {
+    const float y = f32_value((xr[i] * r) * w[i]);
+    if (F16OUT)
+      ((f16 *)out)[(size_t)blockIdx.x * n + i] = (f16)y;
+    else
+      ((float *)out)[(size_t)blockIdx.x * n + i] = y;
+  }
+}
+
+// One wave a (token, head) of 128 dims: lane l holds dims l and l + 64, the pair rotate_half mixes.
+// The head's RMSNorm (when nw is given) then RoPE at position pos0 + token.
+template <bool F16OUT>
+__global__ __launch_bounds__(256) void k_norm_rope(const float *__restrict__ x, const float *__restrict__ nw,
+                                                   const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                                                   double eps, void *__restrict__ out, uint32_t heads, uint32_t rows,
+                                                   uint32_t pos0) {
+#pragma clang fp contract(off)
+  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves leave together
+  const uint32_t l = threadIdx.x & 63, t = row / heads;
+  const float *xr = x + (size_t)row * 128;
+  float y0 = xr[l], y1 = xr[l + 64];
+  if (nw) {
+    double ss = (double)y0 * (double)y0 + (double)y1 * (double)y1;
+    ss = wave_sum_d(ss);
+    const float r = (float)(1.0 / sqrt(ss / 128.0 + eps));
+    y0 = (y0 * r) * nw[l];
+    y1 = (y1 * r) * nw[l + 64];
+  }
+  const size_t p = (size_t)pos0 + t;
+  const float c = cos_t[p * 64 + l], s = sin_t[p * 64 + l];
+  const float o0 = f32_value(y0 * c + (-y1) * s), o1 = f32_value(y1 * c + y0 * s);
+  if (F16OUT) {
+    ((f16 *)out)[(size_t)row * 128 + l] = (f16)o0;
+    ((f16 *)out)[(size_t)row * 128 + l + 64] = (f16)o1;
+  } else {
+    ((float *)out)[(size_t)row * 128 + l] = o0;
+    ((float *)out)[(size_t)row * 128 + l + 64] = o1;
+  }
+}
+
+// kc/vc (kvh, cap, dim) rows pos0 + t of k/v (T, kvh, dim), fp16, 16 bytes a thread.
+__global__ __launch_bounds__(256) void k_kv_append(const uint4 *__restrict__ k, const uint4 *__restrict__ v,
+                                                   uint4 *__restrict__ kc, uint4 *__restrict__ vc, uint32_t kvh,
+                                                   uint32_t cap, uint32_t vecs, uint32_t pos0, uint64_t total) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const uint64_t row = i / vecs, c = i % vecs;  // row = t * kvh + head
+  const uint64_t t = row / kvh, hd = row % kvh;
+  const uint64_t dst = (hd * cap + pos0 + t) * vecs + c;
+  kc[dst] = k[i];
+  vc[dst] = v[i];
+}
+
+template <bool F16OUT>
+__global__ __launch_bounds__(256) void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u,
+                                                  void *__restrict__ out, uint64_t n, uint32_t stride) {
+#pragma clang fp contract(off)
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float gv = g[i * stride], uv = u[i * stride];
+  const float y = f32_value(gv / (1.0f + (float)exp(-(double)gv)) * uv);
+  if (F16OUT)
+    ((f16 *)out)[i] = (f16)y;
+  else
+    ((float *)out)[i] = y;
+}
+
+__global__ __launch_bounds__(256) void k_add(float *__restrict__ y, const float *__restrict__ x, uint64_t n) {
+#pragma clang fp contract(off)
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) y[i] = y[i] + x[i];
+}
+
+// out (T, hidden) fp32 = rows ids[t] of the fp16 table; a row whose id is outside [0, vocab) is NaN.
+__global__ __launch_bounds__(256) void k_embed_ids(const int32_t *__restrict__ ids, const f16 *__restrict__ table,
+                                                   float *__restrict__ out, uint32_t hidden, uint32_t vocab) {
+  const uint32_t t = blockIdx.y;
+  const int32_t id = ids[t];
+  const bool ok = id >= 0 && (uint32_t)id < vocab;
+  const f16 *row = table + (size_t)(ok ? id : 0) * hidden;
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < hidden; i += gridDim.x * 256)
+    out[(size_t)t * hidden + i] = ok ? (float)row[i] : __builtin_nanf("");
+}
+
+constexpr uint32_t kArgParts = 64;  // workgroups a row
+
+__device__ __forceinline__ void arg_better(float &bv, uint32_t &bi, float v, uint32_t i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+// Pass 1: workgroup (part, row) takes a contiguous share of the row; its best (value, index) goes
+// to the workspace.
+__global__ __launch_bounds__(256) void k_argmax_part(const float *__restrict__ x, uint64_t n,
+                                                     float *__restrict__ part_v, uint32_t *__restrict__ part_i) {
+  __shared__ float sv[4];
+  __shared__ uint32_t si[4];
+  const uint32_t t = threadIdx.x, lane = t & 63;
+  const uint64_t per = (n + kArgParts - 1) / kArgParts;
+  const uint64_t lo = blockIdx.x * per, hi = lo + per < n ? lo + per : n;
+  const float *xr = x + (size_t)blockIdx.y * n;
+  float bv = -__builtin_inff();
+  uint32_t bi = 0xffffffffu;
+  for (uint64_t i = lo + t; i < hi; i += 256) arg_better(bv, bi, xr[i], (uint32_t)i);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) arg_better(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+  if (lane == 0) {
+    sv[t >> 6] = bv;
+    si[t >> 6] = bi;
+  }
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < 4; w++) arg_better(bv, bi, sv[w], si[w]);
+    part_v[(size_t)blockIdx.y * kArgParts + blockIdx.x] = bv;
+    part_i[(size_t)blockIdx.y * kArgParts + blockIdx.x] = bi;
+  }
+}
+
+// Pass 2: one wave a row over its kArgParts partials.
+__global__ __launch_bounds__(64) void k_argmax_final(const float *__restrict__ x, uint64_t n,
+                                                     const float *__restrict__ part_v,
+                                                     const uint32_t *__restrict__ part_i, int32_t *__restrict__ out) {
+  const uint32_t lane = threadIdx.x, row = blockIdx.x;
+  float bv = part_v[(size_t)row * kArgParts + lane];
+  uint32_t bi = part_i[(size_t)row * kArgParts + lane];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) arg_better(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+  if (lane == 0) {
+    const float x0 = x[(size_t)row * n];
+    out[row] = (x0 != x0 || bi == 0xffffffffu) ? 0 : (int32_t)bi;
+  }
+}
+
+uint32_t blocks_of(uint64_t n) { return (uint32_t)((n + 255) / 256); }
+
+}  // namespace
+
+extern "C" {
+
+HWK_API char *hwk_rope_tables(uint64_t theta_bits, uint32_t start, uint32_t n, uint32_t head_dim, float *cos_out,
+                              float *sin_out) {
+  HWK_CHECK(cos_out && sin_out, "hwk_rope_tables: null output");
+  HWK_CHECK(head_dim >= 2 && head_dim % 2 == 0, "hwk_rope_tables: head_dim %u is not even", head_dim);
+  double theta;
+  memcpy(&theta, &theta_bits, 8);
+  HWK_CHECK(theta > 1.0 && isfinite(theta), "hwk_rope_tables: theta %g", theta);
+  const uint32_t half = head_dim / 2;
+  for (uint32_t i = 0; i < n; i++)
+    for (uint32_t j = 0; j < half; j++) {
+      const double inv = 1.0 / pow(theta, (double)(2 * j) / (double)head_dim);
+      const double a = (double)(start + i) * inv;
+      cos_out[(size_t)i * half + j] = (float)cos(a);
+      sin_out[(size_t)i * half + j] = (float)sin(a);
+    }
+  return nullptr;
+}
+
+HWK_API char *hwk_rmsnorm(void *stream, const void *x, const void *w, void *out, uint32_t rows, uint32_t n,
+                          uint64_t eps_bits, int out_mode) {
+  HWK_CHECK((x && out) || rows == 0, "hwk_rmsnorm: null pointer");
+  HWK_CHECK(w, "hwk_rmsnorm: null weights");
+  HWK_CHECK(out_mode == HWK_OUT_F32 || out_mode == HWK_OUT_F16, "hwk_rmsnorm: out_mode %d", out_mode);
+  HWK_CHECK(hwk::aligned(x, 4) && hwk::aligned(w, 4) && hwk::aligned(out, out_mode == HWK_OUT_F16 ? 2 : 4),
+            "hwk_rmsnorm: misaligned pointer");
+  double eps;
+  memcpy(&eps, &eps_bits, 8);
+  HWK_CHECK(eps >= 0.0 && isfinite(eps), "hwk_rmsnorm: eps %g", eps);
+  HWK_CHECK(n > 0 || rows == 0, "hwk_rmsnorm: rows of 0 values");
+  if (rows == 0) return nullptr;
+  hipStream_t st = (hipStream_t)stream;
+  if (out_mode == HWK_OUT_F16)
+    hipLaunchKernelGGL(k_rmsnorm<true>, dim3(rows), dim3(256), 0, st, (const float *)x, (const float *)w, eps, out, n);
+  else
+    hipLaunchKernelGGL(k_rmsnorm<false>, dim3(rows), dim3(256), 0, st, (const float *)x, (const float *)w, eps, out,
+                       n);
+  return hwk::launched("hwk_rmsnorm");
+}
+
+HWK_API char *hwk_rope(void *stream, const void *x, const void *norm_w, const void *cos_t, const void *sin_t,
+                       void *out, uint32_t tokens, uint32_t heads, uint32_t head_dim, uint32_t pos0,
+                       uint32_t table_rows, uint64_t eps_bits, int out_mode) {
+  HWK_CHECK(((x && out) || (uint64_t)tokens * heads == 0) && cos_t && sin_t, "hwk_rope: null pointer");
+  HWK_CHECK(head_dim == 128, "hwk_rope: head_dim %u (128 only)", head_dim);
+  HWK_CHECK(out_mode == HWK_OUT_F32 || out_mode == HWK_OUT_F16, "hwk_rope: out_mode %d", out_mode);
+  HWK_CHECK((uint64_t)pos0 + tokens <= table_rows, "hwk_rope: positions %u..%u past the %u table rows", pos0,
+            pos0 + tokens, table_rows);
+  double eps;
+  memcpy(&eps, &eps_bits, 8);
+  HWK_CHECK(!norm_w || (eps >= 0.0 && isfinite(eps)), "hwk_rope: eps %g", eps);
+  const uint64_t rows = (uint64_t)tokens * heads;
+  HWK_CHECK(rows < (1ull << 31), "hwk_rope: %llu rows", (unsigned long long)rows);
+  if (rows == 0) return nullptr;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((uint32_t)((rows + 3) / 4));
+  if (out_mode == HWK_OUT_F16)
+    hipLaunchKernelGGL(k_norm_rope<true>, grid, dim3(256), 0, st, (const float *)x, (const float *)norm_w,
+                       (const float *)cos_t, (const float *)sin_t, eps, out, heads, (uint32_t)rows, pos0);
+  else
+    hipLaunchKernelGGL(k_norm_rope<false>, grid, dim3(256), 0, st, (const float *)x, (const float *)norm_w,
+                       (const float *)cos_t, (const float *)sin_t, eps, out, heads, (uint32_t)rows, pos0);
+  return hwk::launched("hwk_rope");
+}
+
+HWK_API char *hwk_kv_append(void *stream, const void *k, const void *v, void *k_cache, void *v_cache, uint32_t tokens,
+                            uint32_t kv_heads, uint32_t head_dim, uint32_t capacity, uint32_t pos0) {
+  HWK_CHECK((k && v) || tokens == 0, "hwk_kv_append: null pointer");
+  HWK_CHECK(k_cache && v_cache, "hwk_kv_append: null cache");
+  HWK_CHECK(head_dim % 8 == 0 && head_dim > 0, "hwk_kv_append: head_dim %u is not a multiple of 8", head_dim);
+  HWK_CHECK((uint64_t)pos0 + tokens <= capacity, "hwk_kv_append: rows %u..%u past capacity %u", pos0, pos0 + tokens,
+            capacity);
+  const uint64_t total = (uint64_t)tokens * kv_heads * (head_dim / 8);
+  if (total == 0) return nullptr;  // nothing to write: k and v may be NULL
+  HWK_CHECK(hwk::aligned(k, 16) && hwk::aligned(v, 16) && hwk::aligned(k_cache, 16) && hwk::aligned(v_cache, 16),
+            "hwk_kv_append: pointers must be 16-byte aligned");
+  hipLaunchKernelGGL(k_kv_append, dim3(blocks_of(total)), dim3(256), 0, (hipStream_t)stream, (const uint4 *)k,
+                     (const uint4 *)v, (uint4 *)k_cache, (uint4 *)v_cache, kv_heads, capacity, head_dim / 8, pos0,
+                     total);
+  return hwk::launched("hwk_kv_append");
+}
+
+HWK_API char *hwk_silu_mul(void *stream, const void *gate, const void *up, void *out, uint64_t n, uint32_t stride,
+                           int out_mode) {
+  HWK_CHECK((gate && up && out) || n == 0, "hwk_silu_mul: null pointer");
+  HWK_CHECK(stride >= 1, "hwk_silu_mul: stride 0");
+  HWK_CHECK(out_mode == HWK_OUT_F32 || out_mode == HWK_OUT_F16, "hwk_silu_mul: out_mode %d", out_mode);
+  if (n == 0) return nullptr;
+  hipStream_t st = (hipStream_t)stream;
+  if (out_mode == HWK_OUT_F16)
+    hipLaunchKernelGGL(k_silu_mul<true>, dim3(blocks_of(n)), dim3(256), 0, st, (const float *)gate, (const float *)up,
+                       out, n, stride);
+  else
+    hipLaunchKernelGGL(k_silu_mul<false>, dim3(blocks_of(n)), dim3(256), 0, st, (const float *)gate,
+                       (const float *)up, out, n, stride);
+  return hwk::launched("hwk_silu_mul");
+}
+
+HWK_API char *hwk_add(void *stream, void *y, const void *x, uint64_t n) {
+  HWK_CHECK((y && x) || n == 0, "hwk_add: null pointer");
+  if (n == 0) return nullptr;
+  hipLaunchKernelGGL(k_add, dim3(blocks_of(n)), dim3(256), 0, (hipStream_t)stream, (float *)y, (const float *)x, n);
+  return hwk::launched("hwk_add");
+}
+
+HWK_API char *hwk_embed(void *stream, const void *table, const void *ids, void *out, uint32_t tokens, uint32_t hidden,
+                        uint32_t vocab) {
+  HWK_CHECK(table && ((ids && out) || tokens == 0), "hwk_embed: null pointer");
+  HWK_CHECK(vocab > 0 && hidden > 0, "hwk_embed: empty table");
+  HWK_CHECK(tokens <= 65535, "hwk_embed: %u tokens (at most 65535)", tokens);
+  if (tokens == 0) return nullptr;
+  const uint32_t bx = (hidden + 255) / 256 < 8 ? (hidden + 255) / 256 : 8;
+  hipLaunchKernelGGL(k_embed_ids, dim3(bx, tokens), dim3(256), 0, (hipStream_t)stream, (const int32_t *)ids,
+                     (const f16 *)table, (float *)out, hidden, vocab);
+  return hwk::launched("hwk_embed");
+}
+
+HWK_API size_t hwk_argmax_workspace_bytes(uint32_t rows) { return (size_t)rows * kArgParts * 8; }
+
+HWK_API char *hwk_argmax(void *stream, const void *x, void *out, uint32_t rows, uint64_t n, void *workspace,
+                         size_t workspace_bytes) {
+  HWK_CHECK(x && out && workspace, "hwk_argmax: null pointer");
+  HWK_CHECK(n > 0 && n < 0xffffffffull, "hwk_argmax: %llu values a row (1 .. 2^32 - 2)", (unsigned long long)n);
+  HWK_CHECK(rows <= 65535, "hwk_argmax: %u rows (at most 65535)", rows);
+  HWK_CHECK(workspace_bytes >= hwk_argmax_workspace_bytes(rows), "hwk_argmax: workspace %zu bytes, %zu needed",
+            workspace_bytes, hwk_argmax_workspace_bytes(rows));
+  HWK_CHECK(hwk::aligned(workspace, 4) && hwk::aligned(x, 4) && hwk::aligned(out, 4), "hwk_argmax: misaligned pointer");
+  if (rows == 0) return nullptr;
+  float *pv = (float *)workspace;
+  uint32_t *pi = (uint32_t *)(pv + (size_t)rows * kArgParts);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_argmax_part, dim3(kArgParts, rows), dim3(256), 0, st, (const float *)x, n, pv, pi);
+  if (char *e = hwk::launched("hwk_argmax")) return e;
+  hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, (const float *)x, n, pv, pi, (int32_t *)out);
+  return hwk::launched("hwk_argmax (final)");
+}
+
+}  // extern "C"

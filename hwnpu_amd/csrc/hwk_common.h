@@ -99,10 +99,19 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// v as a float32 value of its own: instruction selection cannot see through the empty asm, so a
+// conversion to fp16 that follows rounds this float32 (twice rounded, as the reference's fp16
+// storage of a float32 result). Without it the backend folds a product and the conversion into
+// one mixed-precision FMA that rounds the exact product to fp16 once.
+__device__ __forceinline__ float f32_value(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Store one GEMV/GEMM output per out_mode.
 __device__ __forceinline__ void store_out(void *y, size_t i, float v, int mode) {
   if (mode == HWK_OUT_F16)
-    ((f16 *)y)[i] = (f16)v;
+    ((f16 *)y)[i] = (f16)f32_value(v);
   else if (mode == HWK_OUT_ADD_F32)
     ((float *)y)[i] += v;
   else

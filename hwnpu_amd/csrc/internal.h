@@ -69,6 +69,6 @@ __device__ __forceinline__ void head_norm_rope(float x0, float x1, const float *
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
   const float r = (float)(1.0 / sqrt(ss / 128.0 + eps));
   const float y0 = (x0 * r) * nw[l], y1 = (x1 * r) * nw[l + 64];
-  o0 = y0 * c + (-y1) * s;  // j < half: x*cos + (-x[j+half])*sin
-  o1 = y1 * c + y0 * s;     // j >= half: x*cos + x[j-half]*sin
+  o0 = f32_value(y0 * c + (-y1) * s);  // j < half: x*cos + (-x[j+half])*sin
+  o1 = f32_value(y1 * c + y0 * s);     // j >= half: x*cos + x[j-half]*sin
 }

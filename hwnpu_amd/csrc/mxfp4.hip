@@ -237,7 +237,7 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
     const float r = (float)(1.0 / sqrt(ss / (double)k + in.eps));
 #pragma unroll
     for (int j = 0; j < PER; j++)
-      if (t + j * NT < k) xh[t + j * NT] = (f16)((hv[j] * r) * wv[j]);
+      if (t + j * NT < k) xh[t + j * NT] = (f16)f32_value((hv[j] * r) * wv[j]);
   } else {
     for (uint32_t i = t; i < nb * 4; i += NT) xs[i] = in.x16[i];
   }
@@ -280,13 +280,79 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
           if (r0 + i + 1 < n) {
 #pragma clang fp contract(off)
             const float g = v[i], u = v[i + 1];
-            ((f16 *)y)[(r0 + i) / 2] = (f16)(g / (1.0f + (float)exp(-(double)g)) * u);
+            ((f16 *)y)[(r0 + i) / 2] = (f16)f32_value(g / (1.0f + (float)exp(-(double)g)) * u);
           }
         }
       } else {
 #pragma unroll
         for (int i = 0; i < RPW; i++)
           if (r0 + i < n) store_out(y, r0 + i, v[i], mode);
+      }
+    }
+    if (next >= sets) break;
+    set = next;
+    cur = nxt;
+  }
+}
+
+// K1r: the MXFP4 GEMV of T <= 8 vectors at once (speculative verify, a few tokens), every weight
+// row read once for all of them, as the reference's mxfp4.Run serves several vectors from one read
+// of a row (internal/mxfp4/matvec.go:33-160). The workgroup copies X (T, k) fp16 into LDS; its
+// waves stream row sets as the batch-1 GEMV does (64 lanes a row, BPL blocks a lane), each lane
+// taking its block's x of every vector from LDS. Y (T, n) per out_mode.
+template <int BPL, int RPW, int TT>
+__global__ __launch_bounds__(256) void k_mxfp4_gemv_rows(const uint4 *__restrict__ w, const uint8_t *__restrict__ e,
+                                                         const uint4 *__restrict__ x, void *__restrict__ y,
+                                                         uint32_t n, uint32_t nb, int mode) {
+  extern __shared__ uint4 xs[];  // (TT, nb * 4)
+  const int t = threadIdx.x, lane = t & 63;
+  const uint32_t waves = gridDim.x * 4;
+  uint32_t set = blockIdx.x * 4 + (t >> 6);
+  const uint32_t sets = (n + RPW - 1) / RPW;
+  const bool live = set < sets;
+  RowSet<BPL, RPW> cur, nxt;
+  if (live) load_rowset<64, BPL, RPW>(cur, w, e, set * RPW, n, nb, lane);
+  for (uint32_t i = t; i < TT * nb * 4; i += 256) xs[i] = x[i];
+  __syncthreads();
+  if (!live) return;
+  for (;;) {
+    const uint32_t next = set + waves;
+    if (next < sets) load_rowset<64, BPL, RPW>(nxt, w, e, next * RPW, n, nb, lane);
+    float acc[RPW][TT];
+#pragma unroll
+    for (int i = 0; i < RPW; i++)
+#pragma unroll
+      for (int v = 0; v < TT; v++) acc[i][v] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < BPL; j++) {
+      const uint32_t b = j * 64 + lane;
+      if (b >= nb) continue;
+#pragma unroll
+      for (int v = 0; v < TT; v++) {
+        const uint4 *xv = xs + (size_t)v * nb * 4 + b * 4;
+        const uint4 xr[4] = {xv[0], xv[1], xv[2], xv[3]};
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+          float d0 = 0.0f, d1 = 0.0f;
+          const uint32_t cw[4] = {cur.c[i][j].x, cur.c[i][j].y, cur.c[i][j].z, cur.c[i][j].w};
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<0>(cw[q]), h2_of_bits(xr[q].x), d0, false);
+            d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<1>(cw[q]), h2_of_bits(xr[q].y), d1, false);
+            d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<2>(cw[q]), h2_of_bits(xr[q].z), d0, false);
+            d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<3>(cw[q]), h2_of_bits(xr[q].w), d1, false);
+          }
+          acc[i][v] += (d0 + d1) * e8m0_scale(cur.s[i][j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const uint32_t r = set * RPW + i;
+#pragma unroll
+      for (int v = 0; v < TT; v++) {
+        const float sum = group_sum<64>(acc[i][v]);
+        if (lane == 0 && r < n) store_out(y, (size_t)v * n + r, sum, mode);
       }
     }
     if (next >= sets) break;
@@ -311,7 +377,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_f16(const float *__restrict__ h
   __syncthreads();
   ss = ((red[0] + red[1]) + red[2]) + red[3];
   const float r = (float)(1.0 / sqrt(ss / (double)k + eps));
-  for (uint32_t i = t; i < k; i += 256) out[(size_t)blockIdx.x * k + i] = (f16)((hr[i] * r) * nw[i]);
+  for (uint32_t i = t; i < k; i += 256) out[(size_t)blockIdx.x * k + i] = (f16)f32_value((hr[i] * r) * nw[i]);
 }
 
 // ---- the encoder (reference internal/mxfp4/encode.go:11-78), one thread a block, in float64
@@ -529,6 +595,48 @@ HWK_API char *hwk_mxfp4_gemv(void *stream, const void *w, const void *e, const v
     default: launch_bpl<8>(bpl, st, w, e, x, y, n, nb, out_mode); break;
   }
   return hwk::launched("hwk_mxfp4_gemv");
+}
+
+HWK_API char *hwk_mxfp4_gemv_rows(void *stream, const void *w, const void *e, const void *x, void *y, uint32_t n,
+                                  uint32_t k, uint32_t tokens, int out_mode) {
+  HWK_CHECK(w && e && x && y, "hwk_mxfp4_gemv_rows: null pointer");
+  HWK_CHECK(k % 32 == 0 && k > 0 && k <= 64 * 4 * 32, "hwk_mxfp4_gemv_rows: k=%u (a multiple of 32 up to 8192)", k);
+  HWK_CHECK(tokens >= 1 && tokens <= 8, "hwk_mxfp4_gemv_rows: %u vectors (1..8)", tokens);
+  HWK_CHECK((size_t)tokens * k * 2 <= 64 * 1024, "hwk_mxfp4_gemv_rows: %u x %u fp16 vectors exceed 64 KB", tokens, k);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "hwk_mxfp4_gemv_rows: out_mode %d", out_mode);
+  HWK_CHECK(hwk::aligned(w, 16) && hwk::aligned(x, 16), "hwk_mxfp4_gemv_rows: w and x must be 16-byte aligned");
+  HWK_CHECK(hwk::aligned(y, out_mode == HWK_OUT_F16 ? 2 : 4), "hwk_mxfp4_gemv_rows: y misaligned");
+  if (n == 0) return nullptr;
+  const uint32_t nb = k / 32;
+  constexpr int RPW = 2;
+  const uint32_t sets = (n + RPW - 1) / RPW;
+  const uint32_t waves = sets < stream_waves() ? sets : stream_waves();
+  const dim3 grid((waves + 3) / 4), block(256);
+  const size_t lds = (size_t)tokens * k * 2;
+  hipStream_t st = (hipStream_t)stream;
+#define HWK_ROWS(B, T)                                                                                        \
+  hipLaunchKernelGGL((k_mxfp4_gemv_rows<B, RPW, T>), grid, block, lds, st, (const uint4 *)w, (const uint8_t *)e, \
+                     (const uint4 *)x, y, n, nb, out_mode)
+#define HWK_ROWS_T(B)                \
+  switch (tokens) {                  \
+    case 1: HWK_ROWS(B, 1); break;   \
+    case 2: HWK_ROWS(B, 2); break;   \
+    case 3: HWK_ROWS(B, 3); break;   \
+    case 4: HWK_ROWS(B, 4); break;   \
+    case 5: HWK_ROWS(B, 5); break;   \
+    case 6: HWK_ROWS(B, 6); break;   \
+    case 7: HWK_ROWS(B, 7); break;   \
+    default: HWK_ROWS(B, 8); break;  \
+  }
+  switch ((nb + 63) / 64) {
+    case 1: HWK_ROWS_T(1) break;
+    case 2: HWK_ROWS_T(2) break;
+    case 3: HWK_ROWS_T(3) break;
+    default: HWK_ROWS_T(4) break;
+  }
+#undef HWK_ROWS_T
+#undef HWK_ROWS
+  return hwk::launched("hwk_mxfp4_gemv_rows");
 }
 
 HWK_API char *hwk_mxfp4_encode(void *stream, const void *x, void *w, void *e, uint32_t rows, uint32_t k) {

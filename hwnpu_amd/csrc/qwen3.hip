@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, f1
   const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   const float g = gu[2 * i], u = gu[2 * i + 1];
-  act[i] = (f16)(g / (1.0f + (float)exp(-(double)g)) * u);
+  act[i] = (f16)f32_value(g / (1.0f + (float)exp(-(double)g)) * u);
 }
 
 __global__ void k_set_i32(int32_t *__restrict__ p, int32_t v) { *p = v; }
@@ -142,7 +142,8 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uin
     }
     if (t == 0) {
       const int32_t p = *pos;
-      hist[p + 1] = (int32_t)(i == 0xffffffffu ? 0 : i);
+      const float x0 = x[0];  // a NaN at index 0 is kept: strict > never replaces it
+      hist[p + 1] = (int32_t)((i == 0xffffffffu || x0 != x0) ? 0 : i);
       *pos = p + 1;
       *counter = 0;
     }

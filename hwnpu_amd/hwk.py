@@ -89,8 +89,18 @@ SIGNATURES = {
     "hwk_launch": (ERR, [P, C.POINTER(U32), C.POINTER(U32), U32, P, P, SZ]),
     "hwk_mxfp4_dequant_f16": (ERR, [P, P, P, P, U32, U32]),
     "hwk_mxfp4_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
+    "hwk_mxfp4_gemv_rows": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
     "hwk_i8_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
     "hwk_f16_gemv": (ERR, [P, P, P, P, U32, U32, C.c_int]),
+    "hwk_rope_tables": (ERR, [U64, U32, U32, U32, P, P]),
+    "hwk_rmsnorm": (ERR, [P, P, P, P, U32, U32, U64, C.c_int]),
+    "hwk_rope": (ERR, [P, P, P, P, P, P, U32, U32, U32, U32, U32, U64, C.c_int]),
+    "hwk_kv_append": (ERR, [P, P, P, P, P, U32, U32, U32, U32, U32]),
+    "hwk_silu_mul": (ERR, [P, P, P, P, U64, U32, C.c_int]),
+    "hwk_add": (ERR, [P, P, P, U64]),
+    "hwk_embed": (ERR, [P, P, P, P, U32, U32, U32]),
+    "hwk_argmax_workspace_bytes": (SZ, [U32]),
+    "hwk_argmax": (ERR, [P, P, P, U32, U64, P, SZ]),
     "hwk_i8_gemm": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
     "hwk_mxfp4_gemm": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
     "hwk_attn_workspace_bytes": (SZ, [C.POINTER(AttnParams)]),

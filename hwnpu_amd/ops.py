@@ -72,6 +72,20 @@ def mxfp4_gemv(w, e, x, out_mode="f32", y=None):
     return y
 
 
+def mxfp4_gemv_rows(w, e, x, out_mode="f32", y=None):
+    """Y (T, n) = X W^T for MXFP4 W (n, k) and T <= 8 fp16 vectors X (T, k), W read once for all."""
+    n, half = w.shape
+    k = half * 2
+    T = x.shape[0]
+    _need(w, "w", torch.uint8, (n, half))
+    _need(e, "e", torch.uint8, (n, k // 32))
+    _need(x, "x", torch.float16, (T, k))
+    y = _out2(y, T, n, out_mode, w.device)
+    hwk.load().hwk_mxfp4_gemv_rows(_stream(), w.data_ptr(), e.data_ptr(), x.data_ptr(), y.data_ptr(), n, k, T,
+                                   OUT_MODES[out_mode])
+    return y
+
+
 def i8_gemv(q, scale16, x, out_mode="f32", y=None):
     """y = scale * (Q x) for int8 Q (n, k) and fp16 per-row scales; x fp16 (k)."""
     n, k = q.shape
@@ -269,4 +283,110 @@ def moe_experts(x, idx, w, gu_w, gu_e, dn_w, dn_e, out=None, out_mode="f32", wor
     ws = torch.empty(max(n, 16), dtype=torch.uint8, device=x.device) if workspace is None else workspace
     hwk.load().hwk_moe_experts(_stream(), x.data_ptr(), idx.data_ptr(), w.data_ptr(), gu_w.data_ptr(), gu_e.data_ptr(),
                                dn_w.data_ptr(), dn_e.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), p)
+    return out
+
+
+# ---------------- the decoder's small ops (K6) ----------------
+
+def f64_bits(v: float) -> int:
+    """A float64 scalar as the uint64 bit pattern the ABI takes."""
+    return struct.unpack("<Q", struct.pack("<d", float(v)))[0]
+
+
+def _f_out(shape, mode, device):
+    if mode not in ("f32", "f16"):
+        raise ValueError(f"out_mode {mode!r}: 'f32' or 'f16'")
+    return torch.empty(shape, dtype=torch.float16 if mode == "f16" else torch.float32, device=device)
+
+
+def rope_tables(theta: float, start: int, n: int, head_dim: int = 128):
+    """Host RoPE tables (n, head_dim/2) float32 of positions start .. start+n-1, on the GPU."""
+    import numpy as np
+
+    c = np.empty((n, head_dim // 2), np.float32)
+    s = np.empty((n, head_dim // 2), np.float32)
+    hwk.load().hwk_rope_tables(f64_bits(theta), start, n, head_dim, c.ctypes.data, s.ctypes.data)
+    return torch.from_numpy(c).cuda(), torch.from_numpy(s).cuda()
+
+
+def rmsnorm(x, w, eps: float, out_mode="f16"):
+    """RMSNorm of the rows of x (rows, n) fp32 with weights w (n) fp32."""
+    rows, n = x.shape
+    _need(x, "x", torch.float32, (rows, n))
+    _need(w, "w", torch.float32, (n,))
+    out = _f_out((rows, n), out_mode, x.device)
+    hwk.load().hwk_rmsnorm(_stream(), x.data_ptr(), w.data_ptr(), out.data_ptr(), rows, n, f64_bits(eps),
+                           OUT_MODES[out_mode])
+    return out
+
+
+def rope(x, cos_t, sin_t, pos0: int, norm_w=None, eps: float = 1e-6, out_mode="f16"):
+    """Per-head RMSNorm (when norm_w is given) then RoPE of x (T, heads, 128) fp32 at positions pos0+t."""
+    T, heads, d = x.shape
+    _need(x, "x", torch.float32, (T, heads, d))
+    _need(cos_t, "cos_t", torch.float32)
+    _need(sin_t, "sin_t", torch.float32, tuple(cos_t.shape))
+    if norm_w is not None:
+        _need(norm_w, "norm_w", torch.float32, (d,))
+    out = _f_out((T, heads, d), out_mode, x.device)
+    hwk.load().hwk_rope(_stream(), x.data_ptr(), 0 if norm_w is None else norm_w.data_ptr(), cos_t.data_ptr(),
+                        sin_t.data_ptr(), out.data_ptr(), T, heads, d, pos0, cos_t.shape[0], f64_bits(eps),
+                        OUT_MODES[out_mode])
+    return out
+
+
+def kv_append(k, v, k_cache, v_cache, pos0: int):
+    """Write k, v (T, kv_heads, d) fp16 into rows pos0.. of the caches (kv_heads, capacity, d)."""
+    T, kvh, d = k.shape
+    cap = k_cache.shape[1]
+    _need(k, "k", torch.float16, (T, kvh, d))
+    _need(v, "v", torch.float16, (T, kvh, d))
+    _need(k_cache, "k_cache", torch.float16, (kvh, cap, d))
+    _need(v_cache, "v_cache", torch.float16, (kvh, cap, d))
+    hwk.load().hwk_kv_append(_stream(), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), T, kvh, d,
+                             cap, pos0)
+
+
+def silu_mul(gate, up, out_mode="f16", stride: int = 1, n=None):
+    """silu(gate) * up elementwise over n values taken every `stride` floats of gate and up."""
+    if n is None:
+        n = gate.numel() // stride
+    if gate.dtype != torch.float32 or up.dtype != torch.float32 or not gate.is_cuda or not up.is_cuda:
+        raise TypeError("gate, up: fp32 tensors on the GPU")
+    for t, name in ((gate, "gate"), (up, "up")):
+        end = t.storage_offset() + (n - 1) * stride + 1
+        if n and end > t.untyped_storage().nbytes() // 4:
+            raise ValueError(f"{name}: {n} values at stride {stride} run past the tensor's storage")
+    out = _f_out((n,), out_mode, gate.device)
+    hwk.load().hwk_silu_mul(_stream(), gate.data_ptr(), up.data_ptr(), out.data_ptr(), n, stride, OUT_MODES[out_mode])
+    return out
+
+
+def add_(y, x):
+    """y += x in fp32."""
+    _need(y, "y", torch.float32)
+    _need(x, "x", torch.float32, tuple(y.shape))
+    hwk.load().hwk_add(_stream(), y.data_ptr(), x.data_ptr(), y.numel())
+    return y
+
+
+def embed(table, ids):
+    """Rows ids (T) int32 of the fp16 table (vocab, hidden), as fp32 (T, hidden)."""
+    vocab, hidden = table.shape
+    _need(table, "table", torch.float16, (vocab, hidden))
+    _need(ids, "ids", torch.int32)
+    out = torch.empty((ids.numel(), hidden), dtype=torch.float32, device=table.device)
+    hwk.load().hwk_embed(_stream(), table.data_ptr(), ids.data_ptr(), out.data_ptr(), ids.numel(), hidden, vocab)
+    return out
+
+
+def argmax(x):
+    """The greedy pick of each row of x (rows, n) fp32, int32 (rows)."""
+    if x.dim() == 1:
+        x = x.view(1, -1)
+    rows, n = x.shape
+    _need(x, "x", torch.float32, (rows, n))
+    out = torch.empty(rows, dtype=torch.int32, device=x.device)
+    ws = torch.empty(max(16, hwk.load().hwk_argmax_workspace_bytes(rows)), dtype=torch.uint8, device=x.device)
+    hwk.load().hwk_argmax(_stream(), x.data_ptr(), out.data_ptr(), rows, n, ws.data_ptr(), ws.numel())
     return out

@@ -112,6 +112,13 @@ HWK_API char *hwk_mxfp4_dequant_f16(void *stream, const void *w, const void *e, 
 HWK_API char *hwk_mxfp4_gemv(void *stream, const void *w, const void *e, const void *x, void *y,
                              uint32_t n, uint32_t k, int out_mode);
 
+/* K1r: Y (tokens, n) = X (tokens, k) W^T for tokens <= 8 fp16 vectors (tokens * k * 2 <= 64 KB), every
+ * weight row read once for all of them (replaces mxfp4.Run serving several vectors from one read of
+ * a row, reference internal/mxfp4/matvec.go:33-160; speculative verify, internal/llm/decode/decode.go:
+ * 1235-1261). Y per out_mode, row t at y + t*n. */
+HWK_API char *hwk_mxfp4_gemv_rows(void *stream, const void *w, const void *e, const void *x, void *y,
+                                  uint32_t n, uint32_t k, uint32_t tokens, int out_mode);
+
 /* ---- int8 per-output-channel weights: codes (n, k) int8 row-major, scales (n) fp16
  * (reference internal/milcpu/ops.go:1589-1610 constexpr_blockwise_shift_scale, the
  * mlpackage.Int8Scaled layout internal/mlpackage/program.go:421-461). ---- */
@@ -141,6 +148,50 @@ HWK_API char *hwk_mxfp4_gemm(void *stream, const void *x, const void *w, const v
  * internal/llm/qwen3/build.go:107-109). k a multiple of 8. */
 HWK_API char *hwk_f16_gemv(void *stream, const void *w, const void *x, void *y, uint32_t n,
                            uint32_t k, int out_mode);
+
+/* ---- the decoder's small ops (K6): what the reference's graph runs between the linears
+ * (internal/llm/blocks/blocks.go, internal/llm/qwen3/build.go:107-311). Float scalars travel as
+ * float64 bit patterns. ---- */
+
+/* RoPE tables of positions start .. start+n-1, on the HOST: cos_out/sin_out (n, head_dim/2) float32
+ * of float64 cos/sin of p * theta^(-2j/head_dim) (reference internal/llm/qwen3/config.go:152-159,
+ * blocks.go:412-425: the cat(freqs, freqs) table stored once). Touches no device. */
+HWK_API char *hwk_rope_tables(uint64_t theta_bits, uint32_t start, uint32_t n, uint32_t head_dim,
+                              float *cos_out, float *sin_out);
+/* out (rows, n) = (x * r) * w, r = float(1/sqrt(mean(x^2) + eps)) with the sum in float64; x, w fp32,
+ * out fp16 or fp32 (reference blocks.go:351-395, RMSNormWith). */
+HWK_API char *hwk_rmsnorm(void *stream, const void *x, const void *w, void *out, uint32_t rows, uint32_t n,
+                          uint64_t eps_bits, int out_mode);
+/* x (tokens, heads, 128) fp32: each head's RMSNorm with norm_w (128) when norm_w is not NULL (Qwen3's
+ * q/k norm before RoPE), then RoPE at position pos0 + token with rotate_half over tables from
+ * hwk_rope_tables (device copies of table_rows rows); out fp16 or fp32 (reference blocks.go:427-445,
+ * ApplyRope). */
+HWK_API char *hwk_rope(void *stream, const void *x, const void *norm_w, const void *cos_t, const void *sin_t,
+                       void *out, uint32_t tokens, uint32_t heads, uint32_t head_dim, uint32_t pos0,
+                       uint32_t table_rows, uint64_t eps_bits, int out_mode);
+/* Copies k, v (tokens, kv_heads, head_dim) fp16 into rows pos0 .. pos0+tokens-1 of the caches
+ * (kv_heads, capacity, head_dim) (reference decode.go:1668, writeRows); k and v may be NULL when
+ * tokens is 0. */
+HWK_API char *hwk_kv_append(void *stream, const void *k, const void *v, void *k_cache, void *v_cache,
+                            uint32_t tokens, uint32_t kv_heads, uint32_t head_dim, uint32_t capacity,
+                            uint32_t pos0);
+/* out[i] = g / (1 + float(exp(-g))) * u, exp in float64, g = gate[i*stride], u = up[i*stride], fp32
+ * in, fp16 or fp32 out (reference blocks.go:395-401 SiLU, SwiGLU; interleaved gate/up rows: gate =
+ * base, up = base + 1, stride 2). */
+HWK_API char *hwk_silu_mul(void *stream, const void *gate, const void *up, void *out, uint64_t n,
+                           uint32_t stride, int out_mode);
+/* y[i] += x[i], fp32 (the residual add). */
+HWK_API char *hwk_add(void *stream, void *y, const void *x, uint64_t n);
+/* out (tokens, hidden) fp32 = rows ids[t] (int32, device) of the fp16 table (vocab, hidden); a row
+ * whose id is outside [0, vocab) is NaN (reference qwen3 build.go embedding gather). */
+HWK_API char *hwk_embed(void *stream, const void *table, const void *ids, void *out, uint32_t tokens,
+                        uint32_t hidden, uint32_t vocab);
+/* Greedy pick a row: out[r] (int32, device) = the lowest index of the largest of x (rows, n) fp32, NaNs
+ * never chosen except a NaN at index 0, which is kept (strict >, reference internal/chat/sample.go:
+ * 80-87). Two launches over a workspace of hwk_argmax_workspace_bytes(rows). */
+HWK_API size_t hwk_argmax_workspace_bytes(uint32_t rows);
+HWK_API char *hwk_argmax(void *stream, const void *x, void *out, uint32_t rows, uint64_t n, void *workspace,
+                         size_t workspace_bytes);
 
 /* ---- decode attention (K4): one query token per head over a KV cache, split over the context
  * and merged as Flash-Decoding does (reference internal/llm/paged/paged.go:70-310, the per-chunk

@@ -82,6 +82,18 @@ FAKE = 0x10000  # never dereferenced: every case below is refused before a launc
     (lambda L: L.hwk_mxfp4_dequant_f16(None, FAKE, FAKE, FAKE, 4, 0), "multiple of 32"),
     (lambda L: L.hwk_synth_uniform(None, FAKE, 10, 1, 120, 20, 1), "range past int8"),
     (lambda L: L.hwk_synth_uniform(None, FAKE, 10, 1, 0, 20, 2), "elem_size"),
+    (lambda L: L.hwk_mxfp4_gemv_rows(None, FAKE, FAKE, FAKE, FAKE, 8, 64, 9, 0), "1..8"),
+    (lambda L: L.hwk_mxfp4_gemv_rows(None, FAKE, FAKE, FAKE, FAKE, 8, 8192, 5, 0), "exceed 64 KB"),
+    (lambda L: L.hwk_rmsnorm(None, FAKE, FAKE, FAKE, 4, 64, 0, 2), "out_mode"),
+    (lambda L: L.hwk_rmsnorm(None, FAKE, FAKE, FAKE, 4, 64, 0xFFF0000000000000, 0), "eps"),
+    (lambda L: L.hwk_rope(None, FAKE, 0, FAKE, FAKE, FAKE, 2, 4, 64, 0, 8, 0, 0), "head_dim"),
+    (lambda L: L.hwk_rope(None, FAKE, 0, FAKE, FAKE, FAKE, 2, 4, 128, 7, 8, 0, 0), "table rows"),
+    (lambda L: L.hwk_kv_append(None, FAKE, FAKE, FAKE, FAKE, 4, 8, 128, 64, 61), "past capacity"),
+    (lambda L: L.hwk_kv_append(None, FAKE + 8, FAKE, FAKE, FAKE, 4, 8, 128, 64, 0), "16-byte aligned"),
+    (lambda L: L.hwk_silu_mul(None, FAKE, FAKE, FAKE, 10, 0, 0), "stride 0"),
+    (lambda L: L.hwk_embed(None, FAKE, FAKE, FAKE, 70000, 64, 10), "65535"),
+    (lambda L: L.hwk_argmax(None, FAKE, FAKE, 4, 100, FAKE, 64), "workspace"),
+    (lambda L: L.hwk_argmax(None, FAKE, FAKE, 1, 0, FAKE, 4096), "values a row"),
 ])
 def test_bad_arguments_rejected(call, match):
     with pytest.raises(hwk.HwkError, match=match):
@@ -113,3 +125,23 @@ def test_qwen3_new_rejects_bad_config(field, value, match):
     out = C.c_void_p()
     with pytest.raises(hwk.HwkError, match=match):
         hwk.load().hwk_qwen3_new(C.byref(c), C.byref(out))
+
+
+def test_rope_tables_on_host_match_oracle():
+    """hwk_rope_tables runs on the host (no device): float32 of float64 cos/sin, as the oracle's."""
+    import numpy as np
+
+    from hwnpu_amd import ops
+    from oracle import oracle
+
+    n, start, d = 40, 1000, 128
+    c = np.empty((n, d // 2), np.float32)
+    s = np.empty((n, d // 2), np.float32)
+    hwk.load().hwk_rope_tables(ops.f64_bits(1e6), start, n, d, c.ctypes.data, s.ctypes.data)
+    oc, os_ = oracle.rope_tables(1e6, start, n, d)
+    assert np.array_equal(c, oc[:, : d // 2]) and np.array_equal(s, os_[:, : d // 2])
+    # position 0 is the identity rotation; cos^2 + sin^2 = 1
+    hwk.load().hwk_rope_tables(ops.f64_bits(1e6), 0, 1, d, c.ctypes.data, s.ctypes.data)
+    assert np.all(c[0] == 1) and np.all(s[0] == 0)
+    with pytest.raises(hwk.HwkError, match="theta"):
+        hwk.load().hwk_rope_tables(ops.f64_bits(0.5), 0, 1, d, c.ctypes.data, s.ctypes.data)

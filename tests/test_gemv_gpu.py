@@ -174,3 +174,32 @@ def test_f16_gemv_parity(dev, orc, n, k):
     check_close(y32, want)
     y16 = ops.f16_gemv(w, x, "f16").cpu().numpy()
     assert np.array_equal(y16.view(np.uint16), orc.f32_to_f16(y32))
+
+
+# ---------------- K1r: several vectors, weights read once ----------------
+
+@pytest.mark.parametrize("T,n,k", [(5, 8192, 2048), (1, 300, 6144), (2, 33, 96), (8, 2048, 2048), (3, 7, 4128),
+                                   (5, 6144, 2048), (4, 2048, 6144)])
+def test_mxfp4_gemv_rows_parity(dev, orc, T, n, k):
+    print(f"mxfp4_gemv_rows T={T} n={n} k={k}", flush=True)
+    w, e = synth.mxfp4_uniform(n, k, f"k1r.{n}.{k}")
+    x = synth.normal(T * k, f"k1r.{T}.{n}.{k}.x").view(T, k)
+    wd = orc.mxfp4_dequantize(w.cpu().numpy(), e.cpu().numpy())
+    want = orc.sgemm(x.cpu().numpy().astype(np.float32), wd, transb=True)
+    y32 = ops.mxfp4_gemv_rows(w, e, x, "f32").cpu().numpy()
+    for t in range(T):
+        check_close(y32[t], want[t])
+    # each vector's fp16 output is RNE of its fp32 accumulator; one vector alone equals K1's
+    y16 = ops.mxfp4_gemv_rows(w, e, x, "f16").cpu().numpy()
+    assert np.array_equal(y16.view(np.uint16), orc.f32_to_f16(y32))
+    one = ops.mxfp4_gemv(w, e, x[0].contiguous(), "f32").cpu().numpy()
+    check_close(one, y32[0], tol=1e-5)
+
+
+def test_mxfp4_gemv_rows_rejects_too_many(dev):
+    from hwnpu_amd import HwkError
+
+    w, e = synth.mxfp4_uniform(64, 256, "k1r.bad")
+    x = synth.normal(9 * 256, "k1r.bad.x").view(9, 256)
+    with pytest.raises(HwkError, match="1..8"):
+        ops.mxfp4_gemv_rows(w, e, x)
