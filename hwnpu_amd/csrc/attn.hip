@@ -48,39 +48,36 @@ struct Tile {
   float vscale[4];
 };
 
-// Loads tile keys [key0, key0+16) of the kv head whose rows start at head_base; keys at or past
-// `end` read as zeros (no load is issued for them).
+// Loads tile keys [key0, key0+16) of the kv head whose rows start at head_base. Every load is issued
+// unconditionally, keys at or past `rows` (the head's rows in memory) reading row rows-1 instead:
+// a predicated load would make the compiler wait for it before the next one is issued. The values
+// of keys past the attended range are dropped by attend_tile.
 template <bool I8>
 __device__ __forceinline__ void load_tile(Tile<I8> &t, const void *__restrict__ k, const void *__restrict__ v,
                                           const uint16_t *__restrict__ ks, const uint16_t *__restrict__ vs,
-                                          size_t head_base, uint32_t key0, uint32_t end, int lane) {
-  const uint32_t kk = key0 + (lane & 15);
+                                          size_t head_base, uint32_t key0, uint32_t rows, int lane) {
+  const uint32_t kk = min(key0 + (lane & 15), rows - 1);
   const int grp = lane >> 4;
 #pragma unroll
   for (int s = 0; s < 4; s++) {
     const size_t row = head_base + kk;
     if constexpr (I8) {
-      uint2 w = kk < end ? *(const uint2 *)((const uint8_t *)k + row * 128 + s * 32 + grp * 8) : make_uint2(0, 0);
-      t.k[s] = i8x8_to_half8(w);
+      t.k[s] = i8x8_to_half8(*(const uint2 *)((const uint8_t *)k + row * 128 + s * 32 + grp * 8));
     } else {
-      t.k[s] = half8_of(kk < end ? load_stream((const uint4 *)((const f16 *)k + row * 128 + s * 32 + grp * 8))
-                                 : make_uint4(0, 0, 0, 0));
+      t.k[s] = half8_of(load_stream((const uint4 *)((const f16 *)k + row * 128 + s * 32 + grp * 8)));
     }
   }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
-    const uint32_t key = key0 + 4 * r + grp;
-    const size_t row = head_base + key;
+    const size_t row = head_base + min(key0 + 4 * r + grp, rows - 1);
     if constexpr (I8) {
-      uint2 w = key < end ? *(const uint2 *)((const uint8_t *)v + row * 128 + (lane & 15) * 8) : make_uint2(0, 0);
-      t.v[r] = i8x8_to_half8(w);
-      t.vscale[r] = key < end ? (float)__builtin_bit_cast(f16, vs[row]) : 0.0f;
+      t.v[r] = i8x8_to_half8(*(const uint2 *)((const uint8_t *)v + row * 128 + (lane & 15) * 8));
+      t.vscale[r] = (float)__builtin_bit_cast(f16, vs[row]);
     } else {
-      t.v[r] = half8_of(key < end ? load_stream((const uint4 *)((const f16 *)v + row * 128 + (lane & 15) * 8))
-                                  : make_uint4(0, 0, 0, 0));
+      t.v[r] = half8_of(load_stream((const uint4 *)((const f16 *)v + row * 128 + (lane & 15) * 8)));
     }
   }
-  if constexpr (I8) t.kscale = kk < end ? (float)__builtin_bit_cast(f16, ks[head_base + kk]) : 0.0f;
+  if constexpr (I8) t.kscale = (float)__builtin_bit_cast(f16, ks[head_base + kk]);
 }
 
 __device__ __forceinline__ float max16(float x) {
@@ -132,13 +129,49 @@ __device__ __forceinline__ void attend_tile(const Tile<I8> &t, const half8 (&qa)
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int src = 4 * r + (lane >> 4);
+    // a row past end was loaded from another row (load_tile): zero it, as p = 0 times NaN is NaN
+    const bool vok = key0 + (uint32_t)src < end;
+    const half8 vr = vok ? t.v[r] : half8_of(make_uint4(0, 0, 0, 0));
 #pragma unroll
     for (int g = 0; g < G; g++) {
       float pv = __shfl(p[g], src, 64);
-      if constexpr (I8) pv *= t.vscale[r];
+      if constexpr (I8) pv *= vok ? t.vscale[r] : 0.0f;
 #pragma unroll
-      for (int d = 0; d < 8; d++) acc[g][d] = fmaf(pv, (float)t.v[r][d], acc[g][d]);
+      for (int d = 0; d < 8; d++) acc[g][d] = fmaf(pv, (float)vr[d], acc[g][d]);
     }
+  }
+}
+
+// Attends a wave's nt tiles at key, key + STEP, ... whose first two loads are already in ta and tb
+// (issued unconditionally by the caller). While four or more tiles remain, each buffer takes the
+// load two tiles ahead as soon as it is attended; those loads sit in a loop body of its own with no
+// branch around them, so the wait counter keeps both buffers in flight. The last one to three
+// tiles load at most once more. prep(tile, key0) runs on a tile's registers before it is attended.
+template <int G, bool I8, uint32_t STEP, class Load, class Prep>
+__device__ __forceinline__ void run_tiles(Tile<I8> &ta, Tile<I8> &tb, uint32_t key, uint32_t nt, uint32_t end,
+                                          const half8 (&qa)[4], float scale_log2, int lane, float (&m)[G],
+                                          float (&l)[G], float (&acc)[G][8], Load load, Prep prep) {
+  uint32_t i = 0;
+  for (; i + 3 < nt; i += 2, key += 2 * STEP) {
+    prep(ta, key);
+    attend_tile<G, I8>(ta, qa, key, end, scale_log2, lane, m, l, acc);
+    load(ta, key + 2 * STEP);
+    prep(tb, key + STEP);
+    attend_tile<G, I8>(tb, qa, key + STEP, end, scale_log2, lane, m, l, acc);
+    load(tb, key + 3 * STEP);
+  }
+  const uint32_t rem = nt - i;  // 0 .. 3
+  if (rem == 0) return;
+  prep(ta, key);
+  attend_tile<G, I8>(ta, qa, key, end, scale_log2, lane, m, l, acc);
+  if (rem == 3) load(ta, key + 2 * STEP);
+  if (rem >= 2) {
+    prep(tb, key + STEP);
+    attend_tile<G, I8>(tb, qa, key + STEP, end, scale_log2, lane, m, l, acc);
+  }
+  if (rem == 3) {
+    prep(ta, key + 2 * STEP);
+    attend_tile<G, I8>(ta, qa, key + 2 * STEP, end, scale_log2, lane, m, l, acc);
   }
 }
 
@@ -164,13 +197,14 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const uint4 *__restrict_
   const uint32_t end = begin + chunk < len ? begin + chunk : len;
   const size_t head_base = (size_t)h * cap;
 
-  // A operand: query head lane%16 (zero past G), dims s*32 + (lane/16)*8 .. +8
+  // A operand: query head lane%16, dims s*32 + (lane/16)*8 .. +8 (rows past G repeat head 0: their
+  // scores are never read)
   half8 qa[4];
   {
     const int g = lane & 15, grp = lane >> 4;
 #pragma unroll
     for (int s = 0; s < 4; s++)
-      qa[s] = half8_of(g < G ? q[((size_t)(h * G + g) * 128 + s * 32 + grp * 8) / 8] : make_uint4(0, 0, 0, 0));
+      qa[s] = half8_of(q[((size_t)(h * G + (g < G ? g : 0)) * 128 + s * 32 + grp * 8) / 8]);
   }
   float acc[G][8], m[G], l[G];
 #pragma unroll
@@ -183,17 +217,13 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const uint4 *__restrict_
   // this wave's tiles: begin + 16*wave + 16*W*j, two buffers in turn
   constexpr uint32_t STEP = 16 * W;
   Tile<I8> ta, tb;
-  uint32_t key = begin + 16 * wave;
-  if (key < end) load_tile<I8>(ta, k, v, ks, vs, head_base, key, end, lane);
-  while (key < end) {
-    if (key + STEP < end) load_tile<I8>(tb, k, v, ks, vs, head_base, key + STEP, end, lane);
-    attend_tile<G, I8>(ta, qa, key, end, scale_log2, lane, m, l, acc);
-    key += STEP;
-    if (key >= end) break;
-    if (key + STEP < end) load_tile<I8>(ta, k, v, ks, vs, head_base, key + STEP, end, lane);
-    attend_tile<G, I8>(tb, qa, key, end, scale_log2, lane, m, l, acc);
-    key += STEP;
-  }
+  const uint32_t key = begin + 16 * wave;
+  const uint32_t nt = key < end ? (end - key + STEP - 1) / STEP : 0;
+  auto load = [&](Tile<I8> &t, uint32_t k0) { load_tile<I8>(t, k, v, ks, vs, head_base, k0, cap, lane); };
+  load(ta, key);
+  load(tb, key + STEP);
+  run_tiles<G, I8, STEP>(ta, tb, key, nt, end, qa, scale_log2, lane, m, l, acc, load,
+                         [](Tile<I8> &, uint32_t) {});
   // sum the four key slots of the wave (lanes lane%16 + 16j hold the same dims)
 #pragma unroll
   for (int g = 0; g < G; g++)
@@ -245,139 +275,31 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const uint4 *__restrict_
     }
   }
 }
-// The model's decode step form of k_attn_decode: q (and, in the chunk holding the new position,
-// the new k and v) made from the fp32 projection in the prologue, written to the cache there
-// before this workgroup reads it. Every workgroup leaves its chunk's partial (o unnormalized, m in
-// natural-log units, l) in the workspace for the consumer's merge, as k_attn_decode does with
-// several chunks. Position p = *pos; keys [0, p] are in use.
-template <int G, int W>
-__global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ qkv, const float *__restrict__ qn,
-                                                      const float *__restrict__ kn, const float *__restrict__ cos_t,
-                                                      const float *__restrict__ sin_t, double eps, f16 *__restrict__ kc,
-                                                      f16 *__restrict__ vc, float *__restrict__ ws_o,
-                                                      float *__restrict__ ws_m, float *__restrict__ ws_l,
-                                                      const int32_t *__restrict__ pos, uint32_t heads, uint32_t kvh,
-                                                      uint32_t cap, uint32_t chunk, uint32_t nchunk, float scale_log2) {
-  __shared__ float sm[W][G], sl[W][G];
-  __shared__ float sacc[W][G][128];
-  __shared__ __attribute__((aligned(16))) f16 qs[G][128];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t h = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
-  const uint32_t p = (uint32_t)*pos, len = p + 1;
-  const uint32_t begin = c * chunk;
-  const uint32_t end = begin + chunk < len ? begin + chunk : len;
-  const size_t head_base = (size_t)h * cap;
-  constexpr uint32_t STEP = 16 * W;
-  // this wave's first tile goes out before the prologue unless it holds p (written below)
-  Tile<false> ta, tb;
-  uint32_t key = begin + 16 * wave;
-  const bool early = key < end && !(key <= p && p < key + 16);
-  if (early) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, end, lane);
-  // prologue: jobs [0, G) the query heads of h; in the chunk holding p also G (k) and G+1 (v)
-  const uint32_t jobs = (p / chunk == c) ? G + 2 : G;
-  for (uint32_t j = wave; j < jobs; j += W) {
-    const uint32_t row = j < G ? h * G + j : j == G ? heads + h : heads + kvh + h;
-    const float x0 = qkv[(size_t)row * 128 + lane], x1 = qkv[(size_t)row * 128 + lane + 64];
-    if (j == G + 1) {
-      vc[(head_base + p) * 128 + lane] = (f16)x0;
-      vc[(head_base + p) * 128 + lane + 64] = (f16)x1;
-      continue;
-    }
-    float o0, o1;
-    head_norm_rope(x0, x1, j < G ? qn : kn, cos_t[(size_t)p * 64 + lane], sin_t[(size_t)p * 64 + lane], eps, lane,
-                   o0, o1);
-    if (j < G) {
-      qs[j][lane] = (f16)o0;
-      qs[j][lane + 64] = (f16)o1;
-    } else {
-      kc[(head_base + p) * 128 + lane] = (f16)o0;
-      kc[(head_base + p) * 128 + lane + 64] = (f16)o1;
-    }
-  }
-  __syncthreads();  // q in LDS; the new cache rows visible to the workgroup's loads
-  if (!early && key < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, end, lane);
-  half8 qa[4];
-  {
-    const int g = lane & 15, grp = lane >> 4;
-#pragma unroll
-    for (int s2 = 0; s2 < 4; s2++)
-      qa[s2] = g < G ? *(const half8 *)&qs[g][s2 * 32 + grp * 8] : half8_of(make_uint4(0, 0, 0, 0));
-  }
-  float acc[G][8], m[G], l[G];
-#pragma unroll
-  for (int g = 0; g < G; g++) {
-    m[g] = -__builtin_inff();
-    l[g] = 0.0f;
-#pragma unroll
-    for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
-  }
-  while (key < end) {
-    if (key + STEP < end) load_tile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + STEP, end, lane);
-    attend_tile<G, false>(ta, qa, key, end, scale_log2, lane, m, l, acc);
-    key += STEP;
-    if (key >= end) break;
-    if (key + STEP < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + STEP, end, lane);
-    attend_tile<G, false>(tb, qa, key, end, scale_log2, lane, m, l, acc);
-    key += STEP;
-  }
-#pragma unroll
-  for (int g = 0; g < G; g++)
-#pragma unroll
-    for (int d = 0; d < 8; d++) {
-      float a = acc[g][d];
-      a += __shfl_xor(a, 16, 64);
-      a += __shfl_xor(a, 32, 64);
-      acc[g][d] = a;
-    }
-  if (lane < 16) {
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-      for (int d = 0; d < 8; d++) sacc[wave][g][lane * 8 + d] = acc[g][d];
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      sm[wave][g] = m[g];
-      sl[wave][g] = l[g];
-    }
-  }
-  __syncthreads();
-  const size_t base = ((size_t)h * nchunk + c) * G;
-  for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
-    const uint32_t g = i / 128, d = i % 128;
-    float top = -__builtin_inff();
-#pragma unroll
-    for (int w = 0; w < W; w++) top = fmaxf(top, sm[w][g]);
-    float o = 0.0f, lsum = 0.0f;
-    if (top != -__builtin_inff()) {
-#pragma unroll
-      for (int w = 0; w < W; w++) {
-        const float wt = exp2f(sm[w][g] - top);
-        o += wt * sacc[w][g][d];
-        lsum += wt * sl[w][g];
-      }
-    }
-    ws_o[(base + g) * 128 + d] = o;
-    if (d == 0) {
-      ws_m[base + g] = top * kLn2;
-      ws_l[base + g] = lsum;
-    }
-  }
-}
-
 // The model's decode attention for the token at position p = *pos. NSPLIT workgroups of W waves a
 // kv head each take a contiguous share of the capacity; those whose share starts past p leave at
 // once. Prologue: q for the kv head's G query heads comes from the fp32 projection qkv (heads + 2 *
 // kvh rows of 128) through the per-head RMSNorm and RoPE; the workgroup whose share holds p (the
 // owner) also makes the new k (normed, rotated) and v, writes them to the caches at p for later
-// steps and keeps them in LDS: the tile holding p never reads row p from memory but takes it from
-// LDS, so the owner's keys wait on no store. Every workgroup merges its waves in LDS and leaves its
-// partial (o unnormalized, m in natural-log units, l) in the workspace; the last of the kv head's
-// live workgroups to arrive (a counter a kv head, a single thread's release and acquire fences)
-// merges them with the rule of the reference's Merge into out (fp16), one wave reduction a query
-// head over the partials (a lane a partial) with every partial's o already in flight, and clears
-// the counter for the next call.
+// steps and keeps them in LDS: the tile holding p replaces what its load of row p returned with the
+// LDS copy, so the owner's keys wait on no store. Every workgroup merges its waves in LDS and
+// leaves its partial (o unnormalized, m in natural-log units, l) in the workspace; the last of the
+// kv head's live workgroups to arrive (a counter a kv head, a single thread's release and acquire
+// fences) merges them with the rule of the reference's Merge into out (fp16), one wave reduction a
+// query head over the partials (a lane a partial) with every partial's o already in flight, and
+// clears the counter for the next call. LAST = false is the form for long caches: every workgroup
+// leaves its partial (an empty one past p) for k_attn_merge, with no counter.
+// A workspace store / load, device-coherent (past the XCD's L2) when COH.
+template <bool COH>
+__device__ __forceinline__ void ws_put(float *p, float v) {
+  if (COH)
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *p = v;
+}
+__device__ __forceinline__ float ws_get(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 constexpr uint32_t kHeadSplit = 64;  // most workgroups a kv head (a lane each in the merge)
 
 // Row p = key0 + j of a tile from LDS (k as the MFMA B operand layout, v as the P.V layout).
@@ -392,7 +314,7 @@ __device__ __forceinline__ void patch_row(Tile<false> &t, uint32_t j, const f16 
     if ((uint32_t)(4 * r + grp) == j) t.v[r] = *(const half8 *)&vn16[(lane & 15) * 8];
 }
 
-template <int G, int W>
+template <int G, int W, bool LAST>
 __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ qkv, const float *__restrict__ qn,
                                                       const float *__restrict__ kn, const float *__restrict__ cos_t,
                                                       const float *__restrict__ sin_t, double eps,
@@ -411,30 +333,47 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
   const uint32_t h = blockIdx.x / nsplit, c = blockIdx.x % nsplit;
   const uint32_t p = (uint32_t)*pos, len = p + 1;
   const uint32_t begin = c * chunk;
-  if (begin >= len) return;  // no keys in use here: no partial, no arrival
+  if (begin >= len) {  // no keys in use here: no partial, no arrival (LAST), else an empty partial
+    if (!LAST && threadIdx.x < G) {
+      const size_t slot = ((size_t)h * nsplit + c) * G + threadIdx.x;
+      ws_m[slot] = -__builtin_inff();
+      ws_l[slot] = 0.0f;
+    }
+    return;
+  }
   const bool owner = p - begin < chunk;  // the share holds p (begin <= p)
   const uint32_t end = owner ? len : begin + chunk;
-  const uint32_t lim = owner ? p : end;  // rows loaded from memory: row p comes from LDS
   const size_t head_base = (size_t)h * cap;
   constexpr uint32_t STEP = 16 * W;
-  Tile<false> ta, tb;
-  uint32_t key = begin + 16 * wave;
-  if (key < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, lim, lane);
+  // The prologue's loads go out first (wave j makes job j: query head j < G, then k, then v), then
+  // the wave's first two tiles (a share of up to 32*W keys in flight while q is made): loads
+  // complete in issue order for the wait counter, so q waits only on its own loads.
   const uint32_t jobs = owner ? G + 2 : G;
-  for (uint32_t j = wave; j < jobs; j += W) {
-    const uint32_t row = j < G ? h * G + j : j == G ? heads + h : heads + kvh + h;
-    const float x0 = qkv[(size_t)row * 128 + lane], x1 = qkv[(size_t)row * 128 + lane + 64];
-    if (j == G + 1) {
-      vnew[lane] = (f16)x0;
-      vnew[lane + 64] = (f16)x1;
-      vc[(head_base + p) * 128 + lane] = (f16)x0;
-      vc[(head_base + p) * 128 + lane + 64] = (f16)x1;
-      continue;
-    }
+  const uint32_t j0 = (uint32_t)wave < jobs ? (uint32_t)wave : jobs - 1;
+  auto job_row = [&](uint32_t j) { return j < G ? h * G + j : j == G ? heads + h : heads + kvh + h; };
+  const float *nwp = j0 < G ? qn : kn;
+  const float x0 = qkv[(size_t)job_row(j0) * 128 + lane], x1 = qkv[(size_t)job_row(j0) * 128 + lane + 64];
+  const float nw0 = nwp[lane], nw1 = nwp[lane + 64];
+  const float cp = cos_t[(size_t)p * 64 + lane], sp = sin_t[(size_t)p * 64 + lane];
+  issue_order();
+  Tile<false> ta, tb;
+  const uint32_t key = begin + 16 * wave;
+  // issued whether or not the wave has keys (past the cache end a load reads the last row): a
+  // load under a branch makes the wait counter assume the shorter path's count
+  load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, cap, lane);
+  load_tile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + STEP, cap, lane);
+  // every wave runs its job's arithmetic (a wave past the jobs repeats the last and stores
+  // nothing), so that no load above is moved into a branch below the tile loads
+  auto make_job = [&](uint32_t j, float a0, float a1, float w0, float w1, bool keep) {
     float o0, o1;
-    head_norm_rope(x0, x1, j < G ? qn : kn, cos_t[(size_t)p * 64 + lane], sin_t[(size_t)p * 64 + lane], eps, lane,
-                   o0, o1);
-    if (j < G) {
+    head_norm_rope(a0, a1, w0, w1, cp, sp, eps, o0, o1);
+    if (!keep) return;
+    if (j == G + 1) {
+      vnew[lane] = (f16)a0;
+      vnew[lane + 64] = (f16)a1;
+      vc[(head_base + p) * 128 + lane] = (f16)a0;
+      vc[(head_base + p) * 128 + lane + 64] = (f16)a1;
+    } else if (j < G) {
       qs[j][lane] = (f16)o0;
       qs[j][lane + 64] = (f16)o1;
     } else {
@@ -443,6 +382,12 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
       kc[(head_base + p) * 128 + lane] = (f16)o0;
       kc[(head_base + p) * 128 + lane + 64] = (f16)o1;
     }
+  };
+  make_job(j0, x0, x1, nw0, nw1, (uint32_t)wave < jobs);
+  for (uint32_t j = wave + W; j < jobs; j += W) {  // more jobs than waves (W < G + 2)
+    const float *nj = j < G ? qn : kn;
+    make_job(j, qkv[(size_t)job_row(j) * 128 + lane], qkv[(size_t)job_row(j) * 128 + lane + 64], nj[lane],
+             nj[lane + 64], true);
   }
   __syncthreads();  // q, and the owner's new k/v, in LDS
   half8 qa[4];
@@ -460,17 +405,12 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
 #pragma unroll
     for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
   }
-  while (key < end) {
-    if (key + STEP < end) load_tile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + STEP, lim, lane);
-    if (owner && p - key < 16) patch_row(ta, p - key, knew, vnew, lane);
-    attend_tile<G, false>(ta, qa, key, end, scale_log2, lane, m, l, acc);
-    key += STEP;
-    if (key >= end) break;
-    if (key + STEP < end) load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + STEP, lim, lane);
-    if (owner && p - key < 16) patch_row(tb, p - key, knew, vnew, lane);
-    attend_tile<G, false>(tb, qa, key, end, scale_log2, lane, m, l, acc);
-    key += STEP;
-  }
+  run_tiles<G, false, STEP>(
+      ta, tb, key, key < end ? (end - key + STEP - 1) / STEP : 0, end, qa, scale_log2, lane, m, l, acc,
+      [&](Tile<false> &t, uint32_t k0) { load_tile<false>(t, kc, vc, nullptr, nullptr, head_base, k0, cap, lane); },
+      [&](Tile<false> &t, uint32_t k0) {
+        if (owner && p - k0 < 16) patch_row(t, p - k0, knew, vnew, lane);
+      });
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
@@ -509,39 +449,48 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
         lsum += wt * sl[w][g];
       }
     }
-    if (nsplit == 1) {
-      out[(size_t)(h * G + g) * 128 + d] = (f16)(lsum > 0.0f ? o / lsum : 0.0f);
+    if (LAST && nsplit == 1) {
+      out[(size_t)(h * G + g) * 128 + d] = (f16)f32_value(lsum > 0.0f ? o / lsum : 0.0f);
     } else {
-      ws_o[(base + g) * 128 + d] = o;
+      // LAST: the partials are stored coherent at device scope (past the XCD's L2), so that the
+      // last workgroup reads them with no L2 write-back on the writer's side
+      ws_put<LAST>(&ws_o[(base + g) * 128 + d], o);
       if (d == 0) {
-        ws_m[base + g] = top * kLn2;
-        ws_l[base + g] = lsum;
+        ws_put<LAST>(&ws_m[base + g], top * kLn2);
+        ws_put<LAST>(&ws_l[base + g], lsum);
       }
     }
   }
-  if (nsplit == 1) return;
+  if (!LAST || nsplit == 1) return;
   const uint32_t live = p / chunk + 1;  // workgroups of this kv head that hold keys
-  __syncthreads();  // the workgroup's partial is written (every wave's stores complete)
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const bool lst = __hip_atomic_fetch_add(&counters[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == live - 1;
-    if (lst) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    last = lst;
-  }
+  // Every wave waits for its partial's stores to be acknowledged (device-coherent stores: then
+  // visible to every CU); after the barrier one thread counts the workgroup in. The counter is a
+  // device-scope atomic; the last arrival's reads are device-coherent loads, which see the
+  // acknowledged stores without an L2 invalidate.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(&counters[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == live - 1;
   __syncthreads();
   if (!last) return;
   // A wave's 64 outputs share one query head g0: lane cc holds partial cc's m and l, and the wave's
-  // outputs load every partial's o (U at a time) while the weights exp(m - top) are reduced.
+  // outputs load every partial's o (U at a time, a partial past the live ones reading the last
+  // live one, weighted 0) while the weights exp(m - top) are reduced.
   const size_t b0 = (size_t)h * nsplit * G;
   constexpr uint32_t U = 16;
+  const uint32_t lastc = live - 1;
   for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
     const uint32_t g0 = i / 128, d0 = i % 128;
     float ov[U];
 #pragma unroll
-    for (uint32_t u = 0; u < U; u++) ov[u] = u < live ? ws_o[(b0 + u * G + g0) * 128 + d0] : 0.0f;
+    for (uint32_t u = 0; u < U; u++) ov[u] = ws_get(&ws_o[(b0 + min(u, lastc) * G + g0) * 128 + d0]);
+    const uint32_t cl = min((uint32_t)lane, lastc);
     const bool mine = (uint32_t)lane < live;
-    const float mc = mine ? ws_m[b0 + lane * G + g0] : -__builtin_inff();
-    const float lc = mine ? ws_l[b0 + lane * G + g0] : 0.0f;
+    float mc = ws_get(&ws_m[b0 + cl * G + g0]), lc = ws_get(&ws_l[b0 + cl * G + g0]);
+    if (!mine) {
+      mc = -__builtin_inff();
+      lc = 0.0f;
+    }
     const float top = wave_max(lc > 0.0f ? mc : -__builtin_inff());
     const float wc = (lc > 0.0f && top != -__builtin_inff()) ? expf(mc - top) : 0.0f;
     const float den = group_sum<64>(wc * lc);
@@ -550,13 +499,13 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
     for (uint32_t u = 0; u < U; u++) num += __shfl(wc, u, 64) * ov[u];
     for (uint32_t cc = U; cc < live; cc += U) {
 #pragma unroll
-      for (uint32_t u = 0; u < U; u++) ov[u] = cc + u < live ? ws_o[(b0 + (cc + u) * G + g0) * 128 + d0] : 0.0f;
+      for (uint32_t u = 0; u < U; u++) ov[u] = ws_get(&ws_o[(b0 + min(cc + u, lastc) * G + g0) * 128 + d0]);
 #pragma unroll
       for (uint32_t u = 0; u < U; u++) num += __shfl(wc, (cc + u) & 63, 64) * ov[u];
     }
-    out[(size_t)(h * G + g0) * 128 + d0] = (f16)(den > 0.0f ? num / den : 0.0f);
+    out[(size_t)(h * G + g0) * 128 + d0] = (f16)f32_value(den > 0.0f ? num / den : 0.0f);
   }
-  if (threadIdx.x == 0) counters[h] = 0;
+  if (threadIdx.x == 0) __hip_atomic_store(&counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Merge of chunks (the reference's Merge rule, paged.go:252-310): top = the largest m among
@@ -750,7 +699,8 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
 
 
 // Tuning knobs read once a process: HWK_ATTN_KEYS, the keys a workgroup takes at the cache's capacity
-// (default 256); HWK_ATTN_W, waves a workgroup (2, 4, 8 or 16; default 8).
+// (default 128); HWK_ATTN_W, waves a workgroup (2, 4, 8 or 16; default 4). The defaults are the
+// fastest decode step of the 28-layer model at 1,040-1,290 positions (swept 32-256 keys, 2-8 waves).
 static int attn_env(const char *name, int dflt) {
   const char *v = getenv(name);
   return v ? atoi(v) : dflt;
@@ -758,7 +708,7 @@ static int attn_env(const char *name, int dflt) {
 
 static uint32_t attn_keys() {
   static uint32_t k = [] {
-    const int v = attn_env("HWK_ATTN_KEYS", 256);
+    const int v = attn_env("HWK_ATTN_KEYS", 128);
     return (uint32_t)(v < 16 ? 16 : v > 65536 ? 65536 : v);
   }();
   return k;
@@ -766,8 +716,8 @@ static uint32_t attn_keys() {
 
 static int attn_waves() {
   static int w = [] {
-    const int v = attn_env("HWK_ATTN_W", 8);
-    return v == 2 || v == 4 || v == 16 ? v : 8;
+    const int v = attn_env("HWK_ATTN_W", 4);
+    return v == 2 || v == 8 || v == 16 ? v : 4;
   }();
   return w;
 }
@@ -796,15 +746,16 @@ char *hwk::attn_head(hipStream_t st, const float *qkv, const float *qn, const fl
   float *ws_o = (float *)workspace, *ws_m = ws_o + slots * 128, *ws_l = ws_m + slots;
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
 #define HWK_AH(GG, W)                                                                                             \
-  hipLaunchKernelGGL((k_attn_head<GG, W>), dim3(p->kv_heads * nsplit), dim3(64 * W), 0, st, qkv, qn, kn, cos_t,  \
-                     sin_t, eps, (f16 *)kc, (f16 *)vc, (f16 *)out, ws_o, ws_m, ws_l, counters, pos, p->heads,     \
+  hipLaunchKernelGGL((k_attn_head<GG, W, true>), dim3(p->kv_heads * nsplit), dim3(64 * W), 0, st, qkv, qn, kn,     \
+                     cos_t, sin_t, eps, (f16 *)kc, (f16 *)vc, (f16 *)out, ws_o, ws_m, ws_l, counters, pos,        \
+                     p->heads,                                                                                    \
                      p->kv_heads, p->capacity, chunk, nsplit, scale_log2)
 #define HWK_AHW(GG)                  \
   switch (attn_waves()) {            \
     case 2: HWK_AH(GG, 2); break;    \
-    case 4: HWK_AH(GG, 4); break;    \
+    case 8: HWK_AH(GG, 8); break;    \
     case 16: HWK_AH(GG, 16); break;  \
-    default: HWK_AH(GG, 8); break;   \
+    default: HWK_AH(GG, 4); break;   \
   }
   if (G == 1) {
     HWK_AHW(1)
@@ -847,9 +798,9 @@ char *hwk::attn_decode_step(hipStream_t st, const float *qkv, const float *qn, c
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
   constexpr int W = 8;
 #define HWK_STEP(GG)                                                                                               \
-  hipLaunchKernelGGL((k_attn_step<GG, W>), dim3(p->kv_heads * nchunk), dim3(64 * W), 0, st, qkv, qn, kn, cos_t,   \
-                     sin_t, eps, (f16 *)kc, (f16 *)vc, ws_o, ws_m, ws_l, pos, p->heads, p->kv_heads, p->capacity,  \
-                     chunk, nchunk, scale_log2)
+  hipLaunchKernelGGL((k_attn_head<GG, W, false>), dim3(p->kv_heads * nchunk), dim3(64 * W), 0, st, qkv, qn, kn,   \
+                     cos_t, sin_t, eps, (f16 *)kc, (f16 *)vc, nullptr, ws_o, ws_m, ws_l, nullptr, pos, p->heads,    \
+                     p->kv_heads, p->capacity, chunk, nchunk, scale_log2)
   if (G == 1) HWK_STEP(1);
   else if (G == 2) HWK_STEP(2);
   else HWK_STEP(4);

@@ -108,6 +108,11 @@ __device__ __forceinline__ float f32_value(float v) {
   return v;
 }
 
+// A scheduling barrier: the instruction scheduler moves nothing across it, so loads written before
+// it are issued before those written after it (no wait is implied: the wait counter still waits
+// only where a value is used).
+__device__ __forceinline__ void issue_order() { __builtin_amdgcn_sched_barrier(0); }
+
 // Store one GEMV/GEMM output per out_mode.
 __device__ __forceinline__ void store_out(void *y, size_t i, float v, int mode) {
   if (mode == HWK_OUT_F16)

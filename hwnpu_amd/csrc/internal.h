@@ -61,14 +61,14 @@ char *attn_merge_ws(hipStream_t st, const void *workspace, void *out, const hwk_
 // with r = float(1 / sqrt(mean(x^2) + eps)) (mean in float64), then x*cos + rotate_half(x)*sin
 // with the position's float32 tables (rotate_half = cat(-x2, x1); reference internal/llm/blocks/
 // blocks.go:427-445), each product and sum rounded on its own.
-__device__ __forceinline__ void head_norm_rope(float x0, float x1, const float *__restrict__ nw, float c, float s,
-                                               double eps, int l, float &o0, float &o1) {
+__device__ __forceinline__ void head_norm_rope(float x0, float x1, float nw0, float nw1, float c, float s,
+                                               double eps, float &o0, float &o1) {
 #pragma clang fp contract(off)
   double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
   const float r = (float)(1.0 / sqrt(ss / 128.0 + eps));
-  const float y0 = (x0 * r) * nw[l], y1 = (x1 * r) * nw[l + 64];
+  const float y0 = (x0 * r) * nw0, y1 = (x1 * r) * nw1;
   o0 = f32_value(y0 * c + (-y1) * s);  // j < half: x*cos + (-x[j+half])*sin
   o1 = f32_value(y1 * c + y0 * s);     // j >= half: x*cos + x[j-half]*sin
 }

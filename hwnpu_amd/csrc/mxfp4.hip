@@ -104,22 +104,26 @@ template <int LPR, int BPL, int RPW>
 __device__ __forceinline__ void load_rowset(RowSet<BPL, RPW> &rs, const uint4 *__restrict__ w,
                                             const uint8_t *__restrict__ e, uint32_t row0, uint32_t n,
                                             uint32_t nb, int l) {
+  // Every load is issued, rows past n and blocks past nb reading the last row / block instead
+  // (callers drop those rows and zero those blocks' terms): a predicated load would make the
+  // compiler wait for it before issuing the next one.
   constexpr int RS = 64 / LPR;
 #pragma unroll
   for (int i = 0; i < RPW; i++) {
 #pragma unroll
     for (int j = 0; j < BPL; j++) {
-      const uint32_t r = row0 + i * RS, b = j * LPR + l;
-      if (r < n && b < nb) {
-        const size_t blk = (size_t)r * nb + b;
-        rs.c[i][j] = load_stream(&w[blk]);
-        rs.s[i][j] = e[blk];
-      } else {
-        rs.c[i][j] = make_uint4(0, 0, 0, 0);
-        rs.s[i][j] = 0;
-      }
+      const uint32_t r = min(row0 + i * RS, n - 1), b = min((uint32_t)(j * LPR + l), nb - 1);
+      const size_t blk = (size_t)r * nb + b;
+      rs.c[i][j] = load_stream(&w[blk]);
+      rs.s[i][j] = e[blk];
     }
   }
+}
+
+// A block's term of a row's dot product: its fp32 sum times the block scale; zero for a lane's
+// block past the row's end (its codes and x are copies of the last block's).
+__device__ __forceinline__ float block_term(float d0, float d1, uint32_t s, bool in_row) {
+  return in_row ? (d0 + d1) * e8m0_scale(s) : 0.0f;
 }
 
 // The single-pass GEMV over a grid sized to the device: a wave loads x once, then walks row sets
@@ -142,9 +146,9 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_stream(const uint4 *__restri
   uint4 xr[BPL][4];
 #pragma unroll
   for (int j = 0; j < BPL; j++) {
-    const uint32_t b = j * LPR + l;
+    const uint32_t b = min((uint32_t)(j * LPR + l), nb - 1);
 #pragma unroll
-    for (int q = 0; q < 4; q++) xr[j][q] = b < nb ? x[(size_t)b * 4 + q] : make_uint4(0, 0, 0, 0);
+    for (int q = 0; q < 4; q++) xr[j][q] = x[(size_t)b * 4 + q];
   }
   for (;;) {
     const uint32_t next = set + waves;
@@ -163,7 +167,7 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_stream(const uint4 *__restri
           d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<2>(cw[q]), h2_of_bits(xr[j][q].z), d0, false);
           d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<3>(cw[q]), h2_of_bits(xr[j][q].w), d1, false);
         }
-        acc += (d0 + d1) * e8m0_scale(cur.s[i][j]);
+        acc += block_term(d0, d1, cur.s[i][j], (uint32_t)(j * LPR + l) < nb);
       }
       const float v = group_sum<LPR>(acc);
       const uint32_t r = set * ROWS + sub + i * RS;
@@ -213,19 +217,27 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   uint32_t set = blockIdx.x * WPB + (t >> 6);
   const uint32_t sets = (n + ROWS - 1) / ROWS;
   const bool live = set < sets;
-  // the first row set's loads go out before x is made, so that they overlap its latency
-  RowSet<BPL, RPW> cur, nxt;
-  if (live) load_rowset<64, BPL, RPW>(cur, w, e, set * ROWS, n, nb, lane);
-  f16 *xh = (f16 *)xs;
+  // x's inputs are loaded first, then the first row set's weights (a wave past the last set loads
+  // that one again and leaves), so that x is made while the weights are in flight: the loads
+  // complete in issue order for the wait counter
+  float hv[PER], wv[PER];
   if constexpr (XM == X_NORM) {
-    float hv[PER], wv[PER];
-    double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < PER; j++) {
-      const uint32_t i = t + j * NT;
-      hv[j] = i < k ? in.h[i] : 0.0f;
-      wv[j] = i < k ? in.nw[i] : 0.0f;
+      const uint32_t i = min((uint32_t)(t + j * NT), k - 1);
+      hv[j] = in.h[i];
+      wv[j] = in.nw[i];
     }
+  }
+  issue_order();
+  RowSet<BPL, RPW> cur, nxt;
+  load_rowset<64, BPL, RPW>(cur, w, e, (live ? set : sets - 1) * ROWS, n, nb, lane);
+  f16 *xh = (f16 *)xs;
+  if constexpr (XM == X_NORM) {
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; j++)
+      if (t + j * NT >= k) hv[j] = 0.0f;
 #pragma unroll
     for (int j = 0; j < PER; j++) ss += (double)hv[j] * (double)hv[j];
     ss = wave_sum_f64(ss);
@@ -268,7 +280,7 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
           d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<2>(cw[q]), h2_of_bits(xr[j][q].z), d0, false);
           d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<3>(cw[q]), h2_of_bits(xr[j][q].w), d1, false);
         }
-        acc += (d0 + d1) * e8m0_scale(cur.s[i][j]);
+        acc += block_term(d0, d1, cur.s[i][j], (uint32_t)(j * 64 + lane) < nb);
       }
       v[i] = group_sum<64>(acc);
     }
@@ -342,7 +354,7 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_rows(const uint4 *__restrict
             d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<2>(cw[q]), h2_of_bits(xr[q].z), d0, false);
             d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<3>(cw[q]), h2_of_bits(xr[q].w), d1, false);
           }
-          acc[i][v] += (d0 + d1) * e8m0_scale(cur.s[i][j]);
+          acc[i][v] += block_term(d0, d1, cur.s[i][j], true);
         }
       }
     }

@@ -68,7 +68,8 @@ __global__ __launch_bounds__(256) void k_qk_rope(const float *__restrict__ qkv, 
     return;
   }
   float o0, o1;
-  head_norm_rope(x0, x1, slot < heads ? qn : kn, cos_t[(size_t)p * 64 + l], sin_t[(size_t)p * 64 + l], eps, l, o0, o1);
+  const float *nw = slot < heads ? qn : kn;
+  head_norm_rope(x0, x1, nw[l], nw[l + 64], cos_t[(size_t)p * 64 + l], sin_t[(size_t)p * 64 + l], eps, o0, o1);
   f16 *dst = slot < heads ? q16 + ((size_t)t * heads + slot) * 128
                           : kc + ((size_t)(slot - heads) * cap + p) * 128;
   dst[l] = (f16)o0;
