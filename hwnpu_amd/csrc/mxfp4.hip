@@ -126,6 +126,20 @@ __device__ __forceinline__ float block_term(float d0, float d1, uint32_t s, bool
   return in_row ? (d0 + d1) * e8m0_scale(s) : 0.0f;
 }
 
+// The rows' old y values of an ADD-mode call (a non-ADD call reads x there instead, never used):
+// loaded before the weights so that the sum at the end waits on no load.
+template <int RPW>
+struct YOld {
+  float v[RPW];
+};
+template <int RPW, int RS>
+__device__ __forceinline__ void y_prefetch(bool add, const void *y, const uint4 *x, uint32_t r0, uint32_t n,
+                                           YOld<RPW> &yo) {
+#pragma unroll
+  for (int i = 0; i < RPW; i++)
+    yo.v[i] = add ? ((const float *)y)[min(r0 + i * RS, n - 1)] : ((const float *)x)[i & 1];
+}
+
 // The single-pass GEMV over a grid sized to the device: a wave loads x once, then walks row sets
 // wave_count apart, issuing the next set's loads before it computes the current one, so that
 // every lane keeps 2*RPW*BPL 16-byte loads in flight while the grid streams the matrix.
@@ -141,6 +155,9 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_stream(const uint4 *__restri
   uint32_t set = blockIdx.x * 4 + (threadIdx.x >> 6);
   const uint32_t sets = (n + ROWS - 1) / ROWS;
   if (set >= sets) return;
+  const bool add = mode == HWK_OUT_ADD_F32;
+  YOld<RPW> yo, yn;
+  y_prefetch<RPW, RS>(add, y, x, set * ROWS + sub, n, yo);
   RowSet<BPL, RPW> cur, nxt;
   load_rowset<LPR, BPL, RPW>(cur, w, e, set * ROWS + sub, n, nb, l);
   uint4 xr[BPL][4];
@@ -152,7 +169,10 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_stream(const uint4 *__restri
   }
   for (;;) {
     const uint32_t next = set + waves;
-    if (next < sets) load_rowset<LPR, BPL, RPW>(nxt, w, e, next * ROWS + sub, n, nb, l);
+    if (next < sets) {
+      y_prefetch<RPW, RS>(add, y, x, next * ROWS + sub, n, yn);
+      load_rowset<LPR, BPL, RPW>(nxt, w, e, next * ROWS + sub, n, nb, l);
+    }
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
       float acc = 0.0f;
@@ -171,11 +191,17 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_stream(const uint4 *__restri
       }
       const float v = group_sum<LPR>(acc);
       const uint32_t r = set * ROWS + sub + i * RS;
-      if (l == 0 && r < n) store_out(y, r, v, mode);
+      if (l == 0 && r < n) {
+        if (add)
+          ((float *)y)[r] = yo.v[i] + v;
+        else
+          store_out(y, r, v, mode);
+      }
     }
     if (next >= sets) break;
     set = next;
     cur = nxt;
+    yo = yn;
   }
 }
 

@@ -88,6 +88,7 @@ __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, f1
 __global__ void k_set_i32(int32_t *__restrict__ p, int32_t v) { *p = v; }
 
 constexpr uint32_t kArgBlocks = 64;
+constexpr int kArgPer = 10;  // values a thread takes a pass (151,936 logits: one pass)
 
 __device__ __forceinline__ void better(float &bv, uint32_t &bi, float v, uint32_t i) {
   if (v > bv || (v == bv && i < bi)) {
@@ -103,37 +104,55 @@ __device__ __forceinline__ void better(float &bv, uint32_t &bi, float v, uint32_
 __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uint32_t n, float *__restrict__ part_v,
                                                 uint32_t *__restrict__ part_i, uint32_t *__restrict__ counter,
                                                 int32_t *__restrict__ hist, int32_t *__restrict__ pos) {
-  __shared__ float sv[256];
-  __shared__ uint32_t si[256];
+  __shared__ float sv[4];
+  __shared__ uint32_t si[4];
   __shared__ bool last;
   const uint32_t t = threadIdx.x;
   const uint32_t per = (n + kArgBlocks - 1) / kArgBlocks;
   const uint32_t lo = blockIdx.x * per, hi = lo + per < n ? lo + per : n;
   float bv = -__builtin_inff();
   uint32_t bi = 0xffffffffu;
-  for (uint32_t i = lo + t; i < hi; i += 256) better(bv, bi, x[i], i);
-  sv[t] = bv;
-  si[t] = bi;
-  __syncthreads();
-  for (uint32_t s = 128; s > 0; s >>= 1) {
-    if (t < s) better(sv[t], si[t], sv[t + s], si[t + s]);
-    __syncthreads();
+  // kArgPer values a thread, all loads issued at once (a slot past hi reads an in-range value and
+  // is skipped)
+  for (uint32_t base = lo; base < hi; base += kArgPer * 256) {
+    float v[kArgPer];
+#pragma unroll
+    for (int j = 0; j < kArgPer; j++) v[j] = x[min(base + t + j * 256, hi - 1)];
+#pragma unroll
+    for (int j = 0; j < kArgPer; j++)
+      if (base + t + j * 256 < hi) better(bv, bi, v[j], base + t + j * 256);
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const uint32_t oi = __shfl_xor(bi, off, 64);
+    better(bv, bi, ov, oi);
+  }
+  if ((t & 63) == 0) {
+    sv[t >> 6] = bv;
+    si[t >> 6] = bi;
+  }
+  __syncthreads();
+  // the partial is stored device-coherent and acknowledged before the block counts itself in; the
+  // last block reads the partials with device-coherent loads (no L2 write-back or invalidate)
   if (t == 0) {
-    part_v[blockIdx.x] = sv[0];
-    part_i[blockIdx.x] = si[0];
-    __threadfence();
-    last = atomicAdd(counter, 1u) == gridDim.x - 1;
+    for (int w = 1; w < 4; w++) better(bv, bi, sv[w], si[w]);
+    __hip_atomic_store(&part_v[blockIdx.x], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&part_i[blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
   if (t < 64) {
-    float v = -__builtin_inff();
-    uint32_t i = 0xffffffffu;
-    if (t < gridDim.x) {
-      v = __builtin_nontemporal_load(&part_v[t]);
-      i = __builtin_nontemporal_load(&part_i[t]);
+    const uint32_t c = t < gridDim.x ? t : gridDim.x - 1;
+    float v = __hip_atomic_load(&part_v[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t i = __hip_atomic_load(&part_i[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int32_t p = *pos;
+    const float x0 = x[0];  // a NaN at index 0 is kept: strict > never replaces it
+    if (t >= gridDim.x) {
+      v = -__builtin_inff();
+      i = 0xffffffffu;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -142,11 +161,9 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uin
       better(v, i, ov, oi);
     }
     if (t == 0) {
-      const int32_t p = *pos;
-      const float x0 = x[0];  // a NaN at index 0 is kept: strict > never replaces it
       hist[p + 1] = (int32_t)((i == 0xffffffffu || x0 != x0) ? 0 : i);
       *pos = p + 1;
-      *counter = 0;
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
