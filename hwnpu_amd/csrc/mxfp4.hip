@@ -514,16 +514,19 @@ __global__ void k_synth_mxfp4(uint8_t *__restrict__ w, uint8_t *__restrict__ e, 
 }
 
 // Tuning knobs read once per process: HWK_MXFP4_RPW (row sets of 1, 2, 4 or 8 rows a lane group;
-// default 2) and HWK_GEMV_WPC (resident waves a CU the streaming grid is sized for; default 24).
+// default 0: 1 for matrices of fewer rows than half the streaming grid's waves, else 2) and
+// HWK_GEMV_WPC (resident waves a CU the streaming grid is sized for; default 16). The defaults are
+// the fastest decode step of the 28-layer model (2048-row o_proj/down take 1 row a wave) with the
+// 8192-row GEMV of the roofline unchanged (2 rows a wave).
 int env_int(const char *name, int dflt) {
   const char *s = getenv(name);
   return s ? atoi(s) : dflt;
 }
 
-int gemv_rpw() {
+int gemv_rpw_env() {
   static int v = [] {
-    int r = env_int("HWK_MXFP4_RPW", 2);
-    return (r == 1 || r == 2 || r == 4 || r == 8) ? r : 2;
+    int r = env_int("HWK_MXFP4_RPW", 0);
+    return (r == 1 || r == 2 || r == 4 || r == 8) ? r : 0;
   }();
   return v;
 }
@@ -531,7 +534,7 @@ int gemv_rpw() {
 // Waves the streaming grid runs: resident waves per CU times the current device's CUs.
 uint32_t stream_waves() {
   static int wpc = [] {
-    int v = env_int("HWK_GEMV_WPC", 24);
+    int v = env_int("HWK_GEMV_WPC", 16);
     return v < 1 ? 1 : v > 32 ? 32 : v;
   }();
   int dev = 0, cus = 256;
@@ -557,7 +560,9 @@ void launch_gemv(hipStream_t st, const void *w, const void *e, const void *x, vo
 template <int LPR, int BPL>
 void launch_rpw(hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n, uint32_t nb,
                 int mode) {
-  switch (gemv_rpw()) {
+  int rpw = gemv_rpw_env();
+  if (!rpw) rpw = (n + 1) / 2 < stream_waves() / 2 ? 1 : 2;
+  switch (rpw) {
     case 1: launch_gemv<LPR, BPL, 1>(st, w, e, x, y, n, nb, mode); break;
     case 4: launch_gemv<LPR, BPL, 4>(st, w, e, x, y, n, nb, mode); break;
     case 8: launch_gemv<LPR, BPL, 8>(st, w, e, x, y, n, nb, mode); break;
@@ -717,10 +722,18 @@ int gemvx_wpb() {
   return v;
 }
 
-template <int BPL, int XM, bool SWIGLU, int WPB>
+// HWK_GEMVX_RPW: rows a wave takes a pass (2 or 4; default 2).
+int gemvx_rpw() {
+  static int v = [] {
+    const int r = env_int("HWK_GEMVX_RPW", 2);
+    return r == 4 ? 4 : 2;
+  }();
+  return v;
+}
+
+template <int BPL, int XM, bool SWIGLU, int WPB, int RPW>
 void launch_x_w(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb,
                 int mode) {
-  constexpr int RPW = 2;
   const uint32_t sets = (n + RPW - 1) / RPW;
   const uint32_t waves = sets < stream_waves() ? sets : stream_waves();
   hipLaunchKernelGGL((k_mxfp4_gemv_x<BPL, RPW, XM, SWIGLU, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0,
@@ -729,10 +742,20 @@ void launch_x_w(hipStream_t st, const void *w, const void *e, const XIn &in, voi
 
 template <int BPL, int XM, bool SWIGLU>
 void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb, int mode) {
+  const bool r4 = gemvx_rpw() == 4;
   switch (gemvx_wpb()) {
-    case 4: launch_x_w<BPL, XM, SWIGLU, 4>(st, w, e, in, y, n, nb, mode); break;
-    case 16: launch_x_w<BPL, XM, SWIGLU, 16>(st, w, e, in, y, n, nb, mode); break;
-    default: launch_x_w<BPL, XM, SWIGLU, 8>(st, w, e, in, y, n, nb, mode); break;
+    case 4:
+      r4 ? launch_x_w<BPL, XM, SWIGLU, 4, 4>(st, w, e, in, y, n, nb, mode)
+         : launch_x_w<BPL, XM, SWIGLU, 4, 2>(st, w, e, in, y, n, nb, mode);
+      break;
+    case 16:
+      r4 ? launch_x_w<BPL, XM, SWIGLU, 16, 4>(st, w, e, in, y, n, nb, mode)
+         : launch_x_w<BPL, XM, SWIGLU, 16, 2>(st, w, e, in, y, n, nb, mode);
+      break;
+    default:
+      r4 ? launch_x_w<BPL, XM, SWIGLU, 8, 4>(st, w, e, in, y, n, nb, mode)
+         : launch_x_w<BPL, XM, SWIGLU, 8, 2>(st, w, e, in, y, n, nb, mode);
+      break;
   }
 }
 

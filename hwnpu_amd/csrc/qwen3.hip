@@ -221,8 +221,10 @@ struct hwk_qwen3 {
   uint32_t host_pos = 0;  // mirror of *pos: where the next step writes
   bool started = false;
   hipStream_t cap = nullptr;
-  hipGraphExec_t exec = nullptr;
-  hipGraph_t graph = nullptr;
+  // the decode step captured once as a graph of one step and one of kGraphSteps steps (a step
+  // reads its token and position on the device and advances them, so consecutive replays chain)
+  hipGraphExec_t exec[2] = {nullptr, nullptr};
+  hipGraph_t graph[2] = {nullptr, nullptr};
 };
 
 namespace {
@@ -291,6 +293,12 @@ void layout(hwk_qwen3 *m, uint8_t *base) {
     if (char *e_ = (call)) return e_; \
   } while (0)
 
+// Steps a replay of the long graph runs: the gap between graph launches is paid once for them.
+constexpr uint32_t kGraphSteps = 8;
+
+// Captures graph slot i (n decode steps) on the model's private stream the first time it is needed.
+char *capture(hwk_qwen3 *m, int i, uint32_t n);
+
 // The decode step on stream st: the token hist[*pos] at position *pos.
 char *step(hwk_qwen3 *m, hipStream_t st) {
   const hwk_qwen3_config &c = m->c;
@@ -318,6 +326,23 @@ char *step(hwk_qwen3 *m, hipStream_t st) {
   hipLaunchKernelGGL(k_argmax, dim3(kArgBlocks), dim3(256), 0, st, m->logits, c.vocab, m->part_v, m->part_i,
                      m->counter, m->hist, m->pos);
   return hwk::launched("qwen3 argmax");
+}
+
+char *capture(hwk_qwen3 *m, int i, uint32_t n) {
+  if (m->exec[i]) return nullptr;
+  HWK_TRY("hipStreamBeginCapture", hipStreamBeginCapture(m->cap, hipStreamCaptureModeRelaxed));
+  char *err = nullptr;
+  for (uint32_t s = 0; s < n && !err; s++) err = step(m, m->cap);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(m->cap, &g);
+  if (err) {
+    if (g) (void)hipGraphDestroy(g);
+    return err;
+  }
+  if (e != hipSuccess) return hwk::hip_err("hipStreamEndCapture", e);
+  m->graph[i] = g;
+  HWK_TRY("hipGraphInstantiate", hipGraphInstantiate(&m->exec[i], g, nullptr, nullptr, 0));
+  return nullptr;
 }
 
 // Rows [0, T) of a prompt piece at positions start .. start+T-1, whose tokens are in hist.
@@ -428,8 +453,10 @@ HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
 
 HWK_API void hwk_qwen3_free(hwk_qwen3 *m) {
   if (!m) return;
-  if (m->exec) (void)hipGraphExecDestroy(m->exec);
-  if (m->graph) (void)hipGraphDestroy(m->graph);
+  for (int i = 0; i < 2; i++) {
+    if (m->exec[i]) (void)hipGraphExecDestroy(m->exec[i]);
+    if (m->graph[i]) (void)hipGraphDestroy(m->graph[i]);
+  }
   if (m->cap) (void)hipStreamDestroy(m->cap);
   if (m->base) {
     (void)hipDeviceSynchronize();
@@ -548,20 +575,11 @@ HWK_API char *hwk_qwen3_decode(hwk_qwen3 *m, void *stream, uint32_t steps) {
   HWK_CHECK(m->started, "hwk_qwen3_decode: no prompt yet");
   HWK_CHECK((uint64_t)m->host_pos + steps < m->c.max_ctx, "hwk_qwen3_decode: %u steps from %u pass %u", steps,
             m->host_pos, m->c.max_ctx);
-  if (!m->exec) {
-    HWK_TRY("hipStreamBeginCapture", hipStreamBeginCapture(m->cap, hipStreamCaptureModeRelaxed));
-    char *err = step(m, m->cap);
-    hipGraph_t g = nullptr;
-    hipError_t e = hipStreamEndCapture(m->cap, &g);
-    if (err) {
-      if (g) (void)hipGraphDestroy(g);
-      return err;
-    }
-    if (e != hipSuccess) return hwk::hip_err("hipStreamEndCapture", e);
-    m->graph = g;
-    HWK_TRY("hipGraphInstantiate", hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
-  }
-  for (uint32_t i = 0; i < steps; i++) HWK_TRY("hipGraphLaunch", hipGraphLaunch(m->exec, (hipStream_t)stream));
+  const uint32_t many = steps / kGraphSteps, one = steps % kGraphSteps;
+  if (many) HWK_Q(capture(m, 1, kGraphSteps));
+  if (one) HWK_Q(capture(m, 0, 1));
+  for (uint32_t i = 0; i < many; i++) HWK_TRY("hipGraphLaunch", hipGraphLaunch(m->exec[1], (hipStream_t)stream));
+  for (uint32_t i = 0; i < one; i++) HWK_TRY("hipGraphLaunch", hipGraphLaunch(m->exec[0], (hipStream_t)stream));
   m->host_pos += steps;
   return nullptr;
 }
