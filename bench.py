@@ -6,16 +6,21 @@ Prints one JSON line.
 
 decode (the default, BASELINE's headline): the 28-layer synthetic Qwen3 (hidden 2048, 16/8 heads,
 head_dim 128, SwiGLU 6144, vocab 151936, tied fp16 embeddings, MXFP4 linears of std-0.02 weights,
-seed 0) on one GPU. A 1024-token prompt (ids uniform over the vocabulary) is prefilled, then W
-greedy decode steps run untimed and K timed, each step one replay of the captured step graph
-(W + K = 256 by default). value = K / the timed region's seconds (HIP events on the replay
-stream): decode tokens per second at batch 1. The prefill rate is reported beside it.
+seed 0) on one GPU. A 1024-token prompt (ids uniform over the vocabulary) is prefilled, then 256
+tokens are greedy-decoded, each step one replay of a step graph; both step graphs are captured
+before any timing. The first 256 - K steps (at least W) run untimed and the last K are timed
+(decode_tokens grows past 256 only when K + W exceed it). value = K / the timed region's seconds
+(HIP events on the replay stream): decode tokens per second at batch 1. The prefill rate is
+reported beside it.
 
 roofline: the batch-1 MXFP4 GEMV of the GEMV configuration (W 8192 x 2048 MXFP4, x fp16, y fp16),
 the decode step's dominant kernel kind: 64 back-to-back GEMVs over 64 distinct weight copies (572
 MB, past the 256 MB MALL) in one HIP graph, timed with HIP events on the replay stream; achieved =
 8,933,376 algorithmic bytes a launch (codes 8,388,608 + scales 524,288 + x 4,096 + y 16,384) over
-the average launch time.
+the average launch time. traffic: HBM bytes a launch moves, measured each run by four child
+processes under `rocprofv3 --pmc` (FETCH_SIZE, WRITE_SIZE of the GEMV dispatches, each scaled by the
+counter's reading of a plain device copy of the same bytes) before this process touches the GPU;
+null, with the reason, when rocprofv3 is unavailable.
 
 gemv: only that GEMV measurement. copy: a plain device copy of the same 8,933,376 bytes timed the
 same way (the calibration run for the FETCH_SIZE / WRITE_SIZE counters).
@@ -63,10 +68,8 @@ KV_POS_BYTES = 28 * 2 * 8 * 128 * 2
 GEMV_N, GEMV_K = 8192, 2048
 GEMV_BYTES = GEMV_N * GEMV_K // 2 + GEMV_N * GEMV_K // 32 + GEMV_K * 2 + GEMV_N * 2  # 8,933,376
 COPIES = 64
-# HBM bytes a K1 launch moves, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on the same launches
-# scaled by the counters' reading of a plain copy of known size (profiles/k1_mxfp4_gemv_8192x2048.md):
-# 8,759 KiB read + 32 KiB written
-GEMV_TRAFFIC = (8759 + 32) * 1024
+# the K1 kernel's name as rocprofv3 reports it (the dispatches whose counters measure_traffic reads)
+GEMV_KERNEL = "k_mxfp4_gemv_stream"
 
 
 def _graph_time(launch_all, steps: int, warmup: int, eager: bool = False):
@@ -336,15 +339,22 @@ def moe_cpu(T: int):
             "sample": f"T={T}: Choose + Host.Run (int8 activations, mxfp4.Run), median of 5, {u} unique experts"}
 
 
+DECODE_TOKENS = 256  # C5: greedy-decode 256 tokens after the 1024-token prompt
+
+
 def decode_rate(steps: int, warmup: int):
-    """Prefill the C5 prompt, then time `steps` greedy decode steps (graph replays) after `warmup`."""
+    """The C5 run: prefill the 1024-token prompt, then greedy-decode DECODE_TOKENS tokens (more only
+    when steps + warmup exceed it), each step a replay of a step graph captured before any timing.
+    The first decode_tokens - steps steps (at least `warmup`) run untimed; the last `steps` are timed
+    with HIP events on the replay stream."""
     import numpy as np
     import torch
 
     from hwnpu_amd import synth
     from hwnpu_amd.qwen3 import Qwen3
 
-    total = warmup + steps
+    untimed = max(warmup, DECODE_TOKENS - steps)
+    total = untimed + steps
     m = Qwen3(**C5, max_ctx=PROMPT + total + 8, max_prompt=PROMPT)
     m.synth(seed=0, std=0.02)
     prompt = synth.uniform_int(PROMPT, 0, C5["vocab"], "c5.prompt").cpu().numpy().astype(np.int32)
@@ -358,20 +368,94 @@ def decode_rate(steps: int, warmup: int):
     b.record(s)
     b.synchronize()
     prefill_s = a.elapsed_time(b) / 1e3
-    m.decode(max(warmup, 1))  # captures the step graph
+    m.capture()  # both step graphs, captured and instantiated before any timed region
+    m.decode(untimed)
     torch.cuda.synchronize()
     a.record(s)
     m.decode(steps)
     b.record(s)
     b.synchronize()
     dec_s = a.elapsed_time(b) / 1e3
-    first = PROMPT + max(warmup, 1)  # position of the first timed step
+    first = PROMPT + untimed  # position of the first timed step
     toks = m.history(PROMPT, 8)
     m.close()
     p_mean = first + (steps - 1) / 2
     step_bytes = LIN_BYTES + HEAD_BYTES + KV_POS_BYTES * (p_mean + 1) + KV_POS_BYTES + C5["hidden"] * 2
     return {"tok_s": steps / dec_s, "ms_per_tok": dec_s / steps * 1e3, "prefill_tok_s": PROMPT / prefill_s,
-            "prefill_ms": prefill_s * 1e3, "step_bytes": step_bytes, "first_tokens": [int(t) for t in toks]}
+            "prefill_ms": prefill_s * 1e3, "step_bytes": step_bytes, "first_tokens": [int(t) for t in toks],
+            "decode_tokens": total, "untimed": untimed, "timed_positions": [first, first + steps - 1]}
+
+
+def host_cpu():
+    """The host's CPU model (/proc/cpuinfo) and the cores this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return model, n
+
+
+def _counter_mean_kib(counter: str, workload: str, match: str):
+    """Mean per-dispatch value (KiB) of one rocprofv3 counter over the dispatches whose kernel name
+    contains `match`, from a child `bench.py --workload <workload> --eager` run under
+    `rocprofv3 --pmc <counter>` (a process of its own, started before this one touches the GPU)."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None, "rocprofv3 not found"
+    d = tempfile.mkdtemp(prefix="hwk_pmc_")
+    cmd = ["timeout", "-s", "KILL", "120", prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "run",
+           "--", sys.executable, os.path.abspath(__file__), "--workload", workload, "--eager", "--steps", "128",
+           "--warmup", "0"]
+    try:
+        subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=150)
+        vals = []
+        for root, _, files in os.walk(d):
+            for fn in files:
+                if fn.endswith("counter_collection.csv"):
+                    with open(os.path.join(root, fn)) as f:
+                        for row in csv.DictReader(f):
+                            if match in row["Kernel_Name"] and row["Counter_Name"] == counter:
+                                vals.append(float(row["Counter_Value"]))
+        if not vals:
+            return None, f"no {counter} rows for {match}"
+        return sum(vals) / len(vals), f"{len(vals)} dispatches"
+    except Exception as e:  # the traffic figure is evidence, not the headline: report why it is missing
+        return None, f"{type(e).__name__}: {e}"
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def measure_traffic():
+    """HBM bytes a K1 launch moves: FETCH_SIZE and WRITE_SIZE of the GEMV's dispatches, each scaled by
+    the ratio of a plain device copy's known byte count to what the same counter reads for it. Runs
+    four child processes under rocprofv3 before this process uses the GPU; None when unavailable."""
+    copy_kib = GEMV_BYTES / 1024.0
+    fc, nfc = _counter_mean_kib("FETCH_SIZE", "copy", "copyBuffer")
+    wc, nwc = _counter_mean_kib("WRITE_SIZE", "copy", "copyBuffer")
+    fg, nfg = _counter_mean_kib("FETCH_SIZE", "gemv", GEMV_KERNEL)
+    wg, nwg = _counter_mean_kib("WRITE_SIZE", "gemv", GEMV_KERNEL)
+    if None in (fc, wc, fg, wg) or fc <= 0 or wc <= 0:
+        return None, {"error": [nfc, nwc, nfg, nwg]}
+    rf, rw = copy_kib / fc, copy_kib / wc
+    read_b, write_b = fg * rf * 1024, wg * rw * 1024
+    return int(read_b + write_b), {"fetch_kib": round(fg, 2), "write_kib": round(wg, 2),
+                                   "fetch_scale": round(rf, 4), "write_scale": round(rw, 4),
+                                   "read_bytes": int(read_b), "write_bytes": int(write_b),
+                                   "dispatches": [nfg, nwg], "over_algorithmic": round((read_b + write_b) / GEMV_BYTES, 4)}
 
 
 def cpu_decode_baseline():
@@ -453,16 +537,21 @@ def main():
     ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "copy", "gemm", "attn", "moe"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager", action="store_true", help="gemv/copy: launch one by one, no graph (counter runs)")
+    ap.add_argument("--no-counters", action="store_true", help="decode: skip the rocprofv3 traffic runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(sharding is a design note, not a measured path)", file=sys.stderr)
         sys.exit(2)
+    traffic, traffic_detail = None, {"skipped": True}
+    if args.workload == "decode" and not args.no_counters:
+        # the counter runs are child processes started before this process touches the GPU
+        traffic, traffic_detail = measure_traffic()
     import torch
 
     torch.cuda.synchronize()
     if args.workload == "copy":
-        r = copy_roofline(args.steps or 3200, args.warmup or 320, args.eager)
+        r = copy_roofline(args.steps or 3200, 320 if args.warmup is None else args.warmup, args.eager)
         print(json.dumps({"workload": "copy", "bytes": GEMV_BYTES, "launches": r["launches"],
                           "us_per_launch": round(r["us"], 3), "gbs_read_plus_write": round(r["gbs"], 1)}))
         return
@@ -484,7 +573,7 @@ def main():
         print(json.dumps({"workload": "moe", "results": rows, "cpu_baseline": cpu}))
         return
     if args.workload == "gemv":
-        r = gemv_roofline(args.steps or 3200, args.warmup or 320, args.eager)
+        r = gemv_roofline(args.steps or 3200, 320 if args.warmup is None else args.warmup, args.eager)
         print(json.dumps({"workload": "gemv", "launches": r["launches"], "us_per_launch": round(r["us"], 3),
                           "gbs": round(r["gbs"], 1), "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}))
         return
@@ -495,6 +584,10 @@ def main():
     configs = {"c2_int8_gemm": gemm_rate(4),
                "c3_attention": [attn_rate(L, i8) for L in (2048, 32768) for i8 in (False, True)],
                "c4_moe": [moe_rate(T, 2) for T in (1, 5)]}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_decode_baseline()
+        cpu["cpu_model"], cpu["host_cores"] = host_cpu()
     out = {
         "metric": "decode tok/s at batch 1 (1 GPU); MXFP4 GEMV achieved HBM GB/s vs peak",
         "value": round(d["tok_s"], 2),
@@ -510,8 +603,10 @@ def main():
         "data": "synthetic (seed-0 random-init weights and prompt ids drawn on the GPU)",
         "config": {"workload": "qwen3-shape 28-layer decoder, prompt 1024 then greedy decode at batch 1",
                    "layers": 28, "hidden": 2048, "heads": 16, "kv_heads": 8, "head_dim": 128, "ffn": 6144,
-                   "vocab": 151936, "prompt": PROMPT, "decode_tokens": steps + warmup, "weights": "MXFP4",
-                   "kv_cache": "fp16", "step": "one HIP graph replay"},
+                   "vocab": 151936, "prompt": PROMPT, "decode_tokens": d["decode_tokens"],
+                   "untimed_decode_steps": d["untimed"], "timed_positions": d["timed_positions"],
+                   "weights": "MXFP4", "kv_cache": "fp16",
+                   "step": "one HIP graph replay (graphs captured before timing)"},
         "prefill_tok_s": round(d["prefill_tok_s"], 1),
         "prefill_ms": round(d["prefill_ms"], 3),
         "decode_step_hbm": {"bytes_per_token": int(d["step_bytes"]),
@@ -519,10 +614,11 @@ def main():
                             "frac": round(d["step_bytes"] / (d["ms_per_tok"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "first_tokens": d["first_tokens"],
         "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC,
-                     "kernel": "k_mxfp4_gemv_stream (MXFP4 GEMV 8192x2048, 64 distinct copies, graph)",
+                     "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_detail": traffic_detail,
+                     "kernel": f"{GEMV_KERNEL} (MXFP4 GEMV 8192x2048, 64 distinct copies, graph)",
                      "us_per_launch": round(g["us"], 3), "bytes_per_launch": GEMV_BYTES},
-        "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(),
+        "cpu_baseline": cpu,
         "configs": configs,
     }
     print(json.dumps(out))

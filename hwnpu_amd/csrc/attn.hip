@@ -334,10 +334,13 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
   const uint32_t p = (uint32_t)*pos, len = p + 1;
   const uint32_t begin = c * chunk;
   if (begin >= len) {  // no keys in use here: no partial, no arrival (LAST), else an empty partial
-    if (!LAST && threadIdx.x < G) {
-      const size_t slot = ((size_t)h * nsplit + c) * G + threadIdx.x;
-      ws_m[slot] = -__builtin_inff();
-      ws_l[slot] = 0.0f;
+    if (!LAST) {
+      const size_t slot0 = ((size_t)h * nsplit + c) * G;
+      for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) ws_o[slot0 * 128 + i] = 0.0f;
+      if (threadIdx.x < G) {
+        ws_m[slot0 + threadIdx.x] = -__builtin_inff();
+        ws_l[slot0 + threadIdx.x] = 0.0f;
+      }
     }
     return;
   }
@@ -495,13 +498,20 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
     const float wc = (lc > 0.0f && top != -__builtin_inff()) ? expf(mc - top) : 0.0f;
     const float den = group_sum<64>(wc * lc);
     float num = 0.0f;
+    // a partial of weight 0 adds nothing, whatever its o holds (0 * NaN would be NaN)
 #pragma unroll
-    for (uint32_t u = 0; u < U; u++) num += __shfl(wc, u, 64) * ov[u];
+    for (uint32_t u = 0; u < U; u++) {
+      const float wu = __shfl(wc, u, 64);
+      num += wu > 0.0f ? wu * ov[u] : 0.0f;
+    }
     for (uint32_t cc = U; cc < live; cc += U) {
 #pragma unroll
       for (uint32_t u = 0; u < U; u++) ov[u] = ws_get(&ws_o[(b0 + min(cc + u, lastc) * G + g0) * 128 + d0]);
 #pragma unroll
-      for (uint32_t u = 0; u < U; u++) num += __shfl(wc, (cc + u) & 63, 64) * ov[u];
+      for (uint32_t u = 0; u < U; u++) {
+        const float wu = __shfl(wc, (cc + u) & 63, 64);
+        num += wu > 0.0f ? wu * ov[u] : 0.0f;
+      }
     }
     out[(size_t)(h * G + g0) * 128 + d0] = (f16)f32_value(den > 0.0f ? num / den : 0.0f);
   }
@@ -567,10 +577,17 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ o,
       float ov[U];
 #pragma unroll
       for (uint32_t u = 0; u < U; u++) ov[u] = o[(base + (size_t)(c + 8 * u) * stride) * dim + d];
+      // a skipped chunk (weight 0) adds nothing, whatever its o holds (0 * NaN would be NaN)
 #pragma unroll
-      for (uint32_t u = 0; u < U; u++) num += wgt[c + 8 * u] * ov[u];
+      for (uint32_t u = 0; u < U; u++) {
+        const float wu = wgt[c + 8 * u];
+        num += wu > 0.0f ? wu * ov[u] : 0.0f;
+      }
     }
-    for (; c < chunks; c += 8) num += wgt[c] * o[(base + (size_t)c * stride) * dim + d];
+    for (; c < chunks; c += 8) {
+      const float wu = wgt[c];
+      num += wu > 0.0f ? wu * o[(base + (size_t)c * stride) * dim + d] : 0.0f;
+    }
   }
   red[t] = num;
   __syncthreads();
@@ -843,3 +860,4 @@ HWK_API char *hwk_attn_merge(void *stream, const void *o, const void *m, const v
 }
 
 }  // extern "C"
+

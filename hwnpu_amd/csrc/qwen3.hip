@@ -584,4 +584,11 @@ HWK_API char *hwk_qwen3_decode(hwk_qwen3 *m, void *stream, uint32_t steps) {
   return nullptr;
 }
 
+HWK_API char *hwk_qwen3_capture(hwk_qwen3 *m) {
+  HWK_CHECK(m, "hwk_qwen3_capture: null model");
+  HWK_Q(capture(m, 1, kGraphSteps));
+  HWK_Q(capture(m, 0, 1));
+  return nullptr;
+}
+
 }  // extern "C"

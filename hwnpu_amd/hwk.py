@@ -116,6 +116,7 @@ SIGNATURES = {
     "hwk_qwen3_prefill": (ERR, [P, P, C.POINTER(I32), U32, U32]),
     "hwk_qwen3_step": (ERR, [P, P]),
     "hwk_qwen3_decode": (ERR, [P, P, U32]),
+    "hwk_qwen3_capture": (ERR, [P]),
     "hwk_moe_route": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int, C.c_int, U32]),
     "hwk_moe_workspace_bytes": (SZ, [C.POINTER(MoeParams)]),
     "hwk_moe_experts": (ERR, [P, P, P, P, P, P, P, P, P, P, SZ, C.POINTER(MoeParams)]),

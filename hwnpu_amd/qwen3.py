@@ -101,6 +101,10 @@ class Qwen3:
     def decode(self, steps: int):
         hwk.load().hwk_qwen3_decode(self._h, _stream(), steps)
 
+    def capture(self):
+        """Captures both step graphs now (no replay), so that decode() afterwards only replays."""
+        hwk.load().hwk_qwen3_capture(self._h)
+
     def logits(self) -> np.ndarray:
         return d2h(self._logits, 4 * self.vocab, np.float32)
 

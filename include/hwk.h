@@ -197,7 +197,7 @@ HWK_API char *hwk_argmax(void *stream, const void *x, void *out, uint32_t rows, 
  * and merged as Flash-Decoding does (reference internal/llm/paged/paged.go:70-310, the per-chunk
  * program and Merge, driven by internal/llm/decode/decode.go:1435-1483). ---- */
 typedef struct hwk_attn_params {
-  uint32_t heads;      /* query heads (a multiple of kv_heads; heads/kv_heads in {1, 2, 4, 8}) */
+  uint32_t heads;      /* query heads (a multiple of kv_heads; heads/kv_heads in {1, 2, 4}) */
   uint32_t kv_heads;   /* KV heads */
   uint32_t head_dim;   /* 128 */
   uint32_t len;        /* keys in use, positions 0 .. len-1 (all visible to the query) */
@@ -205,7 +205,7 @@ typedef struct hwk_attn_params {
   uint32_t kv_int8;    /* 0: fp16 K/V; 1: int8 K/V with an fp16 scale per (kv head, position) */
   uint32_t scale_bits; /* the score scale as float32 bits (1/sqrt(head_dim) for the models here) */
   uint32_t out_mode;   /* HWK_OUT_F32 or HWK_OUT_F16 */
-  uint32_t split;      /* keys a split takes (a multiple of 16), 0 for the library's choice */
+  uint32_t split;      /* keys a split takes (a multiple of 64), 0 for the library's choice */
 } hwk_attn_params;
 
 /* Bytes of device workspace hwk_attn_decode needs for these parameters (the chunks' partial
@@ -323,8 +323,12 @@ HWK_API char *hwk_qwen3_prefill(hwk_qwen3 *m, void *stream, const int32_t *token
 /* One decode step, eagerly: the token hist[pos] at position pos -> logits, hist[pos+1] = the
  * greedy token (strict >, ties to the lowest id, reference internal/chat/sample.go:80-87), pos+1. */
 HWK_API char *hwk_qwen3_step(hwk_qwen3 *m, void *stream);
-/* steps decode steps as replays of the captured step graph (captured on the first call). */
+/* steps decode steps as replays of the captured step graphs (one of 8 steps, one of 1 step;
+ * each captured on its first use unless hwk_qwen3_capture captured it before). */
 HWK_API char *hwk_qwen3_decode(hwk_qwen3 *m, void *stream, uint32_t steps);
+/* Captures and instantiates both step graphs now, without running them, so that a later
+ * hwk_qwen3_decode only replays (no capture inside a caller's timed region). */
+HWK_API char *hwk_qwen3_capture(hwk_qwen3 *m);
 
 /* ---- synthetic inputs, reproducible from (seed, name) alone: splitmix64 counter streams keyed
  * by seed ^ fnv64a(name) (the role of reference internal/llm/synth.go:12-56). Each element i

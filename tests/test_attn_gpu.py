@@ -153,6 +153,29 @@ def test_attn_merge_vs_oracle(dev, orc):
     assert np.max(np.abs(got - want)) <= 1e-5 * max(1.0, float(np.max(np.abs(want))))
 
 
+def test_attn_merge_skipped_chunk_never_read(dev, orc):
+    """A chunk whose l is not positive is skipped without reading its o (Merge.Add's `continue`,
+    internal/llm/paged/paged.go:254-256): NaN and Inf there leave the result finite and equal to
+    the merge of the other chunks."""
+    rng = np.random.default_rng(5)
+    chunks, rows, dim = 5, 16, 128
+    o = rng.standard_normal((chunks, rows, dim)).astype(np.float32)
+    m = (rng.standard_normal((chunks, rows)) * 3).astype(np.float32)
+    l = rng.uniform(0.5, 20, (chunks, rows)).astype(np.float32)
+    l[1, :] = 0.0
+    l[3, ::2] = -1.0
+    o[1] = np.nan
+    o[3, ::2] = np.inf
+    m[1] = 50.0  # a skipped chunk's m does not set the top either
+    mg = orc.Merge(rows, dim)
+    for c in range(chunks):
+        mg.add(np.where(l[c][:, None] > 0, o[c], 0.0).astype(np.float32), m[c], l[c])
+    want = mg.result()
+    got = ops.attn_merge(*(torch.from_numpy(a).cuda() for a in (o, m, l))).cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert np.max(np.abs(got - want)) <= 1e-5 * max(1.0, float(np.max(np.abs(want))))
+
+
 def oracle_prefill(orc, q, k, v, start, scale):
     """The reference's chunk program over the whole cache with the causal mask (0 / -1e4), as the
     session runs a prompt (one chunk: every case here is under DefaultChunk = 8192 keys)."""
