@@ -12,6 +12,9 @@
 // The waves merge in LDS; with one chunk a head the workgroup writes the output, else one
 // unnormalized output, max and sum per query head to a workspace that a merge kernel combines
 // with the rule of the reference's Merge (internal/llm/paged/paged.go:252-310).
+#include <mutex>
+#include <vector>
+
 #include "hwk_common.h"
 #include "internal.h"
 
@@ -861,3 +864,53 @@ HWK_API char *hwk_attn_merge(void *stream, const void *o, const void *m, const v
 
 }  // extern "C"
 
+// ---- the allocation-free decode attention: hwk_attn_decode with its split-K partials in a
+// file-scope device array instead of a caller's workspace ----
+
+namespace {
+
+constexpr size_t kScratchBytes = 4u << 20;  // HWK_ATTN_SCRATCH_BYTES in include/hwk.h
+
+// Every device the library runs on holds one copy until the process ends; calls on one device
+// share it (and race when they overlap).
+__device__ __attribute__((aligned(256))) uint8_t scratch[kScratchBytes];
+
+std::mutex scratch_mu;
+std::vector<void *> scratch_ptrs;  // the array's device address, per device
+
+// The address of the current device's copy of `scratch`, looked up once per device (the host-side
+// name of the array is a stand-in that must never reach a kernel).
+char *scratch_of_current_device(void **out) {
+  int dev = 0;
+  HWK_TRY("hipGetDevice", hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if ((size_t)dev >= scratch_ptrs.size()) scratch_ptrs.resize((size_t)dev + 1, nullptr);
+  if (!scratch_ptrs[dev]) {
+    void *p = nullptr;
+    HWK_TRY("hipGetSymbolAddress (attention scratch)", hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    HWK_CHECK(p != nullptr, "hipGetSymbolAddress (attention scratch): null address");
+    scratch_ptrs[dev] = p;
+  }
+  *out = scratch_ptrs[dev];
+  return nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+HWK_API char *hwk_attn_decode_noalloc(void *stream, const void *q, const void *k, const void *v,
+                                      const void *k_scale, const void *v_scale, void *out,
+                                      const hwk_attn_params *p) {
+  HWK_CHECK(p, "hwk_attn_decode_noalloc: null params");
+  const size_t need = hwk_attn_workspace_bytes(p);
+  HWK_CHECK(need <= kScratchBytes,
+            "hwk_attn_decode_noalloc: %zu bytes of partials needed, past the library's %zu-byte scratch "
+            "(use hwk_attn_decode with a workspace)",
+            need, kScratchBytes);
+  void *ws = nullptr;
+  if (char *err = scratch_of_current_device(&ws)) return err;
+  return hwk::attn_decode_dev((hipStream_t)stream, q, k, v, k_scale, v_scale, out, ws, kScratchBytes, p, nullptr, 0);
+}
+
+}  // extern "C"

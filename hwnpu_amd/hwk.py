@@ -23,6 +23,7 @@ SYNC_TO_DEVICE, SYNC_FROM_DEVICE = 0, 1
 INFO_NAME, INFO_ARCH, INFO_PCI_BUS, INFO_CUS, INFO_MEM_BYTES = 0, 1, 2, 3, 4
 STATE_DONE, STATE_PENDING = 0, 1
 OUT_F32, OUT_F16, OUT_ADD_F32 = 0, 1, 2
+ATTN_SCRATCH_BYTES = 4 << 20  # HWK_ATTN_SCRATCH_BYTES
 
 
 class HwkError(RuntimeError):
@@ -105,6 +106,7 @@ SIGNATURES = {
     "hwk_mxfp4_gemm": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
     "hwk_attn_workspace_bytes": (SZ, [C.POINTER(AttnParams)]),
     "hwk_attn_decode": (ERR, [P, P, P, P, P, P, P, P, SZ, C.POINTER(AttnParams)]),
+    "hwk_attn_decode_noalloc": (ERR, [P, P, P, P, P, P, P, C.POINTER(AttnParams)]),
     "hwk_kv_quantize_i8": (ERR, [P, P, P, P, U32, U32]),
     "hwk_attn_merge": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
     "hwk_attn_prefill": (ERR, [P, P, P, P, P, U32, U32, C.POINTER(AttnParams)]),

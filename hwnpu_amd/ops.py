@@ -199,6 +199,32 @@ def attn_decode(q, k, v, length, k_scale=None, v_scale=None, out_mode="f32", sca
     return out
 
 
+def attn_decode_noalloc(q, k, v, length, k_scale=None, v_scale=None, out_mode="f32", scale=None, split=0, out=None):
+    """attn_decode through hwk_attn_decode_noalloc: no workspace (the library's per-device scratch
+    holds the partials), so that nothing is allocated when `out` is given."""
+    heads, d = q.shape
+    kvh, cap, d2 = k.shape
+    if d2 != d:
+        raise ValueError("head_dim of q and k differ")
+    i8 = k.dtype == torch.int8
+    _need(q, "q", torch.float16, (heads, d))
+    _need(k, "k", torch.int8 if i8 else torch.float16, (kvh, cap, d))
+    _need(v, "v", torch.int8 if i8 else torch.float16, (kvh, cap, d))
+    if i8:
+        _need(k_scale, "k_scale", torch.float16, (kvh, cap))
+        _need(v_scale, "v_scale", torch.float16, (kvh, cap))
+    p = attn_params(heads, kvh, length, cap, i8, scale, out_mode, split, d)
+    dt = torch.float16 if out_mode == "f16" else torch.float32
+    if out is None:
+        out = torch.empty((heads, d), dtype=dt, device=q.device)
+    else:
+        _need(out, "out", dt, (heads, d))
+    hwk.load().hwk_attn_decode_noalloc(_stream(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                       k_scale.data_ptr() if i8 else None, v_scale.data_ptr() if i8 else None,
+                                       out.data_ptr(), p)
+    return out
+
+
 def attn_prefill(q, k, v, start, out_mode="f32", scale=None, out=None):
     """Causal attention of tokens query rows q (tokens, heads, d) at positions start .. start+tokens-1
     over fp16 caches k, v (kv_heads, capacity, d) that hold their keys: out (tokens, heads, d)."""

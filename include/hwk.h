@@ -219,6 +219,17 @@ HWK_API size_t hwk_attn_workspace_bytes(const hwk_attn_params *p);
 HWK_API char *hwk_attn_decode(void *stream, const void *q, const void *k, const void *v, const void *k_scale,
                               const void *v_scale, void *out, void *workspace, size_t workspace_bytes,
                               const hwk_attn_params *p);
+/* hwk_attn_decode without a workspace, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no counterpart in
+ * the reference. The split-K partials go to a scratch array the library keeps in each device's
+ * memory (HWK_ATTN_SCRATCH_BYTES, held until the process ends); parameters whose
+ * hwk_attn_workspace_bytes exceed it are refused with an error. It allocates nothing. Every call on
+ * one device shares that device's scratch: calls that overlap on one device (two streams, or two
+ * threads) race. Results equal hwk_attn_decode's bit for bit. */
+#define HWK_ATTN_SCRATCH_BYTES (4u << 20)
+HWK_API char *hwk_attn_decode_noalloc(void *stream, const void *q, const void *k, const void *v,
+                                      const void *k_scale, const void *v_scale, void *out,
+                                      const hwk_attn_params *p);
 /* The int8 KV rule, per row of head_dim values (one kv head at one position): scale =
  * fp16(absmax/127) (1 for a row of zeros), codes = RoundToEven(value/scale) clamped to +-127
  * (reference internal/llm/experts/weights.go:229-252 with internal/vecops/vecops.go:179-185).
