@@ -69,7 +69,7 @@ GEMV_N, GEMV_K = 8192, 2048
 GEMV_BYTES = GEMV_N * GEMV_K // 2 + GEMV_N * GEMV_K // 32 + GEMV_K * 2 + GEMV_N * 2  # 8,933,376
 COPIES = 64
 # the K1 kernel's name as rocprofv3 reports it (the dispatches whose counters measure_traffic reads)
-GEMV_KERNEL = "k_mxfp4_gemv_stream"
+GEMV_KERNEL = "k_mxfp4_gemv_lds"
 
 
 def _graph_time(launch_all, steps: int, warmup: int, eager: bool = False):

@@ -93,6 +93,20 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Sum of a value over the 64 lanes by DPP row shifts and row broadcasts (no LDS traffic): lane 63
+// ends with the total (the other lanes hold partial sums).
+#define HWK_DPP_F32(v, ctrl, row_mask, bound_ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), ctrl, row_mask, 0xf, bound_ctrl))
+__device__ __forceinline__ float wave_sum_to_63(float v) {
+  v += HWK_DPP_F32(v, 0x111, 0xf, true);   // row_shr:1
+  v += HWK_DPP_F32(v, 0x112, 0xf, true);   // row_shr:2
+  v += HWK_DPP_F32(v, 0x114, 0xf, true);   // row_shr:4
+  v += HWK_DPP_F32(v, 0x118, 0xf, true);   // row_shr:8: lane 15 of each row of 16 holds the row's sum
+  v += HWK_DPP_F32(v, 0x142, 0xa, false);  // row_bcast:15 into rows 1 and 3
+  v += HWK_DPP_F32(v, 0x143, 0xc, false);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

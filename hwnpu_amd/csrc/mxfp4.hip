@@ -7,6 +7,7 @@
 // lanes of a row with cross-lane shuffles. x stays in registers for all of a wave's rows.
 #include "hwk_common.h"
 #include "internal.h"
+#include "mxfp4_gemv.h"
 #include "synth.h"
 
 namespace {
@@ -222,31 +223,30 @@ struct XIn {
   double eps;
 };
 
-// The decode-step GEMV (64 lanes a row, BPL blocks a lane, nb <= 64*BPL). The workgroup first puts
-// x in LDS, with one round of global loads (issued after the first row set's weight loads, which
-// overlap them): copied (X_F16) or made from the fp32 residual h by RMSNorm (X_NORM). Then its
-// waves stream row sets as k_mxfp4_gemv_stream does, x read from LDS. SWIGLU: a row set holds
-// (gate, up) row pairs and the output is fp16 silu(gate) * up at the pair's index.
-template <int BPL, int RPW, int XM, bool SWIGLU, int WPB>
+// The decode-step GEMV (64 lanes a row, BPL blocks a lane, nb <= 64*BPL): K1's shape (one row set a
+// wave, the grid as large as the matrix, DPP reduction into lane 63) with x made by the workgroup: its
+// inputs are loaded first, then the wave's weights, and while those are in flight x goes to LDS,
+// copied (X_F16) or made from the fp32 residual h by RMSNorm (X_NORM: every workgroup sums h^2 itself,
+// which hides behind its weight loads). SWIGLU: a wave's rows come in (gate, up) pairs and the output
+// is fp16 silu(gate) * up at the pair's index; otherwise y per MODE.
+template <int BPL, int RPW, int XM, bool SWIGLU, int WPB, int MODE>
 __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restrict__ w, const uint8_t *__restrict__ e,
-                                                           XIn in, void *__restrict__ y, uint32_t n, uint32_t nb,
-                                                           int mode) {
+                                                           XIn in, void *__restrict__ y, uint32_t n, uint32_t nb) {
   static_assert(!SWIGLU || RPW % 2 == 0, "SwiGLU pairs rows");
   constexpr int NT = 64 * WPB;
-  constexpr int PER = (64 * BPL * 32 + NT - 1) / NT;  // x values a thread makes
-  __shared__ uint4 xs[64 * BPL * 4];
+  constexpr int PER = (64 * BPL * 32 + NT - 1) / NT;  // x values a thread makes (X_NORM)
+  constexpr int XC = 64 * BPL * 4;                    // 16-byte chunks of x LDS holds
+  constexpr int XPER = (XC + NT - 1) / NT;            // chunks a thread copies (X_F16)
+  constexpr bool add = MODE == HWK_OUT_ADD_F32;
+  __shared__ uint4 xs[XC];
   __shared__ double red[WPB];
   const int t = threadIdx.x, lane = t & 63;
   const uint32_t k = nb * 32;
-  constexpr uint32_t ROWS = RPW;  // 64 lanes a row: a row set is RPW consecutive rows
-  const uint32_t waves = gridDim.x * WPB;
-  uint32_t set = blockIdx.x * WPB + (t >> 6);
-  const uint32_t sets = (n + ROWS - 1) / ROWS;
-  const bool live = set < sets;
-  // x's inputs are loaded first, then the first row set's weights (a wave past the last set loads
-  // that one again and leaves), so that x is made while the weights are in flight: the loads
-  // complete in issue order for the wait counter
+  const uint32_t r0 = (blockIdx.x * WPB + (t >> 6)) * RPW;
+  // x's inputs first, then the old y of ADD mode, then the weights (loads complete in issue order
+  // for the wait counter, so x is made while the weights are in flight)
   float hv[PER], wv[PER];
+  uint4 xv[XPER];
   if constexpr (XM == X_NORM) {
 #pragma unroll
     for (int j = 0; j < PER; j++) {
@@ -254,10 +254,16 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
       hv[j] = in.h[i];
       wv[j] = in.nw[i];
     }
+  } else {
+#pragma unroll
+    for (int j = 0; j < XPER; j++) xv[j] = in.x16[min((uint32_t)(t + j * NT), nb * 4 - 1)];
   }
+  float yo[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) yo[i] = add ? ((const float *)y)[min(r0 + i, n - 1)] : 0.0f;
   issue_order();
-  RowSet<BPL, RPW> cur, nxt;
-  load_rowset<64, BPL, RPW>(cur, w, e, (live ? set : sets - 1) * ROWS, n, nb, lane);
+  RowSet<BPL, RPW> cur;
+  load_rowset<64, BPL, RPW>(cur, w, e, r0, n, nb, lane);
   f16 *xh = (f16 *)xs;
   if constexpr (XM == X_NORM) {
     double ss = 0.0;
@@ -277,59 +283,51 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
     for (int j = 0; j < PER; j++)
       if (t + j * NT < k) xh[t + j * NT] = (f16)f32_value((hv[j] * r) * wv[j]);
   } else {
-    for (uint32_t i = t; i < nb * 4; i += NT) xs[i] = in.x16[i];
+#pragma unroll
+    for (int j = 0; j < XPER; j++)
+      if (t + j * NT < XC) xs[t + j * NT] = xv[j];
   }
   __syncthreads();
-  if (!live) return;
   uint4 xr[BPL][4];
 #pragma unroll
   for (int j = 0; j < BPL; j++) {
-    const uint32_t b = j * 64 + lane;
+    const uint32_t b = min((uint32_t)(j * 64 + lane), nb - 1);
 #pragma unroll
-    for (int q = 0; q < 4; q++) xr[j][q] = b < nb ? xs[b * 4 + q] : make_uint4(0, 0, 0, 0);
+    for (int q = 0; q < 4; q++) xr[j][q] = xs[b * 4 + q];
   }
-  for (;;) {
-    const uint32_t next = set + waves;
-    if (next < sets) load_rowset<64, BPL, RPW>(nxt, w, e, next * ROWS, n, nb, lane);
-    float v[RPW];
+  float v[RPW];
 #pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      float acc = 0.0f;
+  for (int i = 0; i < RPW; i++) {
+    float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < BPL; j++) {
-        float d0 = 0.0f, d1 = 0.0f;
-        const uint32_t cw[4] = {cur.c[i][j].x, cur.c[i][j].y, cur.c[i][j].z, cur.c[i][j].w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<0>(cw[q]), h2_of_bits(xr[j][q].x), d0, false);
-          d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<1>(cw[q]), h2_of_bits(xr[j][q].y), d1, false);
-          d0 = __builtin_amdgcn_fdot2(fp4x2_to_h2<2>(cw[q]), h2_of_bits(xr[j][q].z), d0, false);
-          d1 = __builtin_amdgcn_fdot2(fp4x2_to_h2<3>(cw[q]), h2_of_bits(xr[j][q].w), d1, false);
-        }
-        acc += block_term(d0, d1, cur.s[i][j], (uint32_t)(j * 64 + lane) < nb);
-      }
-      v[i] = group_sum<64>(acc);
+    for (int j = 0; j < BPL; j++) {
+      const float term = mxfp4_block_dot(cur.c[i][j], xr[j]) * e8m0_scale(cur.s[i][j]);
+      acc += (uint32_t)(j * 64 + lane) < nb ? term : 0.0f;
     }
-    if (lane == 0) {
-      const uint32_t r0 = set * ROWS;
-      if constexpr (SWIGLU) {
+    v[i] = wave_sum_to_63(acc);
+  }
+  if (lane == 63) {
+    if constexpr (SWIGLU) {
 #pragma unroll
-        for (int i = 0; i < RPW; i += 2) {
-          if (r0 + i + 1 < n) {
+      for (int i = 0; i < RPW; i += 2) {
+        if (r0 + i + 1 < n) {
 #pragma clang fp contract(off)
-            const float g = v[i], u = v[i + 1];
-            ((f16 *)y)[(r0 + i) / 2] = (f16)f32_value(g / (1.0f + (float)exp(-(double)g)) * u);
-          }
+          const float g = v[i], u = v[i + 1];
+          ((f16 *)y)[(r0 + i) / 2] = (f16)f32_value(g / (1.0f + (float)exp(-(double)g)) * u);
         }
-      } else {
+      }
+    } else {
 #pragma unroll
-        for (int i = 0; i < RPW; i++)
-          if (r0 + i < n) store_out(y, r0 + i, v[i], mode);
+      for (int i = 0; i < RPW; i++) {
+        if (r0 + i >= n) continue;
+        if constexpr (MODE == HWK_OUT_F16)
+          ((f16 *)y)[r0 + i] = (f16)f32_value(v[i]);
+        else if constexpr (add)
+          ((float *)y)[r0 + i] = yo[i] + v[i];
+        else
+          ((float *)y)[r0 + i] = v[i];
       }
     }
-    if (next >= sets) break;
-    set = next;
-    cur = nxt;
   }
 }
 
@@ -570,6 +568,28 @@ void launch_rpw(hipStream_t st, const void *w, const void *e, const void *x, voi
   }
 }
 
+// K1 for rows of 33..256 blocks (64 lanes a row): 8 waves a workgroup, 2 rows a wave for matrices of
+// 4096 rows or more, else 1 (twice the waves for the short matrices of the decode step).
+template <int BPL, int MODE>
+void launch_lds_m(hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n, uint32_t nb) {
+  constexpr int W = 8;
+  if (n >= 4096) {
+    hipLaunchKernelGGL((k_mxfp4_gemv_lds<W, 2, BPL, MODE>), dim3((n + 2 * W - 1) / (2 * W)), dim3(64 * W), 0, st,
+                       (const uint4 *)w, (const uint8_t *)e, (const uint4 *)x, y, n, nb);
+  } else {
+    hipLaunchKernelGGL((k_mxfp4_gemv_lds<W, 1, BPL, MODE>), dim3((n + W - 1) / W), dim3(64 * W), 0, st,
+                       (const uint4 *)w, (const uint8_t *)e, (const uint4 *)x, y, n, nb);
+  }
+}
+
+template <int BPL>
+void launch_lds(hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n, uint32_t nb,
+                int mode) {
+  if (mode == HWK_OUT_F16) launch_lds_m<BPL, HWK_OUT_F16>(st, w, e, x, y, n, nb);
+  else if (mode == HWK_OUT_ADD_F32) launch_lds_m<BPL, HWK_OUT_ADD_F32>(st, w, e, x, y, n, nb);
+  else launch_lds_m<BPL, HWK_OUT_F32>(st, w, e, x, y, n, nb);
+}
+
 template <int LPR>
 void launch_bpl(int bpl, hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n,
                 uint32_t nb, int mode) {
@@ -631,6 +651,15 @@ HWK_API char *hwk_mxfp4_gemv(void *stream, const void *w, const void *e, const v
   int lpr, bpl;
   gemv_layout(nb, &lpr, &bpl);
   hipStream_t st = (hipStream_t)stream;
+  if (lpr == 64 && nb <= 256) {
+    switch (bpl) {
+      case 1: launch_lds<1>(st, w, e, x, y, n, nb, out_mode); break;
+      case 2: launch_lds<2>(st, w, e, x, y, n, nb, out_mode); break;
+      case 3: launch_lds<3>(st, w, e, x, y, n, nb, out_mode); break;
+      default: launch_lds<4>(st, w, e, x, y, n, nb, out_mode); break;
+    }
+    return hwk::launched("hwk_mxfp4_gemv");
+  }
   switch (lpr) {
     case 64: launch_bpl<64>(bpl, st, w, e, x, y, n, nb, out_mode); break;
     case 32: launch_bpl<32>(bpl, st, w, e, x, y, n, nb, out_mode); break;
@@ -731,43 +760,49 @@ int gemvx_rpw() {
   return v;
 }
 
-template <int BPL, int XM, bool SWIGLU, int WPB, int RPW>
-void launch_x_w(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb,
-                int mode) {
+template <int BPL, int XM, bool SWIGLU, int WPB, int RPW, int MODE>
+void launch_x_w(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb) {
   const uint32_t sets = (n + RPW - 1) / RPW;
-  const uint32_t waves = sets < stream_waves() ? sets : stream_waves();
-  hipLaunchKernelGGL((k_mxfp4_gemv_x<BPL, RPW, XM, SWIGLU, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0,
-                     st, (const uint4 *)w, (const uint8_t *)e, in, y, n, nb, mode);
+  hipLaunchKernelGGL((k_mxfp4_gemv_x<BPL, RPW, XM, SWIGLU, WPB, MODE>), dim3((sets + WPB - 1) / WPB), dim3(64 * WPB), 0,
+                     st, (const uint4 *)w, (const uint8_t *)e, in, y, n, nb);
 }
 
-template <int BPL, int XM, bool SWIGLU>
-void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb, int mode) {
+template <int BPL, int XM, bool SWIGLU, int MODE>
+void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb) {
   const bool r4 = gemvx_rpw() == 4;
   switch (gemvx_wpb()) {
     case 4:
-      r4 ? launch_x_w<BPL, XM, SWIGLU, 4, 4>(st, w, e, in, y, n, nb, mode)
-         : launch_x_w<BPL, XM, SWIGLU, 4, 2>(st, w, e, in, y, n, nb, mode);
+      r4 ? launch_x_w<BPL, XM, SWIGLU, 4, 4, MODE>(st, w, e, in, y, n, nb)
+         : launch_x_w<BPL, XM, SWIGLU, 4, 2, MODE>(st, w, e, in, y, n, nb);
       break;
     case 16:
-      r4 ? launch_x_w<BPL, XM, SWIGLU, 16, 4>(st, w, e, in, y, n, nb, mode)
-         : launch_x_w<BPL, XM, SWIGLU, 16, 2>(st, w, e, in, y, n, nb, mode);
+      r4 ? launch_x_w<BPL, XM, SWIGLU, 16, 4, MODE>(st, w, e, in, y, n, nb)
+         : launch_x_w<BPL, XM, SWIGLU, 16, 2, MODE>(st, w, e, in, y, n, nb);
       break;
     default:
-      r4 ? launch_x_w<BPL, XM, SWIGLU, 8, 4>(st, w, e, in, y, n, nb, mode)
-         : launch_x_w<BPL, XM, SWIGLU, 8, 2>(st, w, e, in, y, n, nb, mode);
+      r4 ? launch_x_w<BPL, XM, SWIGLU, 8, 4, MODE>(st, w, e, in, y, n, nb)
+         : launch_x_w<BPL, XM, SWIGLU, 8, 2, MODE>(st, w, e, in, y, n, nb);
       break;
   }
 }
 
-template <int XM, bool SWIGLU>
-void launch_x_bpl(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb,
-                  int mode) {
+template <int XM, bool SWIGLU, int MODE>
+void launch_x_bpl(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb) {
   switch ((nb + 63) / 64) {
-    case 1: launch_x<1, XM, SWIGLU>(st, w, e, in, y, n, nb, mode); break;
-    case 2: launch_x<2, XM, SWIGLU>(st, w, e, in, y, n, nb, mode); break;
-    case 3: launch_x<3, XM, SWIGLU>(st, w, e, in, y, n, nb, mode); break;
-    default: launch_x<4, XM, SWIGLU>(st, w, e, in, y, n, nb, mode); break;
+    case 1: launch_x<1, XM, SWIGLU, MODE>(st, w, e, in, y, n, nb); break;
+    case 2: launch_x<2, XM, SWIGLU, MODE>(st, w, e, in, y, n, nb); break;
+    case 3: launch_x<3, XM, SWIGLU, MODE>(st, w, e, in, y, n, nb); break;
+    default: launch_x<4, XM, SWIGLU, MODE>(st, w, e, in, y, n, nb); break;
   }
+}
+
+template <int XM>
+void launch_x_mode(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb,
+                   int mode, bool swiglu) {
+  if (swiglu) launch_x_bpl<XM, true, HWK_OUT_F16>(st, w, e, in, y, n, nb);
+  else if (mode == HWK_OUT_F16) launch_x_bpl<XM, false, HWK_OUT_F16>(st, w, e, in, y, n, nb);
+  else if (mode == HWK_OUT_ADD_F32) launch_x_bpl<XM, false, HWK_OUT_ADD_F32>(st, w, e, in, y, n, nb);
+  else launch_x_bpl<XM, false, HWK_OUT_F32>(st, w, e, in, y, n, nb);
 }
 
 }  // namespace
@@ -782,13 +817,8 @@ char *mxfp4_gemv_x(hipStream_t st, const void *w, const void *e, const void *x16
   if (n == 0) return nullptr;
   XIn in{(const uint4 *)x16, h, nw, eps};
   const uint32_t nb = k / 32;
-  if (swiglu) {
-    if (h) launch_x_bpl<X_NORM, true>(st, w, e, in, y, n, nb, out_mode);
-    else launch_x_bpl<X_F16, true>(st, w, e, in, y, n, nb, out_mode);
-  } else {
-    if (h) launch_x_bpl<X_NORM, false>(st, w, e, in, y, n, nb, out_mode);
-    else launch_x_bpl<X_F16, false>(st, w, e, in, y, n, nb, out_mode);
-  }
+  if (h) launch_x_mode<X_NORM>(st, w, e, in, y, n, nb, out_mode, swiglu);
+  else launch_x_mode<X_F16>(st, w, e, in, y, n, nb, out_mode, swiglu);
   return launched("mxfp4_gemv_x");
 }
 

@@ -1,32 +1,10 @@
-// libhwk's device, buffer, stream, event and code-object calls: what hwnpu's backend contract
-// asks of a device (reference internal/backend/backend.go:12-118), over the HIP runtime.
+// libhwk's device, buffer, stream and event calls: what hwnpu's backend contract asks of a device
+// (reference internal/backend/backend.go:12-118), over the HIP runtime. The code-object calls are in
+// codeobj.hip.
 #include <chrono>
 #include <thread>
 
-#include "hwk_common.h"
-
-struct hwk_device {
-  int index;
-  hipDeviceProp_t prop;
-};
-
-struct hwk_buf {
-  hwk_device *dev;
-  size_t size;
-  int kind;
-  void *host;  // pinned mirror (HWK_BUF_MIRRORED), else null
-  void *ptr;   // device allocation
-};
-
-struct hwk_module {
-  hwk_device *dev;
-  hipModule_t mod;
-};
-
-struct hwk_function {
-  hwk_module *mod;
-  hipFunction_t fn;
-};
+#include "runtime.h"
 
 extern "C" {
 
@@ -220,52 +198,6 @@ HWK_API char *hwk_event_elapsed_ns(void *start, void *end, uint64_t *ns) {
   float ms = 0;
   HWK_TRY("hipEventElapsedTime", hipEventElapsedTime(&ms, (hipEvent_t)start, (hipEvent_t)end));
   *ns = (uint64_t)((double)ms * 1e6);
-  return nullptr;
-}
-
-HWK_API char *hwk_module_load(hwk_device *d, const void *image, size_t n, hwk_module **out) {
-  HWK_CHECK(d && image && out && n > 0, "hwk_module_load: null argument");
-  HWK_TRY("hipSetDevice", hipSetDevice(d->index));
-  hipModule_t m;
-  HWK_TRY("hipModuleLoadData", hipModuleLoadData(&m, image));
-  hwk_module *mod = new hwk_module();
-  mod->dev = d;
-  mod->mod = m;
-  *out = mod;
-  return nullptr;
-}
-
-HWK_API void hwk_module_free(hwk_module *m) {
-  if (!m) return;
-  (void)hipModuleUnload(m->mod);
-  delete m;
-}
-
-HWK_API char *hwk_module_function(hwk_module *m, const char *name, hwk_function **out) {
-  HWK_CHECK(m && name && out, "hwk_module_function: null argument");
-  hipFunction_t f;
-  hipError_t e = hipModuleGetFunction(&f, m->mod, name);
-  if (e != hipSuccess) return hwk::errf("hwk_module_function: no kernel %s (%s)", name, hipGetErrorString(e));
-  hwk_function *fn = new hwk_function();
-  fn->mod = m;
-  fn->fn = f;
-  *out = fn;
-  return nullptr;
-}
-
-HWK_API void hwk_function_free(hwk_function *f) { delete f; }
-
-HWK_API char *hwk_launch(hwk_function *f, const uint32_t grid[3], const uint32_t block[3],
-                         uint32_t shared_bytes, void *stream, const void *args, size_t args_size) {
-  HWK_CHECK(f && grid && block, "hwk_launch: null argument");
-  HWK_CHECK(grid[0] && grid[1] && grid[2] && block[0] && block[1] && block[2], "hwk_launch: empty geometry");
-  HWK_CHECK((uint64_t)block[0] * block[1] * block[2] <= 1024, "hwk_launch: block of %u x %u x %u", block[0], block[1], block[2]);
-  size_t size = args_size;
-  void *cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *)args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
-                 HIP_LAUNCH_PARAM_END};
-  HWK_TRY("hipModuleLaunchKernel",
-          hipModuleLaunchKernel(f->fn, grid[0], grid[1], grid[2], block[0], block[1], block[2], shared_bytes,
-                                (hipStream_t)stream, nullptr, args_size ? cfg : nullptr));
   return nullptr;
 }
 

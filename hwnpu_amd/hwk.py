@@ -12,10 +12,12 @@ import ctypes as C
 import os
 import threading
 
-ABI = 1
+ABI = 2
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libhwk.so")
+# the library's gfx950 code object (hwk_module_load): the batch-1 MXFP4 GEMV and a streaming read
+CODE_OBJECT_PATH = os.path.join(LIB_DIR, "hwk_gfx950.hsaco")
 
 # include/hwk.h enums
 BUF_MIRRORED, BUF_DEVICE = 0, 1
@@ -53,6 +55,18 @@ class MoeParams(C.Structure):
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 
 
+class KernelInfo(C.Structure):
+    """hwk_kernel_info (include/hwk.h)."""
+    _fields_ = [("name", C.c_char * 64), ("args", U32), ("kernarg_bytes", U32), ("block", U32), ("max_block", U32),
+                ("lds_bytes", U32), ("cus", U32), ("runnable", U32), ("reserved", U32)]
+
+
+class KernelArg(C.Structure):
+    """hwk_kernel_arg (include/hwk.h)."""
+    _fields_ = [("index", U32), ("offset", U32), ("size", U32), ("buffer", U32), ("name", C.c_char * 64),
+                ("type", C.c_char * 32)]
+
+
 class Qwen3Config(C.Structure):
     """hwk_qwen3_config (include/hwk.h)."""
     _fields_ = [("layers", U32), ("hidden", U32), ("heads", U32), ("kv_heads", U32), ("head_dim", U32),
@@ -85,9 +99,17 @@ SIGNATURES = {
     "hwk_event_elapsed_ns": (ERR, [P, P, C.POINTER(U64)]),
     "hwk_module_load": (ERR, [P, P, SZ, C.POINTER(P)]),
     "hwk_module_free": (None, [P]),
-    "hwk_module_function": (ERR, [P, C.c_char_p, C.POINTER(P)]),
-    "hwk_function_free": (None, [P]),
-    "hwk_launch": (ERR, [P, C.POINTER(U32), C.POINTER(U32), U32, P, P, SZ]),
+    "hwk_module_kernel_count": (ERR, [P, C.POINTER(U32)]),
+    "hwk_module_kernel_info": (ERR, [P, U32, C.POINTER(KernelInfo)]),
+    "hwk_module_kernel_arg": (ERR, [P, U32, U32, C.POINTER(KernelArg)]),
+    "hwk_run_new": (ERR, [P, C.c_char_p, C.POINTER(P)]),
+    "hwk_run_set_arg": (ERR, [P, U32, P, SZ]),
+    "hwk_run_set_buffer": (ERR, [P, U32, P]),
+    "hwk_run_set_buffer_at": (ERR, [P, U32, P, SZ, SZ]),
+    "hwk_run_err": (ERR, [P]),
+    "hwk_run_submit": (ERR, [P, P]),
+    "hwk_run_wait": (ERR, [P, U32, C.POINTER(C.c_int)]),
+    "hwk_run_free": (ERR, [P]),
     "hwk_mxfp4_dequant_f16": (ERR, [P, P, P, P, U32, U32]),
     "hwk_mxfp4_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
     "hwk_mxfp4_gemv_rows": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),

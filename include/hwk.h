@@ -29,12 +29,12 @@ extern "C" {
 
 /* The ABI version: a binding refuses a library of another (reference xrtshim.h:25-26, the XS_ABI
  * check of internal/backend/amdxrt/shim.go:25-26). */
-#define HWK_ABI 1
+#define HWK_ABI 2
 
 typedef struct hwk_device hwk_device;
 typedef struct hwk_buf hwk_buf;
 typedef struct hwk_module hwk_module;
-typedef struct hwk_function hwk_function;
+typedef struct hwk_run hwk_run;
 
 /* Buffer kinds of hwk_buf_alloc (reference internal/types BufferKind): a device allocation with a
  * pinned host mirror synced explicitly (hwnpu Buffer.Bytes/SyncToDevice/SyncFromDevice), or a
@@ -88,15 +88,63 @@ HWK_API char *hwk_event_wait(void *event, uint32_t timeout_ms, int *state);
 /* The time between two recorded events, in nanoseconds. */
 HWK_API char *hwk_event_elapsed_ns(void *start, void *end, uint64_t *ns);
 
-/* ---- code objects (reference KernelDevice.LoadProgram, Program, Run; backend.go:27-46) ----
- * A gfx950 code object loaded with hipModuleLoadData; a kernel launched with its arguments packed
- * as the kernel's argument buffer (little endian, at the offsets the kernel's metadata gives). */
+/* ---- code objects (reference KernelDevice.LoadProgram, Program.Kernels/NewRun, Run, Fence;
+ * internal/backend/backend.go:27-46, internal/types/kernel.go:22-36, kernel.go:109-254) ----
+ * A gfx950 code object (an ELF, or a clang offload bundle holding one) loaded with hipModuleLoadData.
+ * Its kernels and their arguments are read from the object's AMDGPU metadata; the launch geometry of
+ * each kernel from the object's own manifest (the `hwk_co_manifest` constant array: workgroup size,
+ * and grid.x as a function of one 4-byte argument), so that no call takes grid or block sizes. The
+ * library's own code object is lib/hwk_gfx950.hsaco (the batch-1 MXFP4 GEMV and a streaming read). */
+
+/* A kernel of a loaded module (reference types.KernelInfo). */
+typedef struct hwk_kernel_info {
+  char name[64];
+  uint32_t args;          /* explicit arguments (hidden ones are the runtime's) */
+  uint32_t kernarg_bytes; /* bytes the explicit arguments span */
+  uint32_t block;         /* threads a workgroup (the manifest's); 0 without a manifest entry */
+  uint32_t max_block;     /* the kernel's largest workgroup (its launch bounds) */
+  uint32_t lds_bytes;     /* LDS a workgroup: static (metadata) + dynamic (manifest) */
+  uint32_t cus;           /* compute units of the module's device; 0 for an inspection-only module */
+  uint32_t runnable;      /* 1 when the manifest gives the kernel's launch geometry */
+  uint32_t reserved;
+} hwk_kernel_info;
+
+/* An explicit argument of a kernel (reference types.KernelArg). */
+typedef struct hwk_kernel_arg {
+  uint32_t index;  /* position in the kernel's signature */
+  uint32_t offset; /* byte offset in the argument buffer */
+  uint32_t size;   /* bytes */
+  uint32_t buffer; /* 1: a device address, set with hwk_run_set_buffer*; 0: a value, hwk_run_set_arg */
+  char name[64];
+  char type[32];   /* "void *" for a buffer, else "uint8_t", "uint16_t", "uint32_t", "uint64_t" or "bytes" */
+} hwk_kernel_arg;
+
+/* Loads a code object on device d; with d NULL the module only lists its kernels (no HIP call). */
 HWK_API char *hwk_module_load(hwk_device *d, const void *image, size_t n, hwk_module **out);
 HWK_API void hwk_module_free(hwk_module *m);
-HWK_API char *hwk_module_function(hwk_module *m, const char *name, hwk_function **out);
-HWK_API void hwk_function_free(hwk_function *f);
-HWK_API char *hwk_launch(hwk_function *f, const uint32_t grid[3], const uint32_t block[3],
-                         uint32_t shared_bytes, void *stream, const void *args, size_t args_size);
+HWK_API char *hwk_module_kernel_count(hwk_module *m, uint32_t *count);
+HWK_API char *hwk_module_kernel_info(hwk_module *m, uint32_t kernel, hwk_kernel_info *out);
+HWK_API char *hwk_module_kernel_arg(hwk_module *m, uint32_t kernel, uint32_t arg, hwk_kernel_arg *out);
+/* An invocation of a kernel; arguments start zeroed (reference Kernel.NewRun). */
+HWK_API char *hwk_run_new(hwk_module *m, const char *kernel, hwk_run **out);
+/* A value argument from its little-endian bytes: an unknown index, a buffer argument or a size other
+ * than the argument's is an error (reference internal/backend/amd/device.go:349-363). The first
+ * setter error is kept: hwk_run_err returns it and hwk_run_submit refuses (kernel.go:135-199). */
+HWK_API char *hwk_run_set_arg(hwk_run *r, uint32_t index, const void *value, size_t n);
+/* A buffer argument: the device address of b (plus off), b allocated on the module's device; a
+ * value argument or a range past the buffer is an error (device.go:367-394). */
+HWK_API char *hwk_run_set_buffer(hwk_run *r, uint32_t index, hwk_buf *b);
+HWK_API char *hwk_run_set_buffer_at(hwk_run *r, uint32_t index, hwk_buf *b, size_t off, size_t n);
+/* The first error a setter recorded (a copy), or NULL. */
+HWK_API char *hwk_run_err(hwk_run *r);
+/* Launches on the stream with the manifest's geometry. An error while the run's previous
+ * submission is still running (device.go:396-401). Sync input buffers to the device first. */
+HWK_API char *hwk_run_submit(hwk_run *r, void *stream);
+/* The run's fence: waits up to timeout_ms (0: poll once) and writes HWK_STATE_DONE or
+ * HWK_STATE_PENDING; the submission keeps running when the wait gives up (graph.go:144-150). */
+HWK_API char *hwk_run_wait(hwk_run *r, uint32_t timeout_ms, int *state);
+/* Waits for a running submission, then releases the run (reference Run.Close). */
+HWK_API char *hwk_run_free(hwk_run *r);
 
 /* ---- MXFP4 weights: rows of k values, blocks of 32; codes (rows, k/32, 16) bytes with the even
  * value in the low nibble, e8m0 scales (rows, k/32) (reference internal/mxfp4/mxfp4.go:1-20,
