@@ -178,83 +178,249 @@ __device__ __forceinline__ void run_tiles(Tile<I8> &ta, Tile<I8> &tb, uint32_t k
   }
 }
 
-// Workgroup (kv head h, chunk c) of W waves over keys [c*chunk, min((c+1)*chunk, len)), len plus
-// *pos when pos is given (a chunk past the keys in use leaves l = 0, which the merge skips). With one
-// chunk a head it writes out directly; otherwise its partial (o unnormalized, m in natural log
-// units, l) per query head g of h goes to workspace slot (h*nchunk + c)*G + g for k_attn_merge.
+// ---- K4, the split-K decode attention of hwk_attn_decode ----
+//
+// A lane's view of a 16-key tile:
+//   scores   D = K_tile . Q^T on v_mfma_f32_16x16x32_f16, K as the A operand (lane l: key l%16, a
+//            k-step's 8 dims), Q as B with the G query heads repeated over the 16 columns, so that
+//            lane l ends with the scores of keys 4*(l/16) .. +3 for query head l%G: no lane idles;
+//   softmax  a key's scores of one head sit in the 4 row groups of the wave (lanes l, l^16, l^32,
+//            l^48): max and sum over them with two permlane swaps (VALU, no LDS);
+//   P.V      on the VALUs in fp32 (P never rounded): lane l holds V rows 4*(l/16) + r (r = 0..3), dims
+//            (l%16)*8 .. +8, and takes head g's weight of key 4*(l/16)+r from lane (l & ~3) + g of its
+//            quad by a DPP broadcast.
+// Every load is issued unconditionally from a clamped row (a predicated load makes the compiler wait
+// for it before issuing the next), and the terms of keys past the attended range are dropped.
+
+// The two permlane swaps: v_permlane16_swap exchanges the odd rows (16 lanes) of its first operand
+// with the even rows of its second, v_permlane32_swap the upper half of the first with the lower
+// half of the second. On two copies of v, the two results hold v and its row (half) partner in every
+// lane. Issued as inline asm after two wait states (the hazard the compiler inserts before them):
+// the compiler builtin's second result is not usable (it is folded into the first).
+__device__ __forceinline__ void swap_rows16(float &a, float &b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_rows32(float &a, float &b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+// Sum / max over the 4 row groups (l, l^16, l^32, l^48); every lane gets the result.
+__device__ __forceinline__ float row_groups_sum(float v) {
+  float a = v, b = v;
+  swap_rows16(a, b);
+  v = a + b;
+  a = v;
+  b = v;
+  swap_rows32(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float row_groups_max(float v) {
+  float a = v, b = v;
+  swap_rows16(a, b);
+  v = fmaxf(a, b);
+  a = v;
+  b = v;
+  swap_rows32(a, b);
+  return fmaxf(a, b);
+}
+// The value of lane (l & ~3) + Q of the lane's quad (DPP quad_perm broadcast).
+template <int Q>
+__device__ __forceinline__ float quad_lane(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), Q * 0x55, 0xf, 0xf, false));
+}
+template <int G>
+__device__ __forceinline__ void quad_heads(float v, float (&out)[G]) {
+  if constexpr (G == 1) out[0] = v;
+  if constexpr (G == 2) {
+    out[0] = quad_lane<0>(v);
+    out[1] = quad_lane<1>(v);
+  }
+  if constexpr (G == 4) {
+    out[0] = quad_lane<0>(v);
+    out[1] = quad_lane<1>(v);
+    out[2] = quad_lane<2>(v);
+    out[3] = quad_lane<3>(v);
+  }
+}
+
+// 16 int8 values (four dwords) as 16 exact fp16 values.
+__device__ __forceinline__ void i8x16_to_half8x2(uint4 w, half8 &lo, half8 &hi) {
+  lo = i8x8_to_half8(make_uint2(w.x, w.y));
+  hi = i8x8_to_half8(make_uint2(w.z, w.w));
+}
+
+template <bool I8>
+struct KTile {
+  half8 k[4];      // A operand of the 4 k-steps
+  uint4 kraw[2];   // int8: the two 16-byte loads the k operands come from
+  half8 v[4];      // fp16 V rows 4*(l/16) + r, dims (l%16)*8 .. +8
+  uint2 vraw[4];   // int8 V: the same rows and dims as 8 codes
+  uint16_t ksc[4], vsc[4];  // int8: the fp16 scales of keys 4*(l/16) .. +3
+};
+
+// The dims of k-step s a lane takes: fp16 K: 32s + 8*(l/16) .. +8 (one 16-byte load each); int8 K:
+// 64*(s/2) + 16*(l/16) + 8*(s%2) .. +8 (two 16-byte loads of 16 codes). Q's B operand follows the
+// same map, so the contraction sees every dim once.
+template <bool I8>
+__device__ __forceinline__ uint32_t kstep_dim(int s, int lane) {
+  return I8 ? 64 * (s >> 1) + 16 * (lane >> 4) + 8 * (s & 1) : 32 * s + 8 * (lane >> 4);
+}
+
+template <bool I8>
+__device__ __forceinline__ void load_ktile(KTile<I8> &t, const void *__restrict__ k, const void *__restrict__ v,
+                                           const uint16_t *__restrict__ ks, const uint16_t *__restrict__ vs,
+                                           size_t head_base, uint32_t key0, uint32_t rows, int lane) {
+  const size_t rk = head_base + min(key0 + (lane & 15), rows - 1);
+  if constexpr (I8) {
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      t.kraw[j] = load_stream((const uint4 *)((const int8_t *)k + rk * 128 + 64 * j + 16 * (lane >> 4)));
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const size_t rv = head_base + min(key0 + 4 * (lane >> 4) + r, rows - 1);
+      t.vraw[r] = *(const uint2 *)((const int8_t *)v + rv * 128 + (lane & 15) * 8);
+      t.ksc[r] = ks[rv];
+      t.vsc[r] = vs[rv];
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; s++) t.k[s] = half8_of(load_stream((const uint4 *)((const f16 *)k + rk * 128 + kstep_dim<false>(s, lane))));
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const size_t rv = head_base + min(key0 + 4 * (lane >> 4) + r, rows - 1);
+      t.v[r] = half8_of(load_stream((const uint4 *)((const f16 *)v + rv * 128 + (lane & 15) * 8)));
+    }
+  }
+}
+
+// One tile into the wave's running state: m, ls of head l%G (base 2, the same in the lane's 4 row
+// groups), acc[g][8] of dims (l%16)*8 .. +8 over the lane's row group's keys.
+template <int G, bool I8>
+__device__ __forceinline__ void attend_ktile(KTile<I8> &t, const half8 (&qb)[4], uint32_t key0, uint32_t end,
+                                             float scale_log2, int lane, float &m, float &ls, float (&acc)[G][8]) {
+  if constexpr (I8) {
+    i8x16_to_half8x2(t.kraw[0], t.k[0], t.k[1]);
+    i8x16_to_half8x2(t.kraw[1], t.k[2], t.k[3]);
+  }
+  floatx4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < 4; s++) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.k[s], qb[s], sc, 0, 0, 0);
+  const uint32_t kr = key0 + 4 * (lane >> 4);  // the lane's first key
+  float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, vsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  if constexpr (I8) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      ksc[r] = (float)__builtin_bit_cast(f16, t.ksc[r]);
+      vsc[r] = (float)__builtin_bit_cast(f16, t.vsc[r]);
+    }
+  }
+  float s2[4];
+  float tmax = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float x = sc[i] * scale_log2;
+    if constexpr (I8) x *= ksc[i];
+    s2[i] = kr + i < end ? x : -__builtin_inff();
+    tmax = fmaxf(tmax, s2[i]);
+  }
+  tmax = row_groups_max(tmax);
+  const float mnew = fmaxf(m, tmax);
+  const bool none = mnew == -__builtin_inff();  // no key seen yet
+  const float alpha = none ? 1.0f : exp2f(m - mnew);
+  float p[4], psum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    p[i] = none ? 0.0f : exp2f(s2[i] - mnew);
+    psum += p[i];
+  }
+  ls = ls * alpha + row_groups_sum(psum);
+  m = mnew;
+  float ag[G];
+  quad_heads<G>(alpha, ag);
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int d = 0; d < 8; d++) acc[g][d] *= ag[g];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    // a row past end was loaded from another row: zero it (p = 0 times NaN would be NaN)
+    const bool ok = kr + r < end;
+    half8 vr;
+    if constexpr (I8) vr = ok ? i8x8_to_half8(t.vraw[r]) : half8_of(make_uint4(0, 0, 0, 0));
+    else vr = ok ? t.v[r] : half8_of(make_uint4(0, 0, 0, 0));
+    float pg[G];
+    quad_heads<G>(I8 ? p[r] * vsc[r] : p[r], pg);
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+      for (int d = 0; d < 8; d++) acc[g][d] = fmaf(pg[g], (float)vr[d], acc[g][d]);
+  }
+}
+
+// Workgroup (kv head h, chunk c) of W waves over keys [c*chunk, min((c+1)*chunk, len)) (len plus *pos
+// when pos is given); wave w takes keys [c*chunk + w*kpw, +kpw) a tile at a time with the next tile's
+// loads in flight. With one chunk a head the workgroup writes out; otherwise its partial (o
+// unnormalized, m in natural-log units, l) per query head g to workspace slot (h*nchunk + c)*G + g,
+// with plain stores, for k_attn_merge.
 template <int G, bool I8, int W>
-__global__ __launch_bounds__(64 * W) void k_attn_decode(const uint4 *__restrict__ q, const void *__restrict__ k,
+__global__ __launch_bounds__(64 * W) void k_attn_decode(const f16 *__restrict__ q, const void *__restrict__ k,
                                                         const void *__restrict__ v, const uint16_t *__restrict__ ks,
                                                         const uint16_t *__restrict__ vs, float *__restrict__ ws_o,
                                                         float *__restrict__ ws_m, float *__restrict__ ws_l,
-                                                        void *__restrict__ out,
-                                                        int mode, const int32_t *__restrict__ pos, uint32_t len,
-                                                        uint32_t cap, uint32_t chunk, uint32_t nchunk,
-                                                        float scale_log2) {
+                                                        void *__restrict__ out, int mode, const int32_t *__restrict__ pos,
+                                                        uint32_t len, uint32_t cap, uint32_t chunk, uint32_t nchunk,
+                                                        uint32_t kpw, float scale_log2) {
   __shared__ float sm[W][G], sl[W][G];
   __shared__ float sacc[W][G][128];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t h = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
   if (pos) len += (uint32_t)*pos;  // the keys in use, read on the device (a replayed step graph)
-  const uint32_t begin = c * chunk;
-  const uint32_t end = begin + chunk < len ? begin + chunk : len;
+  const uint32_t begin = c * chunk, end = min(begin + chunk, len);
   const size_t head_base = (size_t)h * cap;
-
-  // A operand: query head lane%16, dims s*32 + (lane/16)*8 .. +8 (rows past G repeat head 0: their
-  // scores are never read)
-  half8 qa[4];
-  {
-    const int g = lane & 15, grp = lane >> 4;
+  const uint32_t kb = begin + wave * kpw, ke = min(kb + kpw, end);
+  const uint32_t nt = kb < ke ? (ke - kb + 15) / 16 : 0;
+  KTile<I8> ta, tb;
+  load_ktile<I8>(ta, k, v, ks, vs, head_base, kb, cap, lane);
+  load_ktile<I8>(tb, k, v, ks, vs, head_base, kb + 16, cap, lane);
+  half8 qb[4];
 #pragma unroll
-    for (int s = 0; s < 4; s++)
-      qa[s] = half8_of(q[((size_t)(h * G + (g < G ? g : 0)) * 128 + s * 32 + grp * 8) / 8]);
-  }
-  float acc[G][8], m[G], l[G];
-#pragma unroll
-  for (int g = 0; g < G; g++) {
-    m[g] = -__builtin_inff();
-    l[g] = 0.0f;
-#pragma unroll
-    for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
-  }
-  // this wave's tiles: begin + 16*wave + 16*W*j, two buffers in turn
-  constexpr uint32_t STEP = 16 * W;
-  Tile<I8> ta, tb;
-  const uint32_t key = begin + 16 * wave;
-  const uint32_t nt = key < end ? (end - key + STEP - 1) / STEP : 0;
-  auto load = [&](Tile<I8> &t, uint32_t k0) { load_tile<I8>(t, k, v, ks, vs, head_base, k0, cap, lane); };
-  load(ta, key);
-  load(tb, key + STEP);
-  run_tiles<G, I8, STEP>(ta, tb, key, nt, end, qa, scale_log2, lane, m, l, acc, load,
-                         [](Tile<I8> &, uint32_t) {});
-  // sum the four key slots of the wave (lanes lane%16 + 16j hold the same dims)
+  for (int s = 0; s < 4; s++) qb[s] = half8_of(*(const uint4 *)(q + ((size_t)h * G + (lane % G)) * 128 + kstep_dim<I8>(s, lane)));
+  float m = -__builtin_inff(), ls = 0.0f, acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
-    for (int d = 0; d < 8; d++) {
-      float a = acc[g][d];
-      a += __shfl_xor(a, 16, 64);
-      a += __shfl_xor(a, 32, 64);
-      acc[g][d] = a;
-    }
+    for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
+  uint32_t i = 0, key = kb;
+  for (; i + 3 < nt; i += 2, key += 32) {
+    attend_ktile<G, I8>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
+    load_ktile<I8>(ta, k, v, ks, vs, head_base, key + 32, cap, lane);
+    attend_ktile<G, I8>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
+    load_ktile<I8>(tb, k, v, ks, vs, head_base, key + 48, cap, lane);
+  }
+  const uint32_t rem = nt - i;  // 0 .. 3
+  if (rem >= 1) attend_ktile<G, I8>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
+  if (rem == 3) load_ktile<I8>(ta, k, v, ks, vs, head_base, key + 32, cap, lane);
+  if (rem >= 2) attend_ktile<G, I8>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
+  if (rem == 3) attend_ktile<G, I8>(ta, qb, key + 32, ke, scale_log2, lane, m, ls, acc);
+  // the 4 row groups hold the same dims for different keys (under one m): sum them
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int d = 0; d < 8; d++) acc[g][d] = row_groups_sum(acc[g][d]);
   if (lane < 16) {
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
       for (int d = 0; d < 8; d++) sacc[wave][g][lane * 8 + d] = acc[g][d];
   }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      sm[wave][g] = m[g];
-      sl[wave][g] = l[g];
-    }
+  if (lane < G) {
+    sm[wave][lane] = m;
+    sl[wave][lane] = ls;
   }
   __syncthreads();
   // the waves' states merged: weights 2^(m_w - top)
   const size_t base = ((size_t)h * nchunk + c) * G;
-  for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
-    const uint32_t g = i / 128, d = i % 128;
+  for (uint32_t t = threadIdx.x; t < (uint32_t)G * 128; t += 64 * W) {
+    const uint32_t g = t / 128, d = t % 128;
     float top = -__builtin_inff();
 #pragma unroll
     for (int w = 0; w < W; w++) top = fmaxf(top, sm[w][g]);
@@ -600,6 +766,65 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ o,
   }
 }
 
+// The merge of k_attn_decode's partials (the reference's Merge rule, paged.go:252-310): workgroup =
+// (query head, 64 dims), 4 waves = 4 chunk lanes x 64 dims. Every load is issued at once: each thread's
+// share of the o values (chunks cl, cl+4, ...) is in flight while the chunks' m and l go to LDS. Then
+// top = the largest m among chunks with l > 0, a chunk weighs w = exp(m - top) (0 for a chunk whose l
+// is not positive, which adds nothing whatever its o holds), and out = sum(w * o) / sum(w * l).
+template <int U>
+__global__ __launch_bounds__(256) void k_attn_merge_fast(const float *__restrict__ o, const float *__restrict__ m,
+                                                         const float *__restrict__ l, void *__restrict__ out,
+                                                         uint32_t chunks, uint32_t G, int mode) {
+  __shared__ float sm[kMaxChunks], sl[kMaxChunks];
+  __shared__ float red[2][4];
+  __shared__ float part[4][64];
+  const uint32_t row = blockIdx.x, t = threadIdx.x, lane = t & 63, cl = t >> 6;
+  const uint32_t d = blockIdx.y * 64 + lane;
+  const size_t base = (size_t)(row / G) * chunks * G + row % G;  // slot of chunk c: base + c*G
+  float ov[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) ov[u] = o[(base + (size_t)min(cl + 4 * u, chunks - 1) * G) * 128 + d];
+  for (uint32_t c = t; c < chunks; c += 256) {
+    sm[c] = m[base + (size_t)c * G];
+    sl[c] = l[base + (size_t)c * G];
+  }
+  __syncthreads();
+  float top = -__builtin_inff();
+  for (uint32_t c = t; c < chunks; c += 256)
+    if (sl[c] > 0.0f) top = fmaxf(top, sm[c]);
+  top = wave_max(top);
+  if (lane == 0) red[0][cl] = top;
+  __syncthreads();
+  top = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  float den = 0.0f;
+  for (uint32_t c = t; c < chunks; c += 256) {
+    const float w = (sl[c] > 0.0f && top != -__builtin_inff()) ? expf(sm[c] - top) : 0.0f;
+    den += w * sl[c];
+    sm[c] = w;  // the weight replaces m
+  }
+  den = group_sum<64>(den);
+  if (lane == 0) red[1][cl] = den;
+  __syncthreads();
+  den = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  float num = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint32_t c = cl + 4 * u;
+    const float w = c < chunks ? sm[c] : 0.0f;
+    num += w > 0.0f ? w * ov[u] : 0.0f;
+  }
+  for (uint32_t c = cl + 4 * U; c < chunks; c += 4) {  // chunks past the first 4*U: one load at a time
+    const float w = sm[c];
+    if (w > 0.0f) num += w * o[(base + (size_t)c * G) * 128 + d];
+  }
+  part[cl][lane] = num;
+  __syncthreads();
+  if (cl == 0) {
+    num = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+    store_out(out, (size_t)row * 128 + d, den > 0.0f ? num / den : 0.0f, mode);
+  }
+}
+
 // One wave a row of head_dim (<= 512) fp16 values: absmax over the row, scale rounded to fp16,
 // codes rounded to even against that scale.
 __global__ void k_kv_quantize_i8(const f16 *__restrict__ x, int8_t *__restrict__ q, f16 *__restrict__ scale,
@@ -624,20 +849,25 @@ __global__ void k_kv_quantize_i8(const f16 *__restrict__ x, int8_t *__restrict__
   }
 }
 
-// Keys per chunk: one chunk a head when the context is short (no merge launch), else about 1024
-// workgroups of 4 waves over the device; a multiple of 64 (a tile per wave), at most kMaxChunks
-// chunks a head.
-uint32_t pick_chunk(const hwk_attn_params *p) {
-  if (p->split) return p->split;
+// The split of hwk_attn_decode: workgroups of 4 waves, each wave kpw keys (a multiple of 16), chunk =
+// 4*kpw keys a workgroup. kpw is sized so that the launch runs about 2048 waves (8 a CU, each with two
+// tiles of loads in flight), between 32 and 256 keys, more when a head would exceed kMaxChunks chunks.
+// A caller's split (a multiple of 64) is the chunk.
+constexpr int kDecodeWaves = 4;
+
+uint32_t pick_kpw(const hwk_attn_params *p) {
+  if (p->split) return p->split / kDecodeWaves;
   const uint64_t keys = (uint64_t)p->len * p->kv_heads;
-  if (keys <= 512) return p->len ? (p->len + 63) / 64 * 64 : 64;
-  uint64_t s = (keys + 1023) / 1024;
-  s = (s + 63) / 64 * 64;
-  if (s < 64) s = 64;
-  const uint64_t min_chunk = ((uint64_t)p->len + kMaxChunks - 1) / kMaxChunks;
-  if (s < min_chunk) s = (min_chunk + 63) / 64 * 64;
-  return (uint32_t)s;
+  uint64_t kpw = (keys + 2047) / 2048;
+  kpw = (kpw + 15) / 16 * 16;
+  if (kpw < 32) kpw = 32;
+  if (kpw > 256) kpw = 256;
+  const uint64_t min_kpw = ((uint64_t)p->len + (uint64_t)kMaxChunks * kDecodeWaves - 1) / ((uint64_t)kMaxChunks * kDecodeWaves);
+  if (kpw < min_kpw) kpw = (min_kpw + 15) / 16 * 16;
+  return (uint32_t)kpw;
 }
+
+uint32_t pick_chunk(const hwk_attn_params *p) { return pick_kpw(p) * kDecodeWaves; }
 
 uint32_t chunks_of(const hwk_attn_params *p, uint32_t chunk) { return p->len ? (p->len + chunk - 1) / chunk : 1; }
 
@@ -677,8 +907,8 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
   HWK_CHECK(p->out_mode == HWK_OUT_F32 || p->out_mode == HWK_OUT_F16, "hwk_attn_decode: out_mode %u", p->out_mode);
   HWK_CHECK(p->split % 64 == 0, "hwk_attn_decode: split %u is not a multiple of 64", p->split);
   HWK_CHECK(hwk::aligned(q, 16) && hwk::aligned(workspace, 16), "hwk_attn_decode: q and workspace 16-byte aligned");
-  HWK_CHECK(p->kv_int8 ? (hwk::aligned(k, 8) && hwk::aligned(v, 8)) : (hwk::aligned(k, 16) && hwk::aligned(v, 16)),
-            "hwk_attn_decode: k, v misaligned");
+  HWK_CHECK(p->kv_int8 ? (hwk::aligned(k, 16) && hwk::aligned(v, 8)) : (hwk::aligned(k, 16) && hwk::aligned(v, 16)),
+            "hwk_attn_decode: k, v misaligned (k 16-byte aligned; v 16-byte for fp16, 8-byte for int8)");
   const size_t need = hwk_attn_workspace_bytes(p);
   HWK_CHECK(workspace_bytes >= need, "hwk_attn_decode: workspace %zu bytes, %zu needed", workspace_bytes, need);
   const uint32_t chunk = pick_chunk(p);
@@ -691,17 +921,18 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
   HWK_CHECK(!pos || p->len == p->capacity, "attn_decode_dev: a device length needs the grid of the capacity");
   const uint32_t len = pos ? len_add : p->len;
-  constexpr int W = 4;
+  constexpr int W = kDecodeWaves;
+  const uint32_t kpw = chunk / W;
   const dim3 grid(p->kv_heads * nchunk), block(64 * W);
   const uint16_t *ks = (const uint16_t *)k_scale, *vs = (const uint16_t *)v_scale;
   const int mode = (int)p->out_mode;
-#define HWK_ATTN_LAUNCH(GG)                                                                                         \
-  if (p->kv_int8)                                                                                                   \
-    hipLaunchKernelGGL((k_attn_decode<GG, true, W>), grid, block, 0, st, (const uint4 *)q, k, v, ks, vs, ws_o,     \
-                       ws_m, ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, scale_log2);               \
-  else                                                                                                              \
-    hipLaunchKernelGGL((k_attn_decode<GG, false, W>), grid, block, 0, st, (const uint4 *)q, k, v, ks, vs, ws_o,    \
-                       ws_m, ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, scale_log2);
+#define HWK_ATTN_LAUNCH(GG)                                                                                          \
+  if (p->kv_int8)                                                                                                    \
+    hipLaunchKernelGGL((k_attn_decode<GG, true, W>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,   \
+                       ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, kpw, scale_log2);                      \
+  else                                                                                                               \
+    hipLaunchKernelGGL((k_attn_decode<GG, false, W>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,  \
+                       ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, kpw, scale_log2);
   if (G == 1) {
     HWK_ATTN_LAUNCH(1)
   } else if (G == 2) {
@@ -712,8 +943,10 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
 #undef HWK_ATTN_LAUNCH
   if (char *err = hwk::launched("hwk_attn_decode")) return err;
   if (nchunk == 1) return nullptr;
-  hipLaunchKernelGGL((k_attn_merge<true>), dim3(p->heads, 4), dim3(256), 0, st, ws_o, ws_m, ws_l, out, nchunk,
-                     p->heads, 128u, G, mode);
+  if (nchunk <= 4 * 16)
+    hipLaunchKernelGGL((k_attn_merge_fast<16>), dim3(p->heads, 2), dim3(256), 0, st, ws_o, ws_m, ws_l, out, nchunk, G, mode);
+  else
+    hipLaunchKernelGGL((k_attn_merge_fast<32>), dim3(p->heads, 2), dim3(256), 0, st, ws_o, ws_m, ws_l, out, nchunk, G, mode);
   return hwk::launched("hwk_attn_decode (merge)");
 }
 
