@@ -43,141 +43,6 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint2 w) {
   return out;
 }
 
-template <bool I8>
-struct Tile {
-  half8 k[4];  // B operand of the 4 MFMA k-steps: key lane%16, dims s*32 + (lane/16)*8 .. +8
-  half8 v[4];  // V rows: key 4r + lane/16, dims (lane%16)*8 .. +8
-  float kscale;
-  float vscale[4];
-};
-
-// Loads tile keys [key0, key0+16) of the kv head whose rows start at head_base. Every load is issued
-// unconditionally, keys at or past `rows` (the head's rows in memory) reading row rows-1 instead:
-// a predicated load would make the compiler wait for it before the next one is issued. The values
-// of keys past the attended range are dropped by attend_tile.
-template <bool I8>
-__device__ __forceinline__ void load_tile(Tile<I8> &t, const void *__restrict__ k, const void *__restrict__ v,
-                                          const uint16_t *__restrict__ ks, const uint16_t *__restrict__ vs,
-                                          size_t head_base, uint32_t key0, uint32_t rows, int lane) {
-  const uint32_t kk = min(key0 + (lane & 15), rows - 1);
-  const int grp = lane >> 4;
-#pragma unroll
-  for (int s = 0; s < 4; s++) {
-    const size_t row = head_base + kk;
-    if constexpr (I8) {
-      t.k[s] = i8x8_to_half8(*(const uint2 *)((const uint8_t *)k + row * 128 + s * 32 + grp * 8));
-    } else {
-      t.k[s] = half8_of(load_stream((const uint4 *)((const f16 *)k + row * 128 + s * 32 + grp * 8)));
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const size_t row = head_base + min(key0 + 4 * r + grp, rows - 1);
-    if constexpr (I8) {
-      t.v[r] = i8x8_to_half8(*(const uint2 *)((const uint8_t *)v + row * 128 + (lane & 15) * 8));
-      t.vscale[r] = (float)__builtin_bit_cast(f16, vs[row]);
-    } else {
-      t.v[r] = half8_of(load_stream((const uint4 *)((const f16 *)v + row * 128 + (lane & 15) * 8)));
-    }
-  }
-  if constexpr (I8) t.kscale = (float)__builtin_bit_cast(f16, ks[head_base + kk]);
-}
-
-__device__ __forceinline__ float max16(float x) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
-  return x;
-}
-
-__device__ __forceinline__ float sum16(float x) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
-}
-
-__device__ __forceinline__ float uniform(float x) {
-  return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(x)));
-}
-
-// One tile into the wave's running softmax state (m, l wave-uniform, base 2; acc per lane).
-template <int G, bool I8>
-__device__ __forceinline__ void attend_tile(const Tile<I8> &t, const half8 (&qa)[4], uint32_t key0, uint32_t end,
-                                            float scale_log2, int lane, float (&m)[G], float (&l)[G],
-                                            float (&acc)[G][8]) {
-  floatx4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int s = 0; s < 4; s++) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], t.k[s], sc, 0, 0, 0);
-  const bool valid = key0 + (lane & 15) < end;
-  float p[G];
-#pragma unroll
-  for (int g = 0; g < G; g++) {
-    float s2 = sc[g] * scale_log2;
-    if constexpr (I8) s2 *= t.kscale;
-    s2 = valid ? s2 : -__builtin_inff();
-    const float mnew = fmaxf(m[g], uniform(max16(s2)));  // lanes 0..15 hold the head rows
-    float alpha = 1.0f;
-    if (mnew == -__builtin_inff()) {
-      p[g] = 0.0f;
-    } else {
-      alpha = exp2f(m[g] - mnew);
-      p[g] = exp2f(s2 - mnew);
-    }
-    l[g] = l[g] * alpha + uniform(sum16(lane < 16 ? p[g] : 0.0f));
-    m[g] = mnew;
-    if (alpha != 1.0f) {
-#pragma unroll
-      for (int d = 0; d < 8; d++) acc[g][d] *= alpha;
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int src = 4 * r + (lane >> 4);
-    // a row past end was loaded from another row (load_tile): zero it, as p = 0 times NaN is NaN
-    const bool vok = key0 + (uint32_t)src < end;
-    const half8 vr = vok ? t.v[r] : half8_of(make_uint4(0, 0, 0, 0));
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      float pv = __shfl(p[g], src, 64);
-      if constexpr (I8) pv *= vok ? t.vscale[r] : 0.0f;
-#pragma unroll
-      for (int d = 0; d < 8; d++) acc[g][d] = fmaf(pv, (float)vr[d], acc[g][d]);
-    }
-  }
-}
-
-// Attends a wave's nt tiles at key, key + STEP, ... whose first two loads are already in ta and tb
-// (issued unconditionally by the caller). While four or more tiles remain, each buffer takes the
-// load two tiles ahead as soon as it is attended; those loads sit in a loop body of its own with no
-// branch around them, so the wait counter keeps both buffers in flight. The last one to three
-// tiles load at most once more. prep(tile, key0) runs on a tile's registers before it is attended.
-template <int G, bool I8, uint32_t STEP, class Load, class Prep>
-__device__ __forceinline__ void run_tiles(Tile<I8> &ta, Tile<I8> &tb, uint32_t key, uint32_t nt, uint32_t end,
-                                          const half8 (&qa)[4], float scale_log2, int lane, float (&m)[G],
-                                          float (&l)[G], float (&acc)[G][8], Load load, Prep prep) {
-  uint32_t i = 0;
-  for (; i + 3 < nt; i += 2, key += 2 * STEP) {
-    prep(ta, key);
-    attend_tile<G, I8>(ta, qa, key, end, scale_log2, lane, m, l, acc);
-    load(ta, key + 2 * STEP);
-    prep(tb, key + STEP);
-    attend_tile<G, I8>(tb, qa, key + STEP, end, scale_log2, lane, m, l, acc);
-    load(tb, key + 3 * STEP);
-  }
-  const uint32_t rem = nt - i;  // 0 .. 3
-  if (rem == 0) return;
-  prep(ta, key);
-  attend_tile<G, I8>(ta, qa, key, end, scale_log2, lane, m, l, acc);
-  if (rem == 3) load(ta, key + 2 * STEP);
-  if (rem >= 2) {
-    prep(tb, key + STEP);
-    attend_tile<G, I8>(tb, qa, key + STEP, end, scale_log2, lane, m, l, acc);
-  }
-  if (rem == 3) {
-    prep(ta, key + 2 * STEP);
-    attend_tile<G, I8>(ta, qa, key + 2 * STEP, end, scale_log2, lane, m, l, acc);
-  }
-}
-
 // ---- K4, the split-K decode attention of hwk_attn_decode ----
 //
 // A lane's view of a 16-key tile:
@@ -444,82 +309,41 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const f16 *__restrict__ 
     }
   }
 }
-// The model's decode attention for the token at position p = *pos. NSPLIT workgroups of W waves a
-// kv head each take a contiguous share of the capacity; those whose share starts past p leave at
-// once. Prologue: q for the kv head's G query heads comes from the fp32 projection qkv (heads + 2 *
-// kvh rows of 128) through the per-head RMSNorm and RoPE; the workgroup whose share holds p (the
-// owner) also makes the new k (normed, rotated) and v, writes them to the caches at p for later
-// steps and keeps them in LDS: the tile holding p replaces what its load of row p returned with the
-// LDS copy, so the owner's keys wait on no store. Every workgroup merges its waves in LDS and
-// leaves its partial (o unnormalized, m in natural-log units, l) in the workspace; the last of the
-// kv head's live workgroups to arrive (a counter a kv head, a single thread's release and acquire
-// fences) merges them with the rule of the reference's Merge into out (fp16), one wave reduction a
-// query head over the partials (a lane a partial) with every partial's o already in flight, and
-// clears the counter for the next call. LAST = false is the form for long caches: every workgroup
-// leaves its partial (an empty one past p) for k_attn_merge, with no counter.
-// A workspace store / load, device-coherent (past the XCD's L2) when COH.
-template <bool COH>
-__device__ __forceinline__ void ws_put(float *p, float v) {
-  if (COH)
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else
-    *p = v;
-}
-__device__ __forceinline__ float ws_get(const float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-constexpr uint32_t kHeadSplit = 64;  // most workgroups a kv head (a lane each in the merge)
-
-// Row p = key0 + j of a tile from LDS (k as the MFMA B operand layout, v as the P.V layout).
-__device__ __forceinline__ void patch_row(Tile<false> &t, uint32_t j, const f16 *kn16, const f16 *vn16, int lane) {
-  const int grp = lane >> 4;
-  if ((uint32_t)(lane & 15) == j) {
-#pragma unroll
-    for (int s2 = 0; s2 < 4; s2++) t.k[s2] = *(const half8 *)&kn16[s2 * 32 + grp * 8];
-  }
-#pragma unroll
-  for (int r = 0; r < 4; r++)
-    if ((uint32_t)(4 * r + grp) == j) t.v[r] = *(const half8 *)&vn16[(lane & 15) * 8];
-}
-
-template <int G, int W, bool LAST>
-__global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ qkv, const float *__restrict__ qn,
+// ---- the model's decode attention (K4m): k_attn_decode's tiles with the step's own q, k, v ----
+//
+// Workgroup (kv head h, chunk c) of W waves over the keys [c*chunk, min((c+1)*chunk, p+1)) for the token
+// at position p = *pos; the grid covers the cache's capacity and a workgroup whose chunk starts past p
+// leaves at once (the consumer reads only chunks 0 .. p/chunk). Prologue: q for the kv head's G query
+// heads comes from the fp32 projection qkv (heads + 2*kvh rows of 128) through the per-head RMSNorm and
+// RoPE; the workgroup whose chunk holds p (the owner) also makes the new k (normed, rotated) and v,
+// writes them to the caches at p for later steps and keeps them in LDS: the tile holding p takes them
+// from there in place of its load of row p, so the owner waits on no store. The prologue's loads go
+// out first, then the waves' first tiles (loads complete in issue order for the wait counter). Each
+// workgroup leaves its partial (o unnormalized, m in natural-log units, l) per query head with plain
+// stores at slot (h*nchunk + c)*G + g; the o_proj GEMV merges them (mxfp4_gemv_x's X_MERGE).
+template <int G, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ qkv, const float *__restrict__ qn,
                                                       const float *__restrict__ kn, const float *__restrict__ cos_t,
-                                                      const float *__restrict__ sin_t, double eps,
-                                                      f16 *__restrict__ kc, f16 *__restrict__ vc,
-                                                      f16 *__restrict__ out, float *__restrict__ ws_o,
+                                                      const float *__restrict__ sin_t, double eps, f16 *__restrict__ kc,
+                                                      f16 *__restrict__ vc, float *__restrict__ ws_o,
                                                       float *__restrict__ ws_m, float *__restrict__ ws_l,
-                                                      uint32_t *__restrict__ counters, const int32_t *__restrict__ pos,
-                                                      uint32_t heads, uint32_t kvh, uint32_t cap, uint32_t chunk,
-                                                      uint32_t nsplit, float scale_log2) {
+                                                      const int32_t *__restrict__ pos, uint32_t heads, uint32_t kvh,
+                                                      uint32_t cap, uint32_t chunk, uint32_t nchunk, uint32_t kpw,
+                                                      float scale_log2) {
   __shared__ float sm[W][G], sl[W][G];
   __shared__ float sacc[W][G][128];
   __shared__ __attribute__((aligned(16))) f16 qs[G][128];
   __shared__ __attribute__((aligned(16))) f16 knew[128], vnew[128];
-  __shared__ bool last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t h = blockIdx.x / nsplit, c = blockIdx.x % nsplit;
+  const uint32_t h = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
   const uint32_t p = (uint32_t)*pos, len = p + 1;
   const uint32_t begin = c * chunk;
-  if (begin >= len) {  // no keys in use here: no partial, no arrival (LAST), else an empty partial
-    if (!LAST) {
-      const size_t slot0 = ((size_t)h * nsplit + c) * G;
-      for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) ws_o[slot0 * 128 + i] = 0.0f;
-      if (threadIdx.x < G) {
-        ws_m[slot0 + threadIdx.x] = -__builtin_inff();
-        ws_l[slot0 + threadIdx.x] = 0.0f;
-      }
-    }
-    return;
-  }
-  const bool owner = p - begin < chunk;  // the share holds p (begin <= p)
+  if (begin >= len) return;
+  const bool owner = p - begin < chunk;  // the chunk holds p (begin <= p)
   const uint32_t end = owner ? len : begin + chunk;
   const size_t head_base = (size_t)h * cap;
-  constexpr uint32_t STEP = 16 * W;
-  // The prologue's loads go out first (wave j makes job j: query head j < G, then k, then v), then
-  // the wave's first two tiles (a share of up to 32*W keys in flight while q is made): loads
-  // complete in issue order for the wait counter, so q waits only on its own loads.
+  // prologue jobs: wave j makes job j (query head j < G, then k, then v); a wave past the jobs repeats
+  // the last one and keeps nothing, so that every wave's loads are issued before its tile loads
   const uint32_t jobs = owner ? G + 2 : G;
   const uint32_t j0 = (uint32_t)wave < jobs ? (uint32_t)wave : jobs - 1;
   auto job_row = [&](uint32_t j) { return j < G ? h * G + j : j == G ? heads + h : heads + kvh + h; };
@@ -528,14 +352,11 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
   const float nw0 = nwp[lane], nw1 = nwp[lane + 64];
   const float cp = cos_t[(size_t)p * 64 + lane], sp = sin_t[(size_t)p * 64 + lane];
   issue_order();
-  Tile<false> ta, tb;
-  const uint32_t key = begin + 16 * wave;
-  // issued whether or not the wave has keys (past the cache end a load reads the last row): a
-  // load under a branch makes the wait counter assume the shorter path's count
-  load_tile<false>(ta, kc, vc, nullptr, nullptr, head_base, key, cap, lane);
-  load_tile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + STEP, cap, lane);
-  // every wave runs its job's arithmetic (a wave past the jobs repeats the last and stores
-  // nothing), so that no load above is moved into a branch below the tile loads
+  const uint32_t kb = begin + wave * kpw, ke = min(kb + kpw, end);
+  const uint32_t nt = kb < ke ? (ke - kb + 15) / 16 : 0;
+  KTile<false> ta, tb;
+  load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, kb, cap, lane);
+  load_ktile<false>(tb, kc, vc, nullptr, nullptr, head_base, kb + 16, cap, lane);
   auto make_job = [&](uint32_t j, float a0, float a1, float w0, float w1, bool keep) {
     float o0, o1;
     head_norm_rope(a0, a1, w0, w1, cp, sp, eps, o0, o1);
@@ -562,53 +383,67 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
              nj[lane + 64], true);
   }
   __syncthreads();  // q, and the owner's new k/v, in LDS
-  half8 qa[4];
-  {
-    const int g = lane & 15, grp = lane >> 4;
+  half8 qb[4];
 #pragma unroll
-    for (int s2 = 0; s2 < 4; s2++)
-      qa[s2] = g < G ? *(const half8 *)&qs[g][s2 * 32 + grp * 8] : half8_of(make_uint4(0, 0, 0, 0));
-  }
-  float acc[G][8], m[G], l[G];
+  for (int s = 0; s < 4; s++) qb[s] = *(const half8 *)&qs[lane % G][kstep_dim<false>(s, lane)];
+  // the owner's tile holding p takes row p from LDS
+  auto patch = [&](KTile<false> &t, uint32_t key0) {
+    if (!owner || p - key0 >= 16) return;
+    const uint32_t j = p - key0;
+    if ((uint32_t)(lane & 15) == j) {
 #pragma unroll
-  for (int g = 0; g < G; g++) {
-    m[g] = -__builtin_inff();
-    l[g] = 0.0f;
+      for (int s = 0; s < 4; s++) t.k[s] = *(const half8 *)&knew[kstep_dim<false>(s, lane)];
+    }
 #pragma unroll
-    for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
-  }
-  run_tiles<G, false, STEP>(
-      ta, tb, key, key < end ? (end - key + STEP - 1) / STEP : 0, end, qa, scale_log2, lane, m, l, acc,
-      [&](Tile<false> &t, uint32_t k0) { load_tile<false>(t, kc, vc, nullptr, nullptr, head_base, k0, cap, lane); },
-      [&](Tile<false> &t, uint32_t k0) {
-        if (owner && p - k0 < 16) patch_row(t, p - k0, knew, vnew, lane);
-      });
+    for (int r = 0; r < 4; r++)
+      if ((uint32_t)(4 * (lane >> 4) + r) == j) t.v[r] = *(const half8 *)&vnew[(lane & 15) * 8];
+  };
+  float m = -__builtin_inff(), ls = 0.0f, acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
-    for (int d = 0; d < 8; d++) {
-      float a = acc[g][d];
-      a += __shfl_xor(a, 16, 64);
-      a += __shfl_xor(a, 32, 64);
-      acc[g][d] = a;
-    }
+    for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
+  uint32_t i = 0, key = kb;
+  for (; i + 3 < nt; i += 2, key += 32) {
+    patch(ta, key);
+    attend_ktile<G, false>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
+    load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
+    patch(tb, key + 16);
+    attend_ktile<G, false>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
+    load_ktile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + 48, cap, lane);
+  }
+  const uint32_t rem = nt - i;  // 0 .. 3
+  if (rem >= 1) {
+    patch(ta, key);
+    attend_ktile<G, false>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
+  }
+  if (rem == 3) load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
+  if (rem >= 2) {
+    patch(tb, key + 16);
+    attend_ktile<G, false>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
+  }
+  if (rem == 3) {
+    patch(ta, key + 32);
+    attend_ktile<G, false>(ta, qb, key + 32, ke, scale_log2, lane, m, ls, acc);
+  }
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int d = 0; d < 8; d++) acc[g][d] = row_groups_sum(acc[g][d]);
   if (lane < 16) {
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
       for (int d = 0; d < 8; d++) sacc[wave][g][lane * 8 + d] = acc[g][d];
   }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      sm[wave][g] = m[g];
-      sl[wave][g] = l[g];
-    }
+  if (lane < G) {
+    sm[wave][lane] = m;
+    sl[wave][lane] = ls;
   }
   __syncthreads();
-  const size_t base = ((size_t)h * nsplit + c) * G;
-  for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
-    const uint32_t g = i / 128, d = i % 128;
+  const size_t base = ((size_t)h * nchunk + c) * G;
+  for (uint32_t t = threadIdx.x; t < (uint32_t)G * 128; t += 64 * W) {
+    const uint32_t g = t / 128, d = t % 128;
     float top = -__builtin_inff();
 #pragma unroll
     for (int w = 0; w < W; w++) top = fmaxf(top, sm[w][g]);
@@ -621,89 +456,28 @@ __global__ __launch_bounds__(64 * W) void k_attn_head(const float *__restrict__ 
         lsum += wt * sl[w][g];
       }
     }
-    if (LAST && nsplit == 1) {
-      out[(size_t)(h * G + g) * 128 + d] = (f16)f32_value(lsum > 0.0f ? o / lsum : 0.0f);
-    } else {
-      // LAST: the partials are stored coherent at device scope (past the XCD's L2), so that the
-      // last workgroup reads them with no L2 write-back on the writer's side
-      ws_put<LAST>(&ws_o[(base + g) * 128 + d], o);
-      if (d == 0) {
-        ws_put<LAST>(&ws_m[base + g], top * kLn2);
-        ws_put<LAST>(&ws_l[base + g], lsum);
-      }
+    ws_o[(base + g) * 128 + d] = o;
+    if (d == 0) {
+      ws_m[base + g] = top * kLn2;
+      ws_l[base + g] = lsum;
     }
   }
-  if (!LAST || nsplit == 1) return;
-  const uint32_t live = p / chunk + 1;  // workgroups of this kv head that hold keys
-  // Every wave waits for its partial's stores to be acknowledged (device-coherent stores: then
-  // visible to every CU); after the barrier one thread counts the workgroup in. The counter is a
-  // device-scope atomic; the last arrival's reads are device-coherent loads, which see the
-  // acknowledged stores without an L2 invalidate.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(&counters[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == live - 1;
-  __syncthreads();
-  if (!last) return;
-  // A wave's 64 outputs share one query head g0: lane cc holds partial cc's m and l, and the wave's
-  // outputs load every partial's o (U at a time, a partial past the live ones reading the last
-  // live one, weighted 0) while the weights exp(m - top) are reduced.
-  const size_t b0 = (size_t)h * nsplit * G;
-  constexpr uint32_t U = 16;
-  const uint32_t lastc = live - 1;
-  for (uint32_t i = threadIdx.x; i < (uint32_t)G * 128; i += 64 * W) {
-    const uint32_t g0 = i / 128, d0 = i % 128;
-    float ov[U];
-#pragma unroll
-    for (uint32_t u = 0; u < U; u++) ov[u] = ws_get(&ws_o[(b0 + min(u, lastc) * G + g0) * 128 + d0]);
-    const uint32_t cl = min((uint32_t)lane, lastc);
-    const bool mine = (uint32_t)lane < live;
-    float mc = ws_get(&ws_m[b0 + cl * G + g0]), lc = ws_get(&ws_l[b0 + cl * G + g0]);
-    if (!mine) {
-      mc = -__builtin_inff();
-      lc = 0.0f;
-    }
-    const float top = wave_max(lc > 0.0f ? mc : -__builtin_inff());
-    const float wc = (lc > 0.0f && top != -__builtin_inff()) ? expf(mc - top) : 0.0f;
-    const float den = group_sum<64>(wc * lc);
-    float num = 0.0f;
-    // a partial of weight 0 adds nothing, whatever its o holds (0 * NaN would be NaN)
-#pragma unroll
-    for (uint32_t u = 0; u < U; u++) {
-      const float wu = __shfl(wc, u, 64);
-      num += wu > 0.0f ? wu * ov[u] : 0.0f;
-    }
-    for (uint32_t cc = U; cc < live; cc += U) {
-#pragma unroll
-      for (uint32_t u = 0; u < U; u++) ov[u] = ws_get(&ws_o[(b0 + min(cc + u, lastc) * G + g0) * 128 + d0]);
-#pragma unroll
-      for (uint32_t u = 0; u < U; u++) {
-        const float wu = __shfl(wc, (cc + u) & 63, 64);
-        num += wu > 0.0f ? wu * ov[u] : 0.0f;
-      }
-    }
-    out[(size_t)(h * G + g0) * 128 + d0] = (f16)f32_value(den > 0.0f ? num / den : 0.0f);
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(&counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Merge of chunks (the reference's Merge rule, paged.go:252-310): top = the largest m among
 // chunks with l > 0; a chunk weighs exp(m - top), times l when its o is normalized; out = the
 // weighted sum of o over the weighted sum of l. Block (row, slice of 32 dims) of 256 threads: the
 // chunks' weights go to LDS first (one pass of independent loads), then 8 chunk lanes x 32 dims
-// sum o in batches of independent loads. INTERNAL reads the workspace of k_attn_decode (row = query
-// head, chunk c of kv head row/G at slot ((row/G)*chunks + c)*G + row%G, o unnormalized).
-template <bool INTERNAL>
+// sum o in batches of independent loads. o (chunks, rows, dim) normalized per chunk, m and l (chunks,
+// rows): hwk_attn_merge's layout.
 __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ o, const float *__restrict__ m,
                                                     const float *__restrict__ l, void *__restrict__ out,
-                                                    uint32_t chunks, uint32_t rows, uint32_t dim, uint32_t G,
-                                                    int mode) {
+                                                    uint32_t chunks, uint32_t rows, uint32_t dim, int mode) {
   __shared__ float wgt[kMaxChunks];
   __shared__ float red[256];
   const uint32_t row = blockIdx.x, t = threadIdx.x;
   const uint32_t d = blockIdx.y * 32 + (t & 31), cl = t >> 5;
-  const size_t base = INTERNAL ? (size_t)(row / G) * chunks * G + row % G : row;
-  const size_t stride = INTERNAL ? G : rows;
+  const size_t base = row, stride = rows;
   float top = -__builtin_inff();
   for (uint32_t c = t; c < chunks; c += 256) {
     const size_t i = base + c * stride;
@@ -724,9 +498,8 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ o,
     const float lc = wgt[c];
     float w = 0.0f;
     if (lc > 0.0f && top != -__builtin_inff()) {
-      w = expf(m[base + c * stride] - top);
-      if (!INTERNAL) w *= lc;
-      den += INTERNAL ? w * lc : w;
+      w = expf(m[base + c * stride] - top) * lc;
+      den += w;
     }
     wgt[c] = w;
   }
@@ -951,124 +724,51 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
 }
 
 
-// Tuning knobs read once a process: HWK_ATTN_KEYS, the keys a workgroup takes at the cache's capacity
-// (default 128); HWK_ATTN_W, waves a workgroup (2, 4, 8 or 16; default 4). The defaults are the
-// fastest decode step of the 28-layer model at 1,040-1,290 positions (swept 32-256 keys, 2-8 waves).
-static int attn_env(const char *name, int dflt) {
-  const char *v = getenv(name);
-  return v ? atoi(v) : dflt;
-}
+// The model step's split: 4 waves a workgroup, kpw keys a wave (32: two tiles, both in flight), chunk =
+// 4*kpw keys; kpw grows past 32 so that a kv head has at most kStepMaxChunks chunks (the o_proj GEMV
+// merges every chunk's partial in its prologue).
+constexpr int kStepWaves = 4;
+constexpr uint32_t kStepMaxChunks = 16;
 
-static uint32_t attn_keys() {
-  static uint32_t k = [] {
-    const int v = attn_env("HWK_ATTN_KEYS", 128);
-    return (uint32_t)(v < 16 ? 16 : v > 65536 ? 65536 : v);
-  }();
-  return k;
-}
-
-static int attn_waves() {
-  static int w = [] {
-    const int v = attn_env("HWK_ATTN_W", 4);
-    return v == 2 || v == 8 || v == 16 ? v : 4;
-  }();
-  return w;
-}
-
-uint32_t hwk::attn_head_split(const hwk_attn_params *p) {
-  const uint32_t n = (p->capacity + attn_keys() - 1) / attn_keys();
-  return n < 1 ? 1 : n > kHeadSplit ? kHeadSplit : n;
-}
-
-size_t hwk::attn_head_workspace_bytes(const hwk_attn_params *p) {
-  return (size_t)p->heads * attn_head_split(p) * (128 + 2) * sizeof(float);
-}
-
-char *hwk::attn_head(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *cos_t,
-                     const float *sin_t, double eps, void *kc, void *vc, void *out, void *workspace,
-                     size_t workspace_bytes, uint32_t *counters, const hwk_attn_params *p, const int32_t *pos) {
-  HWK_CHECK(p && qkv && qn && kn && cos_t && sin_t && kc && vc && out && workspace && counters && pos,
-            "attn_head: null argument");
-  HWK_CHECK(p->head_dim == 128 && !p->kv_int8, "attn_head: fp16 caches of head_dim 128 only");
-  HWK_CHECK(p->kv_heads > 0 && p->heads % p->kv_heads == 0, "attn_head: %u heads over %u", p->heads, p->kv_heads);
-  const uint32_t G = p->heads / p->kv_heads;
-  HWK_CHECK(G == 1 || G == 2 || G == 4, "attn_head: %u query heads a kv head", G);
-  HWK_CHECK(workspace_bytes >= attn_head_workspace_bytes(p), "attn_head: workspace too small");
-  const uint32_t nsplit = attn_head_split(p), chunk = (p->capacity + nsplit - 1) / nsplit;
-  const uint64_t slots = (uint64_t)p->heads * nsplit;
-  float *ws_o = (float *)workspace, *ws_m = ws_o + slots * 128, *ws_l = ws_m + slots;
-  const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
-#define HWK_AH(GG, W)                                                                                             \
-  hipLaunchKernelGGL((k_attn_head<GG, W, true>), dim3(p->kv_heads * nsplit), dim3(64 * W), 0, st, qkv, qn, kn,     \
-                     cos_t, sin_t, eps, (f16 *)kc, (f16 *)vc, (f16 *)out, ws_o, ws_m, ws_l, counters, pos,        \
-                     p->heads,                                                                                    \
-                     p->kv_heads, p->capacity, chunk, nsplit, scale_log2)
-#define HWK_AHW(GG)                  \
-  switch (attn_waves()) {            \
-    case 2: HWK_AH(GG, 2); break;    \
-    case 8: HWK_AH(GG, 8); break;    \
-    case 16: HWK_AH(GG, 16); break;  \
-    default: HWK_AH(GG, 4); break;   \
-  }
-  if (G == 1) {
-    HWK_AHW(1)
-  } else if (G == 2) {
-    HWK_AHW(2)
-  } else {
-    HWK_AHW(4)
-  }
-#undef HWK_AHW
-#undef HWK_AH
-  return hwk::launched("attn_head");
-}
-
-uint32_t hwk::attn_step_chunks(const hwk_attn_params *p) {
-  // about 8192 keys a chunk, at least 8 chunks a kv head (at most 64), a multiple of 128 keys
-  uint32_t n = (uint32_t)(((uint64_t)p->capacity * p->kv_heads + 8191) / 8192);
-  n = n < 8 ? 8 : n > 64 ? 64 : n;
-  uint32_t chunk = (p->capacity + n - 1) / n;
-  chunk = (chunk + 127) / 128 * 128;
-  return chunk;
+void hwk::attn_step_layout(const hwk_attn_params *p, uint32_t *chunk, uint32_t *nchunk) {
+  uint32_t kpw = 32;
+  const uint32_t need = (p->capacity + kStepWaves * kStepMaxChunks - 1) / (kStepWaves * kStepMaxChunks);
+  if (kpw < need) kpw = (need + 15) / 16 * 16;
+  *chunk = kpw * kStepWaves;
+  *nchunk = (p->capacity + *chunk - 1) / *chunk;
 }
 
 size_t hwk::attn_step_workspace_bytes(const hwk_attn_params *p) {
-  const uint32_t chunk = attn_step_chunks(p), nchunk = (p->capacity + chunk - 1) / chunk;
+  uint32_t chunk, nchunk;
+  attn_step_layout(p, &chunk, &nchunk);
   return (size_t)p->heads * nchunk * (128 + 2) * sizeof(float);
 }
 
-char *hwk::attn_decode_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *cos_t,
-                            const float *sin_t, double eps, void *kc, void *vc, void *workspace, size_t workspace_bytes,
-                            const hwk_attn_params *p, const int32_t *pos, uint32_t *nchunk_out) {
-  HWK_CHECK(p && qkv && qn && kn && cos_t && sin_t && kc && vc && workspace && pos, "attn_decode_step: null argument");
-  HWK_CHECK(p->head_dim == 128 && !p->kv_int8, "attn_decode_step: fp16 caches of head_dim 128 only");
-  HWK_CHECK(p->kv_heads > 0 && p->heads % p->kv_heads == 0, "attn_decode_step: %u heads over %u", p->heads, p->kv_heads);
+char *hwk::attn_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *cos_t,
+                     const float *sin_t, double eps, void *kc, void *vc, void *workspace, size_t workspace_bytes,
+                     const hwk_attn_params *p, const int32_t *pos) {
+  HWK_CHECK(p && qkv && qn && kn && cos_t && sin_t && kc && vc && workspace && pos, "attn_step: null argument");
+  HWK_CHECK(p->head_dim == 128 && !p->kv_int8, "attn_step: fp16 caches of head_dim 128 only");
+  HWK_CHECK(p->kv_heads > 0 && p->heads % p->kv_heads == 0, "attn_step: %u heads over %u", p->heads, p->kv_heads);
   const uint32_t G = p->heads / p->kv_heads;
-  HWK_CHECK(G == 1 || G == 2 || G == 4, "attn_decode_step: %u query heads a kv head", G);
-  HWK_CHECK(workspace_bytes >= attn_step_workspace_bytes(p), "attn_decode_step: workspace too small");
-  const uint32_t chunk = attn_step_chunks(p), nchunk = (p->capacity + chunk - 1) / chunk;
+  HWK_CHECK(G == 1 || G == 2 || G == 4, "attn_step: %u query heads a kv head", G);
+  HWK_CHECK(workspace_bytes >= attn_step_workspace_bytes(p), "attn_step: workspace too small");
+  uint32_t chunk, nchunk;
+  attn_step_layout(p, &chunk, &nchunk);
   const uint64_t slots = (uint64_t)p->heads * nchunk;
   float *ws_o = (float *)workspace, *ws_m = ws_o + slots * 128, *ws_l = ws_m + slots;
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
-  constexpr int W = 8;
-#define HWK_STEP(GG)                                                                                               \
-  hipLaunchKernelGGL((k_attn_head<GG, W, false>), dim3(p->kv_heads * nchunk), dim3(64 * W), 0, st, qkv, qn, kn,   \
-                     cos_t, sin_t, eps, (f16 *)kc, (f16 *)vc, nullptr, ws_o, ws_m, ws_l, nullptr, pos, p->heads,    \
-                     p->kv_heads, p->capacity, chunk, nchunk, scale_log2)
-  if (G == 1) HWK_STEP(1);
-  else if (G == 2) HWK_STEP(2);
-  else HWK_STEP(4);
-#undef HWK_STEP
-  if (nchunk_out) *nchunk_out = nchunk;
-  return hwk::launched("attn_decode_step");
-}
-
-char *hwk::attn_merge_ws(hipStream_t st, const void *workspace, void *out, const hwk_attn_params *p, uint32_t nchunk) {
-  const uint32_t G = p->heads / p->kv_heads;
-  const uint64_t slots = (uint64_t)p->heads * nchunk;
-  const float *ws_o = (const float *)workspace, *ws_m = ws_o + slots * 128, *ws_l = ws_m + slots;
-  hipLaunchKernelGGL((k_attn_merge<true>), dim3(p->heads, 4), dim3(256), 0, st, ws_o, ws_m, ws_l, out, nchunk,
-                     p->heads, 128u, G, HWK_OUT_F16);
-  return hwk::launched("attn_merge_ws");
+  constexpr int W = kStepWaves;
+  const uint32_t kpw = chunk / W;
+#define HWK_STEP2(GG)                                                                                             \
+  hipLaunchKernelGGL((k_attn_step<GG, W>), dim3(p->kv_heads * nchunk), dim3(64 * W), 0, st, qkv, qn, kn, cos_t,    \
+                     sin_t, eps, (f16 *)kc, (f16 *)vc, ws_o, ws_m, ws_l, pos, p->heads, p->kv_heads, p->capacity,    \
+                     chunk, nchunk, kpw, scale_log2)
+  if (G == 1) HWK_STEP2(1);
+  else if (G == 2) HWK_STEP2(2);
+  else HWK_STEP2(4);
+#undef HWK_STEP2
+  return hwk::launched("attn_step");
 }
 
 extern "C" {
@@ -1090,8 +790,8 @@ HWK_API char *hwk_attn_merge(void *stream, const void *o, const void *m, const v
   HWK_CHECK(chunks <= kMaxChunks, "hwk_attn_merge: %u chunks (at most %u)", chunks, kMaxChunks);
   HWK_CHECK(out_mode == HWK_OUT_F32 || out_mode == HWK_OUT_F16, "hwk_attn_merge: out_mode %d", out_mode);
   if (rows == 0) return nullptr;
-  hipLaunchKernelGGL((k_attn_merge<false>), dim3(rows, (dim + 31) / 32), dim3(256), 0, (hipStream_t)stream, (const float *)o,
-                     (const float *)m, (const float *)l, out, chunks, rows, dim, 1u, out_mode);
+  hipLaunchKernelGGL(k_attn_merge, dim3(rows, (dim + 31) / 32), dim3(256), 0, (hipStream_t)stream, (const float *)o,
+                     (const float *)m, (const float *)l, out, chunks, rows, dim, out_mode);
   return hwk::launched("hwk_attn_merge");
 }
 

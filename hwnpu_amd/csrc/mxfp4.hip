@@ -214,14 +214,22 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 }
 
 // Where the decode-step GEMV's x comes from.
-enum XMode { X_F16 = 0, X_NORM = 1 };
+enum XMode { X_F16 = 0, X_NORM = 1, X_MERGE = 2 };
 
 struct XIn {
   const uint4 *x16;  // X_F16: x itself
   const float *h;    // X_NORM: the fp32 residual and the norm weights
   const float *nw;
   double eps;
+  const float *ws;   // X_MERGE: attn_step's partials, o (slots, 128) | m (slots) | l (slots)
+  const int32_t *pos;
+  uint32_t G, chunk, nchunk;  // query heads a kv head; the partials' chunking
 };
+
+// Chunks of attention partials the X_MERGE prologue loads at once (more are loaded a chunk at a time).
+constexpr int kMergeBatch = 8;
+// The most chunks X_MERGE takes (LDS holds their m and l for every query head).
+constexpr uint32_t kMergeMaxChunks = 16;
 
 // The decode-step GEMV (64 lanes a row, BPL blocks a lane, nb <= 64*BPL): K1's shape (one row set a
 // wave, the grid as large as the matrix, DPP reduction into lane 63) with x made by the workgroup: its
@@ -237,9 +245,12 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   constexpr int PER = (64 * BPL * 32 + NT - 1) / NT;  // x values a thread makes (X_NORM)
   constexpr int XC = 64 * BPL * 4;                    // 16-byte chunks of x LDS holds
   constexpr int XPER = (XC + NT - 1) / NT;            // chunks a thread copies (X_F16)
+  constexpr int M4 = (64 * BPL * 32 / 4 + NT - 1) / NT;  // groups of 4 x values a thread merges (X_MERGE)
   constexpr bool add = MODE == HWK_OUT_ADD_F32;
   __shared__ uint4 xs[XC];
   __shared__ double red[WPB];
+  __shared__ float mm[XM == X_MERGE ? 64 * BPL / 4 * kMergeMaxChunks : 1];  // m, then the weight, of (head, chunk)
+  __shared__ float ml[XM == X_MERGE ? 64 * BPL / 4 * kMergeMaxChunks : 1];
   const int t = threadIdx.x, lane = t & 63;
   const uint32_t k = nb * 32;
   const uint32_t r0 = (blockIdx.x * WPB + (t >> 6)) * RPW;
@@ -247,7 +258,31 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   // for the wait counter, so x is made while the weights are in flight)
   float hv[PER], wv[PER];
   uint4 xv[XPER];
-  if constexpr (XM == X_NORM) {
+  float4 ov[XM == X_MERGE ? M4 : 1][XM == X_MERGE ? kMergeBatch : 1];
+  uint32_t live = 1;
+  if constexpr (XM == X_MERGE) {
+    // the partials of the live chunks: o of this thread's x values (4 consecutive dims of one query
+    // head a group), and every (head, chunk)'s m and l into LDS
+    const uint32_t heads = k / 128, slots = heads * in.nchunk;
+    live = min((uint32_t)*in.pos / in.chunk + 1, in.nchunk);
+    const float *ws_m = in.ws + (size_t)slots * 128, *ws_l = ws_m + slots;
+#pragma unroll
+    for (int j = 0; j < M4; j++) {
+      const uint32_t e = min((uint32_t)(t + j * NT), k / 4 - 1) * 4, hq = e / 128, d = e % 128;
+#pragma unroll
+      for (int c = 0; c < kMergeBatch; c++) {
+        const uint32_t cc = min((uint32_t)c, live - 1);
+        const size_t slot = ((size_t)(hq / in.G) * in.nchunk + cc) * in.G + hq % in.G;
+        ov[j][c] = *(const float4 *)(in.ws + slot * 128 + d);
+      }
+    }
+    for (uint32_t i = t; i < heads * live; i += NT) {
+      const uint32_t hq = i / live, cc = i % live;
+      const size_t slot = ((size_t)(hq / in.G) * in.nchunk + cc) * in.G + hq % in.G;
+      mm[hq * kMergeMaxChunks + cc] = ws_m[slot];
+      ml[hq * kMergeMaxChunks + cc] = ws_l[slot];
+    }
+  } else if constexpr (XM == X_NORM) {
 #pragma unroll
     for (int j = 0; j < PER; j++) {
       const uint32_t i = min((uint32_t)(t + j * NT), k - 1);
@@ -282,6 +317,48 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
 #pragma unroll
     for (int j = 0; j < PER; j++)
       if (t + j * NT < k) xh[t + j * NT] = (f16)f32_value((hv[j] * r) * wv[j]);
+  } else if constexpr (XM == X_MERGE) {
+    // the reference's Merge rule per query head: top = the largest m among chunks with l > 0, a chunk
+    // weighs exp(m - top), x = fp16(sum(w * o) / sum(w * l))
+    __syncthreads();
+    const uint32_t heads = k / 128, slots = heads * in.nchunk;
+#pragma unroll
+    for (int j = 0; j < M4; j++) {
+      const uint32_t e = (uint32_t)(t + j * NT) * 4;
+      if (e >= k) continue;
+      const uint32_t hq = e / 128, d = e % 128;
+      const float *hm = mm + hq * kMergeMaxChunks, *hl = ml + hq * kMergeMaxChunks;
+      float top = -__builtin_inff();
+      for (uint32_t c = 0; c < live; c++)
+        if (hl[c] > 0.0f) top = fmaxf(top, hm[c]);
+      float den = 0.0f, n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
+      for (uint32_t c = 0; c < live; c++) {
+        const float wc = (hl[c] > 0.0f && top != -__builtin_inff()) ? expf(hm[c] - top) : 0.0f;
+        if (wc > 0.0f) {
+          float4 o;
+          if (c < (uint32_t)kMergeBatch) {
+#pragma unroll
+            for (int cb = 0; cb < kMergeBatch; cb++)
+              if ((uint32_t)cb == c) o = ov[j][cb];
+          } else {
+            const size_t slot = ((size_t)(hq / in.G) * in.nchunk + c) * in.G + hq % in.G;
+            o = *(const float4 *)(in.ws + slot * 128 + d);
+          }
+          den += wc * hl[c];
+          n0 += wc * o.x;
+          n1 += wc * o.y;
+          n2 += wc * o.z;
+          n3 += wc * o.w;
+        }
+      }
+      const float r0 = den > 0.0f ? n0 / den : 0.0f, r1 = den > 0.0f ? n1 / den : 0.0f;
+      const float r2 = den > 0.0f ? n2 / den : 0.0f, r3 = den > 0.0f ? n3 / den : 0.0f;
+      xh[e] = (f16)f32_value(r0);
+      xh[e + 1] = (f16)f32_value(r1);
+      xh[e + 2] = (f16)f32_value(r2);
+      xh[e + 3] = (f16)f32_value(r3);
+    }
+    (void)slots;
   } else {
 #pragma unroll
     for (int j = 0; j < XPER; j++)
@@ -815,11 +892,27 @@ char *mxfp4_gemv_x(hipStream_t st, const void *w, const void *e, const void *x16
   HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "mxfp4_gemv_x: out_mode %d", out_mode);
   HWK_CHECK(aligned(w, 16) && (h || aligned(x16, 16)), "mxfp4_gemv_x: w and x must be 16-byte aligned");
   if (n == 0) return nullptr;
-  XIn in{(const uint4 *)x16, h, nw, eps};
+  XIn in{(const uint4 *)x16, h, nw, eps, nullptr, nullptr, 1, 1, 1};
   const uint32_t nb = k / 32;
   if (h) launch_x_mode<X_NORM>(st, w, e, in, y, n, nb, out_mode, swiglu);
   else launch_x_mode<X_F16>(st, w, e, in, y, n, nb, out_mode, swiglu);
   return launched("mxfp4_gemv_x");
+}
+
+char *mxfp4_gemv_merge(hipStream_t st, const void *w, const void *e, const void *workspace, uint32_t heads, uint32_t G,
+                       uint32_t chunk, uint32_t nchunk, const int32_t *pos, void *y, uint32_t n, int out_mode) {
+  HWK_CHECK(w && e && workspace && pos && y, "mxfp4_gemv_merge: null pointer");
+  const uint32_t k = heads * 128;
+  HWK_CHECK(heads >= 1 && k <= 64 * 4 * 32, "mxfp4_gemv_merge: %u heads of 128 (at most 8192 values)", heads);
+  HWK_CHECK(G >= 1 && heads % G == 0 && chunk > 0, "mxfp4_gemv_merge: G %u, chunk %u", G, chunk);
+  HWK_CHECK(nchunk >= 1 && nchunk <= kMergeMaxChunks, "mxfp4_gemv_merge: %u chunks (at most %u)", nchunk,
+            kMergeMaxChunks);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "mxfp4_gemv_merge: out_mode %d", out_mode);
+  HWK_CHECK(aligned(w, 16) && aligned(workspace, 16), "mxfp4_gemv_merge: w and the workspace 16-byte aligned");
+  if (n == 0) return nullptr;
+  XIn in{nullptr, nullptr, nullptr, 0.0, (const float *)workspace, pos, G, chunk, nchunk};
+  launch_x_mode<X_MERGE>(st, w, e, in, y, n, k / 32, out_mode, false);
+  return launched("mxfp4_gemv_merge");
 }
 
 char *synth_mxfp4_rows(hipStream_t st, void *w, void *e, uint32_t rows, uint32_t k, uint64_t key, float stdv,

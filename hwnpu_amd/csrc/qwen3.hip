@@ -210,8 +210,8 @@ struct hwk_qwen3 {
   f16 *embed;
   float *cos_t, *sin_t;
   int32_t *hist, *pos;
-  uint32_t *counter, *part_i, *counters;
-  bool head_attn = true;  // short caches: attn_head; long ones: the split attention and its merge
+  uint32_t *counter, *part_i;
+  uint32_t step_chunk = 0, step_nchunk = 0;  // the decode attention's chunking (attn_step_layout)
   float *part_v, *logits;
   float *h, *qkv, *gu;
   f16 *x16, *q16, *att16, *a16;
@@ -272,7 +272,6 @@ void layout(hwk_qwen3 *m, uint8_t *base) {
   m->hist = cv.take<int32_t>(base, 4ull * (c.max_ctx + 1));
   m->pos = cv.take<int32_t>(base, 4);
   m->counter = cv.take<uint32_t>(base, 4);
-  m->counters = cv.take<uint32_t>(base, 4ull * c.kv_heads);
   m->part_i = cv.take<uint32_t>(base, 4 * kArgBlocks);
   m->part_v = cv.take<float>(base, 4 * kArgBlocks);
   m->logits = cv.take<float>(base, 4ull * c.vocab);
@@ -307,16 +306,11 @@ char *step(hwk_qwen3 *m, hipStream_t st) {
   for (auto &ly : m->L) {
     HWK_Q(hwk::mxfp4_gemv_x(st, ly.qkv.w, ly.qkv.e, nullptr, m->h, ly.in_norm, m->eps, m->qkv, m->qkv_n, c.hidden,
                             HWK_OUT_F32, false));
-    if (m->head_attn) {
-      HWK_Q(hwk::attn_head(st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t, m->sin_t, m->eps, ly.kc, ly.vc, m->att16, m->ws,
-                           m->ws_bytes, m->counters, &m->ap, m->pos));
-    } else {  // long caches: the split attention and its merge kernel
-      uint32_t nchunk = 0;
-      HWK_Q(hwk::attn_decode_step(st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t, m->sin_t, m->eps, ly.kc, ly.vc, m->ws,
-                                  m->ws_bytes, &m->ap, m->pos, &nchunk));
-      HWK_Q(hwk::attn_merge_ws(st, m->ws, m->att16, &m->ap, nchunk));
-    }
-    HWK_Q(hwk_mxfp4_gemv(st, ly.o.w, ly.o.e, m->att16, m->h, c.hidden, m->att_n, HWK_OUT_ADD_F32));
+    // attention partials over chunks of the cache, merged by the o_proj GEMV into its input
+    HWK_Q(hwk::attn_step(st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t, m->sin_t, m->eps, ly.kc, ly.vc, m->ws, m->ws_bytes,
+                         &m->ap, m->pos));
+    HWK_Q(hwk::mxfp4_gemv_merge(st, ly.o.w, ly.o.e, m->ws, c.heads, c.heads / c.kv_heads, m->step_chunk, m->step_nchunk,
+                                m->pos, m->h, c.hidden, HWK_OUT_ADD_F32));
     HWK_Q(hwk::mxfp4_gemv_x(st, ly.gu.w, ly.gu.e, nullptr, m->h, ly.post_norm, m->eps, m->a16, 2 * c.inter, c.hidden,
                             HWK_OUT_F16, true));
     HWK_Q(hwk_mxfp4_gemv(st, ly.down.w, ly.down.e, m->a16, m->h, c.hidden, c.inter, HWK_OUT_ADD_F32));
@@ -414,9 +408,8 @@ HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
   memcpy(&ap.scale_bits, &sc, 4);
   ap.out_mode = HWK_OUT_F16;
   ap.split = 0;
-  // attn_head while its workgroups take at most 2048 keys each; past that the split attention
-  m->head_attn = c.max_ctx <= 2048 * 8;
-  m->ws_bytes = m->head_attn ? hwk::attn_head_workspace_bytes(&ap) : hwk::attn_step_workspace_bytes(&ap);
+  hwk::attn_step_layout(&ap, &m->step_chunk, &m->step_nchunk);
+  m->ws_bytes = hwk::attn_step_workspace_bytes(&ap);
   layout(m, nullptr);
   hipError_t e = hipMalloc((void **)&m->base, m->bytes);
   if (e != hipSuccess) {
@@ -439,7 +432,7 @@ HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
   if ((e = hipMemcpy(m->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
       (e = hipMemcpy(m->sin_t, stb.data(), stb.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
       (e = hipMemset(m->hist, 0, 4ull * (c.max_ctx + 1))) != hipSuccess || (e = hipMemset(m->pos, 0, 4)) != hipSuccess ||
-      (e = hipMemset(m->counter, 0, 4)) != hipSuccess || (e = hipMemset(m->counters, 0, 4ull * c.kv_heads)) != hipSuccess ||
+      (e = hipMemset(m->counter, 0, 4)) != hipSuccess ||
       (e = hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking)) != hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess)
     err = hwk::hip_err("hwk_qwen3_new", e);
