@@ -290,14 +290,12 @@ def moe_rate(T: int, copies: int = 4):
         uniq.append(len(set(idx.cpu().numpy().ravel().tolist())))
         layers.append((gw, ge, dw, de, logits, x))
     out = torch.empty((T, MOE_H), dtype=torch.float32, device="cuda")
-    idx = torch.empty((T, MOE_K), dtype=torch.int32, device="cuda")
-    w = torch.empty((T, MOE_K), dtype=torch.float32, device="cuda")
-    ws = torch.empty(T * MOE_K * (MOE_I + MOE_H) * 4, dtype=torch.uint8, device="cuda")
+    ws = torch.empty(T * MOE_K * MOE_I * 4, dtype=torch.uint8, device="cuda")
 
     def launch_all():
+        # hwk_moe_layer: the route folded into the gate_up launch, down with the ordered combine
         for gw, ge, dw, de, logits, x in layers:
-            i2, w2 = ops.moe_route(logits, MOE_K)
-            ops.moe_experts(x, i2, w2, gw, ge, dw, de, out=out, workspace=ws)
+            ops.moe_layer(x, logits, MOE_K, gw, ge, dw, de, out=out, workspace=ws)
 
     us = _graph_us(launch_all, copies, 20)
     u = sum(uniq) / len(uniq)

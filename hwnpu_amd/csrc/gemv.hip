@@ -108,9 +108,115 @@ void dispatch(hipStream_t st, const void *w, const void *s, const void *x, void 
   else launch<INT8, 8, 1, 4>(st, w, s, x, y, n, nc, mode);
 }
 
+// K7r: Y (T, n) = X W^T for fp16 W (n, k) and T <= 8 fp16 vectors X (T, k): the tied head over the
+// rows of a speculative verify, each weight row read once for all T vectors. The workgroup copies X
+// into LDS; a wave walks rows (grid-stride), 64 lanes over a row's 16-byte chunks, 4 chunks a lane
+// a pass, and with a single pass (k <= 2048) the next row's chunks are loaded before this row's
+// products.
+template <int TT, bool ONEPASS>
+__global__ __launch_bounds__(256) void k_f16_gemv_rows(const uint4 *__restrict__ w, const uint4 *__restrict__ x,
+                                                       void *__restrict__ y, uint32_t n, uint32_t nc, int mode) {
+  extern __shared__ uint4 xsr[];  // (TT, nc)
+  for (uint32_t i = threadIdx.x; i < TT * nc; i += 256) xsr[i] = x[i];
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const uint32_t waves = gridDim.x * 4;
+  uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  auto load4 = [&](uint32_t row, uint32_t base, uint4 (&c)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t ch = base + j * 64 + lane;
+      c[j] = ch < nc ? load_stream(&w[(size_t)row * nc + ch]) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto dot4 = [&](const uint4 (&c)[4], uint32_t base, float (&acc)[TT]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t ch = base + j * 64 + lane;
+      if (ch >= nc) continue;
+      const uint32_t cw[4] = {c[j].x, c[j].y, c[j].z, c[j].w};
+#pragma unroll
+      for (int v = 0; v < TT; v++) {
+        const uint4 xv = xsr[(size_t)v * nc + ch];
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+        float d0 = 0.0f, d1 = 0.0f;
+        d0 = __builtin_amdgcn_fdot2(h2_of_bits(cw[0]), h2_of_bits(xw[0]), d0, false);
+        d1 = __builtin_amdgcn_fdot2(h2_of_bits(cw[1]), h2_of_bits(xw[1]), d1, false);
+        d0 = __builtin_amdgcn_fdot2(h2_of_bits(cw[2]), h2_of_bits(xw[2]), d0, false);
+        d1 = __builtin_amdgcn_fdot2(h2_of_bits(cw[3]), h2_of_bits(xw[3]), d1, false);
+        acc[v] += d0 + d1;
+      }
+    }
+  };
+  if (r >= n) return;
+  uint4 cur[4];
+  if constexpr (ONEPASS) load4(r, 0, cur);
+  for (; r < n; r += waves) {
+    float acc[TT];
+#pragma unroll
+    for (int v = 0; v < TT; v++) acc[v] = 0.0f;
+    if constexpr (ONEPASS) {
+      uint4 nxt[4];
+      const uint32_t rn = r + waves < n ? r + waves : r;
+      load4(rn, 0, nxt);
+      dot4(cur, 0, acc);
+#pragma unroll
+      for (int j = 0; j < 4; j++) cur[j] = nxt[j];
+    } else {
+      for (uint32_t base = 0; base < nc; base += 256) {
+        uint4 c[4];
+        load4(r, base, c);
+        dot4(c, base, acc);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < TT; v++) {
+      const float s = group_sum<64>(acc[v]);
+      if (lane == 0) store_out(y, (size_t)v * n + r, s, mode);
+    }
+  }
+}
+
+template <int TT>
+void launch_f16_rows(hipStream_t st, const void *w, const void *x, void *y, uint32_t n, uint32_t nc, int mode) {
+  const uint32_t blocks = (n + 3) / 4 < 1024u ? (n + 3) / 4 : 1024u;
+  const size_t lds = (size_t)TT * nc * 16;
+  if (nc <= 256)
+    hipLaunchKernelGGL((k_f16_gemv_rows<TT, true>), dim3(blocks), dim3(256), lds, st, (const uint4 *)w,
+                       (const uint4 *)x, y, n, nc, mode);
+  else
+    hipLaunchKernelGGL((k_f16_gemv_rows<TT, false>), dim3(blocks), dim3(256), lds, st, (const uint4 *)w,
+                       (const uint4 *)x, y, n, nc, mode);
+}
+
 }  // namespace
 
 extern "C" {
+
+HWK_API char *hwk_f16_gemv_rows(void *stream, const void *w, const void *x, void *y, uint32_t n, uint32_t k,
+                                uint32_t tokens, int out_mode) {
+  HWK_CHECK(w && x && y, "hwk_f16_gemv_rows: null pointer");
+  HWK_CHECK(k % 8 == 0 && k > 0, "hwk_f16_gemv_rows: k=%u is not a positive multiple of 8", k);
+  HWK_CHECK(tokens >= 1 && tokens <= 8, "hwk_f16_gemv_rows: %u vectors (1..8)", tokens);
+  HWK_CHECK((size_t)tokens * k * 2 <= 64 * 1024, "hwk_f16_gemv_rows: %u x %u fp16 vectors exceed 64 KB", tokens, k);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "hwk_f16_gemv_rows: out_mode %d", out_mode);
+  HWK_CHECK(hwk::aligned(w, 16) && hwk::aligned(x, 16), "hwk_f16_gemv_rows: w and x must be 16-byte aligned");
+  HWK_CHECK(hwk::aligned(y, out_mode == HWK_OUT_F16 ? 2 : 4), "hwk_f16_gemv_rows: y misaligned");
+  if (n == 0) return nullptr;
+  hipStream_t st = (hipStream_t)stream;
+  const uint32_t nc = k / 8;
+  switch (tokens) {
+    case 1: launch_f16_rows<1>(st, w, x, y, n, nc, out_mode); break;
+    case 2: launch_f16_rows<2>(st, w, x, y, n, nc, out_mode); break;
+    case 3: launch_f16_rows<3>(st, w, x, y, n, nc, out_mode); break;
+    case 4: launch_f16_rows<4>(st, w, x, y, n, nc, out_mode); break;
+    case 5: launch_f16_rows<5>(st, w, x, y, n, nc, out_mode); break;
+    case 6: launch_f16_rows<6>(st, w, x, y, n, nc, out_mode); break;
+    case 7: launch_f16_rows<7>(st, w, x, y, n, nc, out_mode); break;
+    default: launch_f16_rows<8>(st, w, x, y, n, nc, out_mode); break;
+  }
+  return hwk::launched("hwk_f16_gemv_rows");
+}
 
 HWK_API char *hwk_i8_gemv(void *stream, const void *q, const void *scale16, const void *x, void *y, uint32_t n,
                           uint32_t k, int out_mode) {

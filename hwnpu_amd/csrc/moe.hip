@@ -1,93 +1,129 @@
-// MoE on gfx950: the router's top-k choice (K5a) and the chosen experts' SwiGLU FFNs (K5b).
+// MoE on gfx950: the router's top-k choice (K5a) and the chosen experts' gated FFNs (K5b).
 //
-// K5a is one wave per token and restates the reference's Routing.Choose operation for operation
-// (float64 exp rounded to float32, a sequential float32 sum, a stable descending order), so that
-// the chosen expert ids are the reference's bit for bit.
+// K5a restates the reference's Routing.Choose operation for operation (float64 exp rounded to
+// float32, a sequential float32 sum, a stable descending order) in one wave per token with lane j
+// holding expert j, so that the chosen expert ids are the reference's bit for bit.
 //
-// K5b is three launches and needs nothing from the host between them: every workgroup derives the
-// sorted set of chosen experts from idx itself (a 64-bit ballot of the expert ids). The gate_up
-// kernel gives each (chosen expert, row-pair tile) to a workgroup, reads the expert's rows once
-// for all tokens that chose it, and writes silu(gate)*up in fp32 (it overflows fp16 at the
-// benchmark's scales). The down kernel does the same for (chosen expert, row tile), so that every
-// expert's rows stream in parallel, and leaves each token's per-expert outputs in fp32; the combine
-// adds w * y for each token in ascending expert id, the reference's summation order
+// K5b is two launches and needs nothing from the host between them. The gate_up kernel gives each
+// (chosen expert, row-pair tile) to a workgroup: with the route folded in (hwk_moe_layer) every
+// workgroup first derives the token's choice from the router logits itself; otherwise it reads the
+// given idx. It reads the expert's rows once for all tokens that chose it, adds the gate/up biases,
+// and writes the gated unit (SiLU, or gpt-oss's clamped one) in fp32 (it overflows fp16 at the
+// benchmark's scales). The down kernel gives each workgroup a tile of output rows for every chosen
+// expert (its waves take the experts in turn, all their rows' loads issued at once) and then adds,
+// for each token, w * (y + down bias) in ascending expert id, the reference's summation order
 // (host.go:566-578,866-881), with no atomics.
 #include "hwk_common.h"
+
+#define HWK_Q(call)                  \
+  do {                               \
+    if (char *e_ = (call)) return e_; \
+  } while (0)
 
 namespace {
 
 // ---- K5a ----
 
-__global__ __launch_bounds__(64) void k_moe_route(const float *__restrict__ logits, const float *__restrict__ bias,
-                                                  int32_t *__restrict__ idx, float *__restrict__ w, uint32_t E,
-                                                  uint32_t k, int score, int norm, float scale) {
+// A lane's float as a wave-uniform value (v_readlane: no LDS round trip).
+__device__ __forceinline__ float lane_f(float v, uint32_t j) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)j));
+}
+
+// Routing.Choose (internal/llm/experts/weights.go:33-81) of one row of E <= 64 logits by one wave,
+// lane j holding expert j, reading other lanes' values with v_readlane only (no LDS, no barrier):
+// softmax scores in float32 (exp in float64 rounded to float32, the sum taken in expert order), or
+// sigmoid; the rank of each expert in a stable descending sort of score + bias (ties to the lower
+// index); the first k (idx, w) with w the chosen scores over their float32 sum + 1e-6 (norm), times
+// scale unless 0. Lanes < k write idx_out/w_out.
+__device__ void choose_wave(const float *__restrict__ logits, const float *__restrict__ bias, uint32_t E, uint32_t k,
+                            int score, int norm, float scale, int32_t *idx_out, float *w_out) {
 #pragma clang fp contract(off)
-  __shared__ float sc[64], key[64], chosen_w[64];
-  __shared__ int chosen_e[64];
-  __shared__ float total;
-  const uint32_t row = blockIdx.x, lane = threadIdx.x;
+  const uint32_t lane = threadIdx.x & 63;
   const bool live = lane < E;
-  const float v = live ? logits[(size_t)row * E + lane] : -__builtin_inff();
+  const float v = live ? logits[lane] : -__builtin_inff();
+  const float bl = bias && live ? bias[lane] : 0.0f;
   float s;
   if (score == HWK_SCORE_SOFTMAX) {
     float m = v;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    const float d = v - m;
-    const float ex = live ? (float)exp((double)d) : 0.0f;
-    sc[lane] = ex;
-    __syncthreads();
-    if (lane == 0) {
-      float sum = 0.0f;
-      for (uint32_t j = 0; j < E; j++) sum += sc[j];
-      total = sum;
-    }
-    __syncthreads();
+    const float ex = live ? (float)exp((double)(v - m)) : 0.0f;
+    float total = 0.0f;
+    for (uint32_t j = 0; j < E; j++) total += lane_f(ex, j);
     s = ex / total;
   } else {
     s = 1.0f / (1.0f + (float)exp((double)(-v)));
   }
-  const float kv = bias && live ? s + bias[lane] : s;
-  key[lane] = kv;
-  __syncthreads();
-  // position in a stable descending sort: larger keys first, equal keys by index
+  const float kv = bias && live ? s + bl : s;
   uint32_t rank = 0;
   for (uint32_t j = 0; j < E; j++) {
-    const float kj = key[j];
+    const float kj = lane_f(kv, j);
     rank += (kj > kv) || (kj == kv && j < lane);
   }
-  if (live && rank < k) {
-    chosen_e[rank] = (int)lane;
-    chosen_w[rank] = s;
+  // the k chosen in rank order: lane r learns the expert of rank r and its score
+  int my_e = -1;
+  float my_w = 0.0f, sum = 0.0f;
+  for (uint32_t r = 0; r < k; r++) {
+    const uint64_t who = __ballot(live && rank == r);
+    const uint32_t src = who ? (uint32_t)__builtin_ctzll(who) : 0u;  // no such rank only with NaN scores
+    const float wr = lane_f(s, src);
+    sum += wr;
+    if (lane == r) {
+      my_e = (int)src;
+      my_w = wr;
+    }
   }
-  __syncthreads();
-  if (lane == 0) {
-    float sum = 0.0f;
-    for (uint32_t j = 0; j < k; j++) sum += chosen_w[j];
-    total = sum;
-  }
-  __syncthreads();
   if (lane < k) {
-    float wj = chosen_w[lane];
-    if (norm) wj /= total + 1e-6f;
+    float wj = my_w;
+    if (norm) wj /= sum + 1e-6f;
     if (scale != 0.0f) wj *= scale;
-    idx[(size_t)row * k + lane] = chosen_e[lane];
-    w[(size_t)row * k + lane] = wj;
+    idx_out[lane] = my_e;
+    w_out[lane] = wj;
   }
+}
+
+// hwk_moe_route: one wave a row.
+__global__ __launch_bounds__(256) void k_moe_route(const float *__restrict__ logits, const float *__restrict__ bias,
+                                                   int32_t *__restrict__ idx, float *__restrict__ w, uint32_t rows,
+                                                   uint32_t E, uint32_t k, int score, int norm, float scale) {
+  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  choose_wave(logits + (size_t)row * E, bias, E, k, score, norm, scale, idx + (size_t)row * k, w + (size_t)row * k);
 }
 
 // ---- K5b helpers ----
 
-// The set of experts idx names (n entries, experts < 64) as a bit mask, the same in every lane.
-__device__ __forceinline__ uint64_t chosen_mask(const int32_t *__restrict__ idx, uint32_t n) {
+// dst[0, n) = src[0, n) (16-byte items) by the 256 threads of a workgroup, every thread's loads of
+// a pass (up to SPT) issued before its stores, so that a pass waits on one memory latency, not SPT.
+// Native vectors: an array of HIP's uint4 (a union) would be left in scratch memory.
+template <int SPT, int NT = 256>
+__device__ __forceinline__ void stage_copy(void *dstv, const void *__restrict__ srcv, uint32_t n) {
+  typedef uint32_t V __attribute__((ext_vector_type(4)));
+  V *dst = (V *)dstv;
+  const V *src = (const V *)srcv;
+  for (uint32_t base = 0; base < n; base += NT * SPT) {
+    V r[SPT];
+#pragma unroll
+    for (int j = 0; j < SPT; j++) r[j] = src[min(base + j * NT + threadIdx.x, n - 1)];
+#pragma unroll
+    for (int j = 0; j < SPT; j++) {
+      const uint32_t i = base + j * NT + threadIdx.x;
+      if (i < n) dst[i] = r[j];
+    }
+  }
+}
+
+// The set of experts idx names (n entries) as a bit mask, the same in every lane: ids outside
+// [0, E) name none (E <= 64).
+__device__ __forceinline__ uint64_t chosen_mask(const int32_t *idx, uint32_t n, uint32_t E) {
   const int lane = threadIdx.x & 63;
   bool hit = false;
   for (uint32_t j = 0; j < n; j++) hit |= idx[j] == lane;
-  return __ballot(hit);
+  return __ballot(hit && (uint32_t)lane < E);
 }
 
 // The slot of expert e among token t's k choices, -1 if none (uniform).
-__device__ __forceinline__ int slot_of(const int32_t *__restrict__ idx, uint32_t t, uint32_t k, int e) {
+__device__ __forceinline__ int slot_of(const int32_t *idx, uint32_t t, uint32_t k, int e) {
   for (uint32_t j = 0; j < k; j++)
     if (idx[t * k + j] == e) return (int)j;
   return -1;
@@ -128,23 +164,68 @@ __device__ __forceinline__ float dot_block_f32(uint4 c, const float4 (&a)[8]) {
   return d0 + d1;
 }
 
-// ---- K5b stage 1: gate_up + SwiGLU ----
+// ---- K5b stage 1: route (optional), gate_up + bias, the gated unit ----
+
+struct MoeArgs {
+  uint32_t T, H, I, E, k;
+  int act;  // HWK_ACT_SILU or HWK_ACT_GPTOSS
+  int score, norm;
+  float alpha, limit, scale;
+  int mode;  // out_mode of the down stage
+};
+
+// The gated unit of one (gate, up) pair (host.go:516-527): SiLU g/(1+e^-g)*u, or gpt-oss's
+// min(g, L)/(1+e^(-a*min(g, L))) * (clamp(u, -L, L) + 1), exp in float64 rounded to float32, every
+// other step a float32 operation of its own.
+__device__ __forceinline__ float gated(float g, float u, const MoeArgs &a) {
+#pragma clang fp contract(off)
+  if (a.act == HWK_ACT_GPTOSS) {
+    g = fminf(g, a.limit);
+    u = fminf(fmaxf(u, -a.limit), a.limit);
+    return g / (1.0f + (float)exp((double)(-(a.alpha * g)))) * (u + 1.0f);
+  }
+  return g / (1.0f + (float)exp((double)(-g))) * u;
+}
+
 // Workgroup (row-pair tile blockIdx.x, chosen expert number blockIdx.y in ascending id). 64 lanes
 // a row, BPL blocks a lane (nb = H/32 <= 64*BPL); a wave takes PPW row pairs (gate 2j, up 2j+1).
-template <int BPL, int PPW>
-__global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x, const int32_t *__restrict__ idx,
-                                                     const uint4 *__restrict__ gw, const uint8_t *__restrict__ ge,
-                                                     float *__restrict__ act, uint32_t T, uint32_t H, uint32_t I,
-                                                     uint32_t k) {
+// ROUTE: the workgroup routes every token from the logits first (waves over tokens), and workgroup
+// (0, 0) writes idx and w; else idx is given. XL: x (T, H) fp16 is copied into LDS (dynamic, T*H*2
+// bytes) before the route, so that no token's products wait on a global load.
+template <int BPL, int PPW, bool ROUTE, bool XL>
+__global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x, const float *__restrict__ logits,
+                                                     const float *__restrict__ rbias, int32_t *__restrict__ idx,
+                                                     float *__restrict__ wout, const uint4 *__restrict__ gw,
+                                                     const uint8_t *__restrict__ ge, const float *__restrict__ gb,
+                                                     float *__restrict__ act, MoeArgs a) {
+  __shared__ int32_t sidx[64];
+  __shared__ float sw[64];
+  extern __shared__ uint4 xsh[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint64_t mask = chosen_mask(idx, T * k);
+  const uint32_t n = a.T * a.k;
+  if constexpr (XL) stage_copy<8>(xsh, x, a.T * a.H / 8);
+  if constexpr (ROUTE) {
+    for (uint32_t t = wave; t < a.T; t += 4)
+      choose_wave(logits + (size_t)t * a.E, rbias, a.E, a.k, a.score, a.norm, a.scale, sidx + t * a.k, sw + t * a.k);
+    __syncthreads();
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < n) {
+      idx[threadIdx.x] = sidx[threadIdx.x];
+      wout[threadIdx.x] = sw[threadIdx.x];
+    }
+  } else {
+    if (threadIdx.x < n) sidx[threadIdx.x] = idx[threadIdx.x];
+    __syncthreads();
+  }
+  uint64_t mask = chosen_mask(sidx, n, a.E);
   const uint32_t u = blockIdx.y;
   if (u >= (uint32_t)__builtin_popcountll(mask)) return;
   for (uint32_t i = 0; i < u; i++) mask &= mask - 1;
   const int e = __builtin_ctzll(mask);
-  const uint32_t nb = H / 32;
+  const uint32_t nb = a.H / 32, I = a.I;
   const uint32_t pair0 = (blockIdx.x * 4 + wave) * PPW;
   const size_t erow = (size_t)e * 2 * I;  // the expert's first row
+  // every load issued unconditionally from a clamped row / block (a load under a branch is waited
+  // for where the branches join): terms of blocks past nb are dropped, rows past I not written
   uint4 c[PPW][2][BPL];
   uint32_t s[PPW][2][BPL];
 #pragma unroll
@@ -153,130 +234,259 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x
     for (int r = 0; r < 2; r++)
 #pragma unroll
       for (int j = 0; j < BPL; j++) {
-        const uint32_t pair = pair0 + p, b = j * 64 + lane;
-        if (pair < I && b < nb) {
-          const size_t blk = (erow + 2 * pair + r) * nb + b;
-          c[p][r][j] = load_stream(&gw[blk]);
-          s[p][r][j] = ge[blk];
-        } else {
-          c[p][r][j] = make_uint4(0, 0, 0, 0);
-          s[p][r][j] = 0;
-        }
+        const uint32_t pair = min(pair0 + p, I - 1), b = min((uint32_t)(j * 64 + lane), nb - 1);
+        const size_t blk = (erow + 2 * pair + r) * nb + b;
+        c[p][r][j] = load_stream(&gw[blk]);
+        s[p][r][j] = ge[blk];
       }
-  for (uint32_t t = 0; t < T; t++) {
-    const int slot = slot_of(idx, t, k, e);
+  float bias[PPW][2];
+#pragma unroll
+  for (int p = 0; p < PPW; p++)
+#pragma unroll
+    for (int r = 0; r < 2; r++) bias[p][r] = gb ? gb[erow + 2 * min(pair0 + p, I - 1) + r] : 0.0f;
+  for (uint32_t t = 0; t < a.T; t++) {
+    const int slot = slot_of(sidx, t, a.k, e);
     if (slot < 0) continue;
     uint4 xr[BPL][4];
 #pragma unroll
     for (int j = 0; j < BPL; j++) {
-      const uint32_t b = j * 64 + lane;
+      const uint32_t b = min((uint32_t)(j * 64 + lane), nb - 1);
 #pragma unroll
-      for (int q = 0; q < 4; q++) xr[j][q] = b < nb ? x[((size_t)t * H + b * 32) / 8 + q] : make_uint4(0, 0, 0, 0);
+      for (int q = 0; q < 4; q++) {
+        const size_t xi = ((size_t)t * a.H + b * 32) / 8 + q;
+        xr[j][q] = XL ? xsh[xi] : x[xi];
+      }
     }
 #pragma unroll
     for (int p = 0; p < PPW; p++) {
       float gu[2];
 #pragma unroll
       for (int r = 0; r < 2; r++) {
-        float a = 0.0f;
+        float v = 0.0f;
 #pragma unroll
-        for (int j = 0; j < BPL; j++) a += dot_block_f16(c[p][r][j], xr[j]) * e8m0_scale(s[p][r][j]);
-        gu[r] = group_sum<64>(a);
+        for (int j = 0; j < BPL; j++) {
+          const float term = dot_block_f16(c[p][r][j], xr[j]) * e8m0_scale(s[p][r][j]);
+          v += (uint32_t)(j * 64 + lane) < nb ? term : 0.0f;
+        }
+        gu[r] = group_sum<64>(v) + bias[p][r];
       }
       const uint32_t pair = pair0 + p;
-      if (lane == 0 && pair < I) {
-        const float g = gu[0];
-        act[((size_t)t * k + slot) * I + pair] = g / (1.0f + expf(-g)) * gu[1];
-      }
+      if (lane == 0 && pair < I) act[((size_t)t * a.k + slot) * I + pair] = gated(gu[0], gu[1], a);
     }
   }
 }
 
-// ---- K5b stage 2: down, one chosen expert a workgroup column ----
-// Workgroup (row tile blockIdx.x, chosen expert number blockIdx.y in ascending id), one wave: LPR
-// lanes a row (RS = 64/LPR rows), BPL blocks a lane (nb = I/32 <= LPR*BPL). The expert's rows are
-// read once for all the tokens that chose it; y = down(act) goes unweighted to ydown (tokens, k, H)
-// at the token's slot of that expert.
-template <int LPR, int BPL>
-__global__ __launch_bounds__(64) void k_moe_down(const float *__restrict__ act, const int32_t *__restrict__ idx,
-                                                 const uint4 *__restrict__ dw, const uint8_t *__restrict__ de,
-                                                 float *__restrict__ ydown, uint32_t T, uint32_t H, uint32_t I,
-                                                 uint32_t k) {
+// ---- K5b stage 2: down for every chosen expert, then the ordered combine ----
+// Workgroup: RS = 64/LPR output rows (row0 + lane/LPR), 4 waves; wave wv takes the chosen experts
+// u = wv, wv+4, ... (ascending id), EPW of them at a time with all their rows' loads issued at
+// once; LPR lanes a row, BPL blocks a lane (nb = I/32 <= LPR*BPL). Each expert's rows are read once
+// for every token that chose it, its unweighted y kept in LDS by (token slot, row). Then one thread
+// a (token, row) adds w * (y + down bias) over the token's experts in ascending expert id. AL: the
+// activations (T*k, I) fp32 are copied into LDS (dynamic) after the first experts' weight loads are
+// issued, so that the products wait on no global load.
+template <int LPR, int BPL, int EPW, bool AL, int NW>
+__global__ __launch_bounds__(64 * NW) void k_moe_down(const float *__restrict__ act, const int32_t *__restrict__ idx,
+                                                  const float *__restrict__ w, const uint4 *__restrict__ dw,
+                                                  const uint8_t *__restrict__ de, const float *__restrict__ db,
+                                                  float *__restrict__ out, MoeArgs a) {
   constexpr int RS = 64 / LPR;
-  const int lane = threadIdx.x & 63, l = lane % LPR;
-  const uint32_t row = blockIdx.x * RS + lane / LPR;
-  uint64_t mask = chosen_mask(idx, T * k);
-  const uint32_t u = blockIdx.y;
-  if (u >= (uint32_t)__builtin_popcountll(mask)) return;
-  for (uint32_t i = 0; i < u; i++) mask &= mask - 1;
-  const int e = __builtin_ctzll(mask);
-  const uint32_t nb = I / 32;
-  uint4 c[BPL];
-  uint32_t sc[BPL];
-#pragma unroll
-  for (int j = 0; j < BPL; j++) {
-    const uint32_t b = j * LPR + l;
-    if (row < H && b < nb) {
-      const size_t blk = ((size_t)e * H + row) * nb + b;
-      c[j] = load_stream(&dw[blk]);
-      sc[j] = de[blk];
-    } else {
-      c[j] = make_uint4(0, 0, 0, 0);
-      sc[j] = 0;
-    }
+  __shared__ int32_t sidx[64];
+  __shared__ float sw[64];
+  __shared__ float ys[64 * RS];  // (token slot, row)
+  extern __shared__ float4 ash[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l = lane % LPR;
+  const uint32_t n = a.T * a.k, H = a.H, nb = a.I / 32;
+  if (threadIdx.x < n) {
+    sidx[threadIdx.x] = idx[threadIdx.x];
+    sw[threadIdx.x] = w[threadIdx.x];
   }
-  for (uint32_t t = 0; t < T; t++) {
-    const int slot = slot_of(idx, t, k, e);
-    if (slot < 0) continue;
-    const float *ar = act + ((size_t)t * k + slot) * I;
-    float a = 0.0f;
+  __syncthreads();
+  const uint64_t mask = chosen_mask(sidx, n, a.E);
+  const uint32_t U = (uint32_t)__builtin_popcountll(mask);
+  const uint32_t e0 = mask ? (uint32_t)__builtin_ctzll(mask) : 0u;  // the rows padding slots read
+  const uint32_t row0 = blockIdx.x * RS, row = row0 + lane / LPR;
+  const uint32_t rowc = row < H ? row : H - 1;
+  const float4 *act4 = (const float4 *)act;
+  bool staged = !AL;
+  for (uint32_t base = wave; base < U + NW * EPW * (staged ? 0 : 1); base += NW * EPW) {
+    uint4 c[EPW][BPL];
+    uint32_t sc[EPW][BPL];
+    int ex[EPW];
+    // every load issued unconditionally (a load under a branch is waited for where the branches
+    // join): slots past the chosen experts read the first chosen expert's rows, blocks past nb the
+    // last block; their terms are dropped
 #pragma unroll
-    for (int j = 0; j < BPL; j++) {
-      const uint32_t b = j * LPR + l;
-      float4 av[8];
+    for (int i = 0; i < EPW; i++) {
+      const uint32_t u = base + NW * i;
+      uint64_t m = mask;
+      for (uint32_t q = 0; q < u && m; q++) m &= m - 1;
+      ex[i] = u < U ? __builtin_ctzll(m) : -1;
+      const uint32_t el = u < U ? (uint32_t)__builtin_ctzll(m) : e0;
 #pragma unroll
-      for (int q = 0; q < 8; q++) av[q] = b < nb ? ((const float4 *)(ar + b * 32))[q] : make_float4(0, 0, 0, 0);
-      a += dot_block_f32(c[j], av) * e8m0_scale(sc[j]);
-    }
-    const float y = group_sum<LPR>(a);
-    if (l == 0 && row < H) ydown[((size_t)t * k + slot) * H + row] = y;
-  }
-}
-
-// ---- K5b stage 3: the ordered combine ----
-// out[t][r] (+)= sum over token t's experts in ascending expert id of w * y (the reference's order,
-// host.go:566-578,866-881), one thread an output.
-__global__ __launch_bounds__(256) void k_moe_combine(const float *__restrict__ ydown, const int32_t *__restrict__ idx,
-                                                     const float *__restrict__ w, float *__restrict__ out, uint32_t T,
-                                                     uint32_t H, uint32_t k, int mode) {
-  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= T * H) return;
-  const uint32_t t = i / H, r = i % H;
-  float acc = mode == HWK_OUT_ADD_F32 ? out[i] : 0.0f;
-  int prev = -1;
-  for (uint32_t n = 0; n < k; n++) {
-    int best = 1 << 30;
-    uint32_t bs = 0;
-    for (uint32_t j = 0; j < k; j++) {
-      const int e = idx[t * k + j];
-      if (e > prev && e < best) {
-        best = e;
-        bs = j;
+      for (int j = 0; j < BPL; j++) {
+        const uint32_t b = min((uint32_t)(j * LPR + l), nb - 1);
+        const size_t blk = ((size_t)el * H + rowc) * nb + b;
+        c[i][j] = load_stream(&dw[blk]);
+        sc[i][j] = de[blk];
       }
     }
-    acc += w[t * k + bs] * ydown[((size_t)t * k + bs) * H + r];
-    prev = best;
+    if (!staged) {  // once, behind the first weight loads: every wave of the workgroup takes part
+      stage_copy<16, 64 * NW>(ash, act4, n * a.I / 4);
+      __syncthreads();
+      staged = true;
+    }
+#pragma unroll
+    for (int i = 0; i < EPW; i++) {
+      if (ex[i] < 0) continue;
+      for (uint32_t t = 0; t < a.T; t++) {
+        const int slot = slot_of(sidx, t, a.k, ex[i]);
+        if (slot < 0) continue;
+        const size_t a0 = ((size_t)t * a.k + slot) * a.I / 4;
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < BPL; j++) {
+          const uint32_t b = min((uint32_t)(j * LPR + l), nb - 1);
+          float4 av[8];
+#pragma unroll
+          for (int q = 0; q < 8; q++) av[q] = AL ? ash[a0 + b * 8 + q] : act4[a0 + b * 8 + q];
+          const float term = dot_block_f32(c[i][j], av) * e8m0_scale(sc[i][j]);
+          v += (uint32_t)(j * LPR + l) < nb ? term : 0.0f;
+        }
+        const float y = group_sum<LPR>(v);
+        if (l == 0) ys[(t * a.k + slot) * RS + lane / LPR] = y;
+      }
+    }
   }
-  out[i] = acc;
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < a.T * RS; i += 64 * NW) {
+#pragma clang fp contract(off)
+    const uint32_t t = i / RS, r = i % RS, orow = row0 + r;
+    if (orow >= H) continue;
+    float acc = a.mode == HWK_OUT_ADD_F32 ? out[(size_t)t * H + orow] : 0.0f;
+    int prev = -1;
+    for (uint32_t q = 0; q < a.k; q++) {
+      int best = 1 << 30;
+      uint32_t bs = 0;
+      for (uint32_t j = 0; j < a.k; j++) {
+        const int e = sidx[t * a.k + j];
+        if (e > prev && e < best) {
+          best = e;
+          bs = j;
+        }
+      }
+      if (best >= (int)a.E) break;  // an id outside [0, E) (a caller's error): no term
+      const float bias = db ? db[(size_t)best * H + orow] : 0.0f;
+      acc += sw[t * a.k + bs] * (ys[(t * a.k + bs) * RS + r] + bias);
+      prev = best;
+    }
+    out[(size_t)t * H + orow] = acc;
+  }
 }
 
+// LDS the staging copies may take (gfx950: 160 KB a workgroup, 64 KB without the attribute).
+constexpr size_t kMoeStageLds = 128 * 1024;
+
 template <int LPR, int BPL>
-void launch_down(hipStream_t st, const float *act, const int32_t *idx, const void *dw, const void *de, float *ydown,
-                 const hwk_moe_params *p, uint32_t unique_max) {
-  constexpr uint32_t rows = 64 / LPR;
-  hipLaunchKernelGGL((k_moe_down<LPR, BPL>), dim3((p->hidden + rows - 1) / rows, unique_max), dim3(64), 0, st, act,
-                     idx, (const uint4 *)dw, (const uint8_t *)de, ydown, p->tokens, p->hidden, p->inter, p->k);
+void launch_down(hipStream_t st, const float *act, const int32_t *idx, const float *w, const void *dw, const void *de,
+                 const float *db, float *out, const MoeArgs &a) {
+  constexpr int RS = 64 / LPR, NW = 8;
+  constexpr int EPW = BPL <= 1 ? 8 : 12 / BPL;
+  const size_t lds = (size_t)a.T * a.k * a.I * 4;
+  const dim3 grid((a.H + RS - 1) / RS);
+  if (lds <= kMoeStageLds) {
+    static bool attr = false;  // once per instance: the dynamic LDS past 64 KB
+    if (!attr) {
+      (void)hipFuncSetAttribute((const void *)k_moe_down<LPR, BPL, EPW, true, NW>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMoeStageLds);
+      attr = true;
+    }
+    hipLaunchKernelGGL((k_moe_down<LPR, BPL, EPW, true, NW>), grid, dim3(64 * NW), lds, st, act, idx, w,
+                       (const uint4 *)dw, (const uint8_t *)de, db, out, a);
+  } else {
+    hipLaunchKernelGGL((k_moe_down<LPR, BPL, EPW, false, NW>), grid, dim3(64 * NW), 0, st, act, idx, w,
+                       (const uint4 *)dw, (const uint8_t *)de, db, out, a);
+  }
 }
+
+char *check_params(const char *what, const hwk_moe_params *p) {
+  HWK_CHECK(p, "%s: null params", what);
+  HWK_CHECK(p->tokens >= 1 && p->tokens <= 8, "%s: %u tokens (1..8)", what, p->tokens);
+  HWK_CHECK(p->experts >= 1 && p->experts <= 64, "%s: %u experts (1..64)", what, p->experts);
+  HWK_CHECK(p->k >= 1 && p->k <= p->experts && p->tokens * p->k <= 64, "%s: k=%u", what, p->k);
+  HWK_CHECK(p->hidden % 32 == 0 && p->hidden > 0 && p->hidden <= 8192, "%s: hidden %u", what, p->hidden);
+  HWK_CHECK(p->inter % 32 == 0 && p->inter > 0 && p->inter <= 8192, "%s: inter %u", what, p->inter);
+  HWK_CHECK(p->out_mode == HWK_OUT_F32 || p->out_mode == HWK_OUT_ADD_F32, "%s: out_mode %u", what, p->out_mode);
+  HWK_CHECK(p->act == HWK_ACT_SILU || p->act == HWK_ACT_GPTOSS, "%s: act %u", what, p->act);
+  return nullptr;
+}
+
+MoeArgs args_of(const hwk_moe_params *p) {
+  MoeArgs a;
+  a.T = p->tokens;
+  a.H = p->hidden;
+  a.I = p->inter;
+  a.E = p->experts;
+  a.k = p->k;
+  a.act = (int)p->act;
+  a.alpha = hwk::f32_of_bits(p->alpha_bits);
+  a.limit = hwk::f32_of_bits(p->limit_bits);
+  a.score = (int)p->score;
+  a.norm = (int)p->norm;
+  a.scale = hwk::f32_of_bits(p->scale_bits);
+  a.mode = (int)p->out_mode;
+  return a;
+}
+
+template <int PPW, bool ROUTE>
+void launch_gate_up(hipStream_t st, const void *x, const float *logits, const float *rbias, int32_t *idx, float *w,
+                    const void *gu_w, const void *gu_e, const float *gu_b, float *act, const MoeArgs &a) {
+  const uint32_t unique_max = a.T * a.k < a.E ? a.T * a.k : a.E;
+  const dim3 g1((a.I + 4 * PPW - 1) / (4 * PPW), unique_max);
+  const int bpl1 = (int)((a.H / 32 + 63) / 64);
+  const size_t xl = (size_t)a.T * a.H * 2;  // x in LDS when it fits in 32 KB
+#define HWK_GU(B)                                                                                                \
+  if (xl <= 32 * 1024)                                                                                           \
+    hipLaunchKernelGGL((k_moe_gate_up<B, PPW, ROUTE, true>), g1, dim3(256), xl, st, (const uint4 *)x, logits,     \
+                       rbias, idx, w, (const uint4 *)gu_w, (const uint8_t *)gu_e, gu_b, act, a);                  \
+  else                                                                                                           \
+    hipLaunchKernelGGL((k_moe_gate_up<B, PPW, ROUTE, false>), g1, dim3(256), 0, st, (const uint4 *)x, logits,     \
+                       rbias, idx, w, (const uint4 *)gu_w, (const uint8_t *)gu_e, gu_b, act, a)
+  switch (bpl1) {
+    case 1: HWK_GU(1); break;
+    case 2: HWK_GU(2); break;
+    case 3: HWK_GU(3); break;
+    default: HWK_GU(4); break;
+  }
+#undef HWK_GU
+}
+
+// K5b: gate_up (with the route folded in when ROUTE), then down with the ordered combine. Past 2
+// tokens a workgroup takes 4 row pairs a wave instead of 2: fewer waves repeat the per-token work.
+template <bool ROUTE>
+char *run_experts(hipStream_t st, const void *x, const float *logits, const float *rbias, int32_t *idx, float *w,
+                  const void *gu_w, const void *gu_e, const float *gu_b, const void *dn_w, const void *dn_e,
+                  const float *dn_b, float *out, float *act, const MoeArgs &a, const char *what) {
+  if (a.T <= 2)
+    launch_gate_up<2, ROUTE>(st, x, logits, rbias, idx, w, gu_w, gu_e, gu_b, act, a);
+  else
+    launch_gate_up<4, ROUTE>(st, x, logits, rbias, idx, w, gu_w, gu_e, gu_b, act, a);
+  if (char *err = hwk::launched(what)) return err;
+  // down: lanes a row by I/32 blocks, the fewest idle slots (8 lanes x 3 blocks for I = 768)
+  const uint32_t nbi = a.I / 32;
+  if (nbi <= 8) launch_down<8, 1>(st, act, idx, w, dn_w, dn_e, dn_b, out, a);
+  else if (nbi <= 16) launch_down<16, 1>(st, act, idx, w, dn_w, dn_e, dn_b, out, a);
+  else if (nbi <= 24) launch_down<8, 3>(st, act, idx, w, dn_w, dn_e, dn_b, out, a);
+  else if (nbi <= 32) launch_down<32, 1>(st, act, idx, w, dn_w, dn_e, dn_b, out, a);
+  else if (nbi <= 64) launch_down<64, 1>(st, act, idx, w, dn_w, dn_e, dn_b, out, a);
+  else if (nbi <= 128) launch_down<64, 2>(st, act, idx, w, dn_w, dn_e, dn_b, out, a);
+  else if (nbi <= 192) launch_down<64, 3>(st, act, idx, w, dn_w, dn_e, dn_b, out, a);
+  else launch_down<64, 4>(st, act, idx, w, dn_w, dn_e, dn_b, out, a);
+  return hwk::launched(what);
+}
+
+// Tokens up to which hwk_moe_layer folds the route into the gate_up launch: every workgroup routes
+// every token, which past a few tokens costs more vector issue than the route launch it saves.
+constexpr uint32_t kFoldRouteMaxTokens = 2;
 
 }  // namespace
 
@@ -289,68 +499,57 @@ HWK_API char *hwk_moe_route(void *stream, const void *logits, const void *bias, 
   HWK_CHECK(k >= 1 && k <= experts, "hwk_moe_route: k=%u of %u experts", k, experts);
   HWK_CHECK(score == HWK_SCORE_SOFTMAX || score == HWK_SCORE_SIGMOID, "hwk_moe_route: score %d", score);
   if (rows == 0) return nullptr;
-  hipLaunchKernelGGL(k_moe_route, dim3(rows), dim3(64), 0, (hipStream_t)stream, (const float *)logits,
-                     (const float *)bias, (int32_t *)idx, (float *)w, experts, k, score, norm,
+  hipLaunchKernelGGL(k_moe_route, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, (const float *)logits,
+                     (const float *)bias, (int32_t *)idx, (float *)w, rows, experts, k, score, norm,
                      hwk::f32_of_bits(scale_bits));
   return hwk::launched("hwk_moe_route");
 }
 
-// Layout: act (tokens, k, I) fp32 | ydown (tokens, k, H) fp32.
+// Layout: act (tokens, k, I) fp32.
 HWK_API size_t hwk_moe_workspace_bytes(const hwk_moe_params *p) {
   if (!p) return 0;
-  return (size_t)p->tokens * p->k * (p->inter + p->hidden) * sizeof(float);
+  return (size_t)p->tokens * p->k * p->inter * sizeof(float);
 }
 
 HWK_API char *hwk_moe_experts(void *stream, const void *x, const void *idx, const void *w, const void *gu_w,
-                              const void *gu_e, const void *dn_w, const void *dn_e, void *out, void *workspace,
-                              size_t workspace_bytes, const hwk_moe_params *p) {
-  HWK_CHECK(p, "hwk_moe_experts: null params");
+                              const void *gu_e, const void *gu_b, const void *dn_w, const void *dn_e,
+                              const void *dn_b, void *out, void *workspace, size_t workspace_bytes,
+                              const hwk_moe_params *p) {
+  HWK_Q(check_params("hwk_moe_experts", p));
   HWK_CHECK(x && idx && w && gu_w && gu_e && dn_w && dn_e && out && workspace, "hwk_moe_experts: null pointer");
-  HWK_CHECK(p->tokens >= 1 && p->tokens <= 8, "hwk_moe_experts: %u tokens (1..8)", p->tokens);
-  HWK_CHECK(p->experts >= 1 && p->experts <= 64, "hwk_moe_experts: %u experts (1..64)", p->experts);
-  HWK_CHECK(p->k >= 1 && p->k <= p->experts && p->tokens * p->k <= 64, "hwk_moe_experts: k=%u", p->k);
-  HWK_CHECK(p->hidden % 32 == 0 && p->hidden > 0 && p->hidden <= 8192, "hwk_moe_experts: hidden %u", p->hidden);
-  HWK_CHECK(p->inter % 32 == 0 && p->inter > 0 && p->inter <= 8192, "hwk_moe_experts: inter %u", p->inter);
-  HWK_CHECK(p->out_mode == HWK_OUT_F32 || p->out_mode == HWK_OUT_ADD_F32, "hwk_moe_experts: out_mode %u", p->out_mode);
   HWK_CHECK(hwk::aligned(x, 16) && hwk::aligned(gu_w, 16) && hwk::aligned(dn_w, 16) && hwk::aligned(workspace, 16),
             "hwk_moe_experts: x, weights and workspace must be 16-byte aligned");
   HWK_CHECK(workspace_bytes >= hwk_moe_workspace_bytes(p), "hwk_moe_experts: workspace %zu bytes, %zu needed",
             workspace_bytes, hwk_moe_workspace_bytes(p));
+  return run_experts<false>((hipStream_t)stream, x, nullptr, nullptr, (int32_t *)idx, (float *)w, gu_w, gu_e,
+                            (const float *)gu_b, dn_w, dn_e, (const float *)dn_b, (float *)out, (float *)workspace,
+                            args_of(p), "hwk_moe_experts");
+}
+
+HWK_API char *hwk_moe_layer(void *stream, const void *x, const void *logits, const void *router_bias, void *idx,
+                            void *w, const void *gu_w, const void *gu_e, const void *gu_b, const void *dn_w,
+                            const void *dn_e, const void *dn_b, void *out, void *workspace, size_t workspace_bytes,
+                            const hwk_moe_params *p) {
+  HWK_Q(check_params("hwk_moe_layer", p));
+  HWK_CHECK(x && logits && idx && w && gu_w && gu_e && dn_w && dn_e && out && workspace,
+            "hwk_moe_layer: null pointer");
+  HWK_CHECK(p->score == HWK_SCORE_SOFTMAX || p->score == HWK_SCORE_SIGMOID, "hwk_moe_layer: score %u", p->score);
+  HWK_CHECK(hwk::aligned(x, 16) && hwk::aligned(gu_w, 16) && hwk::aligned(dn_w, 16) && hwk::aligned(workspace, 16),
+            "hwk_moe_layer: x, weights and workspace must be 16-byte aligned");
+  HWK_CHECK(workspace_bytes >= hwk_moe_workspace_bytes(p), "hwk_moe_layer: workspace %zu bytes, %zu needed",
+            workspace_bytes, hwk_moe_workspace_bytes(p));
+  const MoeArgs a = args_of(p);
   hipStream_t st = (hipStream_t)stream;
-  float *act = (float *)workspace;
-  const int32_t *id = (const int32_t *)idx;
-  const uint32_t unique_max = p->tokens * p->k < p->experts ? p->tokens * p->k : p->experts;
-  constexpr int PPW = 2;
-  const dim3 g1((p->inter + 4 * PPW - 1) / (4 * PPW), unique_max);
-  const uint32_t nbh = p->hidden / 32;
-  const int bpl1 = (int)((nbh + 63) / 64);
-#define HWK_GU(B) \
-  hipLaunchKernelGGL((k_moe_gate_up<B, PPW>), g1, dim3(256), 0, st, (const uint4 *)x, id, (const uint4 *)gu_w, \
-                     (const uint8_t *)gu_e, act, p->tokens, p->hidden, p->inter, p->k)
-  switch (bpl1) {
-    case 1: HWK_GU(1); break;
-    case 2: HWK_GU(2); break;
-    case 3: HWK_GU(3); break;
-    default: HWK_GU(4); break;
-  }
-#undef HWK_GU
-  if (char *err = hwk::launched("hwk_moe_experts (gate_up)")) return err;
-  // down: lanes a row by I/32 blocks, the fewest idle slots (8 lanes x 3 blocks for I = 768)
-  const uint32_t nbi = p->inter / 32;
-  float *yd = act + (size_t)p->tokens * p->k * p->inter;
-  if (nbi <= 8) launch_down<8, 1>(st, act, id, dn_w, dn_e, yd, p, unique_max);
-  else if (nbi <= 16) launch_down<16, 1>(st, act, id, dn_w, dn_e, yd, p, unique_max);
-  else if (nbi <= 24) launch_down<8, 3>(st, act, id, dn_w, dn_e, yd, p, unique_max);
-  else if (nbi <= 32) launch_down<32, 1>(st, act, id, dn_w, dn_e, yd, p, unique_max);
-  else if (nbi <= 64) launch_down<64, 1>(st, act, id, dn_w, dn_e, yd, p, unique_max);
-  else if (nbi <= 128) launch_down<64, 2>(st, act, id, dn_w, dn_e, yd, p, unique_max);
-  else if (nbi <= 192) launch_down<64, 3>(st, act, id, dn_w, dn_e, yd, p, unique_max);
-  else launch_down<64, 4>(st, act, id, dn_w, dn_e, yd, p, unique_max);
-  if (char *err = hwk::launched("hwk_moe_experts (down)")) return err;
-  const uint32_t n = p->tokens * p->hidden;
-  hipLaunchKernelGGL(k_moe_combine, dim3((n + 255) / 256), dim3(256), 0, st, yd, id, (const float *)w, (float *)out,
-                     p->tokens, p->hidden, p->k, (int)p->out_mode);
-  return hwk::launched("hwk_moe_experts (combine)");
+  if (p->tokens <= kFoldRouteMaxTokens)
+    return run_experts<true>(st, x, (const float *)logits, (const float *)router_bias, (int32_t *)idx, (float *)w,
+                             gu_w, gu_e, (const float *)gu_b, dn_w, dn_e, (const float *)dn_b, (float *)out,
+                             (float *)workspace, a, "hwk_moe_layer");
+  hipLaunchKernelGGL(k_moe_route, dim3((p->tokens + 3) / 4), dim3(256), 0, st, (const float *)logits,
+                     (const float *)router_bias, (int32_t *)idx, (float *)w, p->tokens, p->experts, p->k,
+                     (int)p->score, (int)p->norm, a.scale);
+  HWK_Q(hwk::launched("hwk_moe_layer (route)"));
+  return run_experts<false>(st, x, nullptr, nullptr, (int32_t *)idx, (float *)w, gu_w, gu_e, (const float *)gu_b,
+                            dn_w, dn_e, (const float *)dn_b, (float *)out, (float *)workspace, a, "hwk_moe_layer");
 }
 
 }  // extern "C"

@@ -19,6 +19,7 @@
 // and position are read on the device (hist[pos], pos), and the argmax writes the next token
 // and advances pos, so one captured graph replays for every step.
 #include <math.h>
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -188,6 +189,66 @@ __global__ void k_fill_f32(float *__restrict__ p, uint64_t n, float v) {
   if (i < n) p[i] = v;
 }
 
+// Rows of positions [from, from + gridDim.x) of every K/V cache, packed per position with the caches
+// in the order of tab (their base pointers): cache c's row is kvh heads x 128 fp16 (16 uint4 a
+// head). EXPORT copies the caches into packed, else packed into the caches.
+template <bool EXPORT>
+__global__ __launch_bounds__(256) void k_kv_rows(const uint64_t *__restrict__ tab, uint4 *__restrict__ packed,
+                                                 uint32_t from, uint32_t ncache, uint32_t kvh, uint32_t cap) {
+  const uint32_t p = blockIdx.x, c = blockIdx.y, per = kvh * 16;
+  uint4 *cache = (uint4 *)tab[c];
+  uint4 *pk = packed + ((size_t)p * ncache + c) * per;
+  for (uint32_t i = threadIdx.x; i < per; i += 256) {
+    uint4 *cell = cache + ((size_t)(i / 16) * cap + from + p) * 16 + i % 16;
+    if constexpr (EXPORT)
+      pk[i] = *cell;
+    else
+      *cell = pk[i];
+  }
+}
+
+// The greedy token of each row of logits (rows, n), one workgroup a row: strict > (the lowest index
+// of the largest value), a NaN at index 0 kept, as k_argmax.
+__global__ __launch_bounds__(1024) void k_argmax_rows(const float *__restrict__ x, uint32_t n,
+                                                      int32_t *__restrict__ out) {
+  __shared__ float sv[16];
+  __shared__ uint32_t si[16];
+  const float *row = x + (size_t)blockIdx.x * n;
+  const uint32_t t = threadIdx.x;
+  float bv = -__builtin_inff();
+  uint32_t bi = 0xffffffffu;
+  for (uint32_t i = t; i < n; i += 1024) better(bv, bi, row[i], i);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const uint32_t oi = __shfl_xor(bi, off, 64);
+    better(bv, bi, ov, oi);
+  }
+  if ((t & 63) == 0) {
+    sv[t >> 6] = bv;
+    si[t >> 6] = bi;
+  }
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < 16; w++) better(bv, bi, sv[w], si[w]);
+    const float x0 = row[0];
+    out[blockIdx.x] = (int32_t)((bi == 0xffffffffu || x0 != x0) ? 0 : bi);
+  }
+}
+
+// Keep of a verify: the greedy token of row kept-1 becomes the next step's token, past the kept rows.
+__global__ void k_keep(const int32_t *__restrict__ am, uint32_t kept, uint32_t start, int32_t *__restrict__ hist,
+                       int32_t *__restrict__ pos) {
+  hist[start + kept] = am[kept - 1];
+  *pos = (int32_t)(start + kept);
+}
+
+// The sequence moved to position p, with the token there set when tok >= 0.
+__global__ void k_rewind(int32_t *__restrict__ hist, int32_t *__restrict__ pos, uint32_t p, int32_t tok) {
+  if (tok >= 0) hist[p] = tok;
+  *pos = (int32_t)p;
+}
+
 }  // namespace
 
 struct hwk_qwen3 {
@@ -213,6 +274,10 @@ struct hwk_qwen3 {
   uint32_t *counter, *part_i;
   uint32_t step_chunk = 0, step_nchunk = 0;  // the decode attention's chunking (attn_step_layout)
   float *part_v, *logits;
+  uint64_t *cache_tab;  // the K/V caches' base pointers in the export order (kv_k_N_new / kv_v_N_new sorted)
+  float *vlogits;       // a verify's logits (kMaxVerify, vocab) and greedy tokens (kMaxVerify)
+  int32_t *vargmax;
+  uint32_t verify_start = 0, verify_n = 0;  // the last verify, until its keep (verify_n 0: none)
   float *h, *qkv, *gu;
   f16 *x16, *q16, *att16, *a16;
   void *ws;
@@ -228,6 +293,8 @@ struct hwk_qwen3 {
 };
 
 namespace {
+
+constexpr uint32_t kMaxVerify = 8;  // rows a speculative verify takes
 
 struct Carver {
   size_t off = 0;
@@ -275,6 +342,9 @@ void layout(hwk_qwen3 *m, uint8_t *base) {
   m->part_i = cv.take<uint32_t>(base, 4 * kArgBlocks);
   m->part_v = cv.take<float>(base, 4 * kArgBlocks);
   m->logits = cv.take<float>(base, 4ull * c.vocab);
+  m->cache_tab = cv.take<uint64_t>(base, 16ull * c.layers);
+  m->vlogits = cv.take<float>(base, 4ull * kMaxVerify * c.vocab);
+  m->vargmax = cv.take<int32_t>(base, 4ull * kMaxVerify);
   const size_t T = c.max_prompt;
   m->h = cv.take<float>(base, 4 * T * c.hidden);
   m->qkv = cv.take<float>(base, 4 * T * m->qkv_n);
@@ -374,6 +444,53 @@ char *prefill_piece(hwk_qwen3 *m, hipStream_t st, uint32_t T, uint32_t start, bo
   return hwk::launched("qwen3 argmax");
 }
 
+// y (T rows) = the linear of T fp16 vectors x, every weight row read once for each piece of
+// vectors whose fp16 copy fits K1r's 64 KB of LDS. mode F32 or ADD (fp32 y).
+char *rows_linear(hipStream_t st, const f16 *x, const hwk_qwen3::Lin &l, float *y, uint32_t T, int mode) {
+  const uint32_t per = (64u * 1024u) / (2u * l.cols);
+  for (uint32_t t0 = 0; t0 < T; t0 += per) {
+    const uint32_t tn = T - t0 < per ? T - t0 : per;
+    HWK_Q(hwk_mxfp4_gemv_rows(st, l.w, l.e, x + (size_t)t0 * l.cols, y + (size_t)t0 * l.rows, l.rows, l.cols, tn,
+                              mode));
+  }
+  return nullptr;
+}
+
+// A speculative verify: the T tokens in hist[start .. start+T-1] at those positions, every row
+// through the decoder (K1r linears, causal attention over the cache and the rows before it), the
+// head on every row into vlogits and each row's greedy token into vargmax. The values cross
+// kernels in fp16 where the decode step rounds them, so row t's logits are those of the decode
+// step at position start+t up to fp32 summation order. *pos is start throughout.
+char *verify_piece(hwk_qwen3 *m, hipStream_t st, uint32_t T, uint32_t start) {
+  const hwk_qwen3_config &c = m->c;
+  hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(1), 0, st, m->pos, (int32_t)start);
+  hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed, m->h, c.hidden, c.vocab);
+  HWK_Q(hwk::launched("qwen3 verify embed"));
+  const uint32_t slots = c.heads + 2 * c.kv_heads;
+  hwk_attn_params pp = m->ap;
+  pp.len = start + T;
+  pp.out_mode = HWK_OUT_F16;
+  for (auto &ly : m->L) {
+    HWK_Q(hwk::rmsnorm_f16(st, m->h, ly.in_norm, m->eps, m->x16, T, c.hidden));
+    HWK_Q(rows_linear(st, m->x16, ly.qkv, m->qkv, T, HWK_OUT_F32));
+    hipLaunchKernelGGL(k_qk_rope, dim3((slots + 3) / 4, T), dim3(256), 0, st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t,
+                       m->sin_t, m->pos, 0u, m->q16, ly.kc, ly.vc, c.heads, c.kv_heads, c.max_ctx, m->eps);
+    HWK_Q(hwk::launched("qwen3 verify qk_rope"));
+    HWK_Q(hwk_attn_prefill(st, m->q16, ly.kc, ly.vc, m->att16, T, start, &pp));
+    HWK_Q(rows_linear(st, m->att16, ly.o, m->h, T, HWK_OUT_ADD_F32));
+    HWK_Q(hwk::rmsnorm_f16(st, m->h, ly.post_norm, m->eps, m->x16, T, c.hidden));
+    HWK_Q(rows_linear(st, m->x16, ly.gu, m->gu, T, HWK_OUT_F32));
+    const uint64_t n = (uint64_t)T * c.inter;
+    hipLaunchKernelGGL(k_swiglu, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, m->gu, m->a16, n);
+    HWK_Q(hwk::launched("qwen3 verify swiglu"));
+    HWK_Q(rows_linear(st, m->a16, ly.down, m->h, T, HWK_OUT_ADD_F32));
+  }
+  HWK_Q(hwk::rmsnorm_f16(st, m->h, m->norm, m->eps, m->x16, T, c.hidden));
+  HWK_Q(hwk_f16_gemv_rows(st, m->embed, m->x16, m->vlogits, c.vocab, c.hidden, T, HWK_OUT_F32));
+  hipLaunchKernelGGL(k_argmax_rows, dim3(T), dim3(1024), 0, st, m->vlogits, c.vocab, m->vargmax);
+  return hwk::launched("qwen3 verify argmax");
+}
+
 }  // namespace
 
 extern "C" {
@@ -418,6 +535,16 @@ HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
     return err;
   }
   layout(m, m->base);
+  // the caches in the order of the reference's names sorted as strings (decode.go:484), for the
+  // rows export_rows packs
+  std::vector<std::pair<std::string, uint64_t>> caches;
+  for (uint32_t i = 0; i < c.layers; i++) {
+    caches.push_back({"kv_k_" + std::to_string(i) + "_new", (uint64_t)(uintptr_t)m->L[i].kc});
+    caches.push_back({"kv_v_" + std::to_string(i) + "_new", (uint64_t)(uintptr_t)m->L[i].vc});
+  }
+  std::sort(caches.begin(), caches.end());
+  std::vector<uint64_t> tab;
+  for (auto &cp : caches) tab.push_back(cp.second);
   // RoPE tables in float32 of float64 cos/sin (reference blocks.go:412-425, config.go:152-159)
   const uint32_t half = c.head_dim / 2;
   std::vector<float> ct((size_t)c.max_ctx * half), stb((size_t)c.max_ctx * half);
@@ -430,6 +557,7 @@ HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
     }
   char *err = nullptr;
   if ((e = hipMemcpy(m->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
+      (e = hipMemcpy(m->cache_tab, tab.data(), tab.size() * 8, hipMemcpyHostToDevice)) != hipSuccess ||
       (e = hipMemcpy(m->sin_t, stb.data(), stb.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
       (e = hipMemset(m->hist, 0, 4ull * (c.max_ctx + 1))) != hipSuccess || (e = hipMemset(m->pos, 0, 4)) != hipSuccess ||
       (e = hipMemset(m->counter, 0, 4)) != hipSuccess ||
@@ -520,6 +648,8 @@ HWK_API char *hwk_qwen3_tensor(hwk_qwen3 *m, const char *name, void **ptr, size_
     if (r == "post_norm") return put(ly.post_norm, 4ull * c.hidden);
     if (r == "q_norm") return put(ly.q_norm, 4ull * c.head_dim);
     if (r == "k_norm") return put(ly.k_norm, 4ull * c.head_dim);
+    if (r == "k_cache") return put(ly.kc, 2ull * c.kv_heads * c.max_ctx * c.head_dim);
+    if (r == "v_cache") return put(ly.vc, 2ull * c.kv_heads * c.max_ctx * c.head_dim);
   }
   return hwk::errf("hwk_qwen3_tensor: no tensor %s", name);
 }
@@ -551,6 +681,7 @@ HWK_API char *hwk_qwen3_prefill(hwk_qwen3 *m, void *stream, const int32_t *token
   }
   m->host_pos = start + n;
   m->started = true;
+  m->verify_n = 0;
   return nullptr;
 }
 
@@ -560,6 +691,7 @@ HWK_API char *hwk_qwen3_step(hwk_qwen3 *m, void *stream) {
   HWK_CHECK(m->host_pos + 1 < m->c.max_ctx, "hwk_qwen3_step: position %u is the last of %u", m->host_pos, m->c.max_ctx);
   HWK_Q(step(m, (hipStream_t)stream));
   m->host_pos++;
+  m->verify_n = 0;
   return nullptr;
 }
 
@@ -574,6 +706,7 @@ HWK_API char *hwk_qwen3_decode(hwk_qwen3 *m, void *stream, uint32_t steps) {
   for (uint32_t i = 0; i < many; i++) HWK_TRY("hipGraphLaunch", hipGraphLaunch(m->exec[1], (hipStream_t)stream));
   for (uint32_t i = 0; i < one; i++) HWK_TRY("hipGraphLaunch", hipGraphLaunch(m->exec[0], (hipStream_t)stream));
   m->host_pos += steps;
+  m->verify_n = 0;
   return nullptr;
 }
 
@@ -581,6 +714,95 @@ HWK_API char *hwk_qwen3_capture(hwk_qwen3 *m) {
   HWK_CHECK(m, "hwk_qwen3_capture: null model");
   HWK_Q(capture(m, 1, kGraphSteps));
   HWK_Q(capture(m, 0, 1));
+  return nullptr;
+}
+
+HWK_API char *hwk_qwen3_row_bytes(hwk_qwen3 *m, size_t *bytes) {
+  HWK_CHECK(m && bytes, "hwk_qwen3_row_bytes: null argument");
+  *bytes = 2ull * m->c.layers * m->c.kv_heads * m->c.head_dim * 2;
+  return nullptr;
+}
+
+HWK_API char *hwk_qwen3_export_rows(hwk_qwen3 *m, void *stream, uint32_t from, uint32_t to, void *dst) {
+  HWK_CHECK(m, "hwk_qwen3_export_rows: null model");
+  HWK_CHECK(from <= to && to <= m->c.max_ctx, "hwk_qwen3_export_rows: rows %u to %u of a cache of %u", from, to,
+            m->c.max_ctx);
+  if (to == from) return nullptr;
+  HWK_CHECK(dst, "hwk_qwen3_export_rows: null dst");
+  HWK_CHECK(hwk::aligned(dst, 16), "hwk_qwen3_export_rows: dst must be 16-byte aligned");
+  hipLaunchKernelGGL(k_kv_rows<true>, dim3(to - from, 2 * m->c.layers), dim3(256), 0, (hipStream_t)stream,
+                     m->cache_tab, (uint4 *)dst, from, 2 * m->c.layers, m->c.kv_heads, m->c.max_ctx);
+  return hwk::launched("hwk_qwen3_export_rows");
+}
+
+HWK_API char *hwk_qwen3_import_rows(hwk_qwen3 *m, void *stream, uint32_t from, const void *src, size_t bytes) {
+  HWK_CHECK(m, "hwk_qwen3_import_rows: null model");
+  const size_t rb = 2ull * m->c.layers * m->c.kv_heads * m->c.head_dim * 2;
+  HWK_CHECK(bytes % rb == 0, "hwk_qwen3_import_rows: %zu bytes of rows, not a multiple of %zu", bytes, rb);
+  const uint64_t n = bytes / rb;
+  HWK_CHECK((uint64_t)from + n <= m->c.max_ctx, "hwk_qwen3_import_rows: rows %u to %llu of a cache of %u", from,
+            (unsigned long long)(from + n), m->c.max_ctx);
+  if (n == 0) return nullptr;
+  HWK_CHECK(src, "hwk_qwen3_import_rows: null src");
+  HWK_CHECK(hwk::aligned(src, 16), "hwk_qwen3_import_rows: src must be 16-byte aligned");
+  hipLaunchKernelGGL(k_kv_rows<false>, dim3((uint32_t)n, 2 * m->c.layers), dim3(256), 0, (hipStream_t)stream,
+                     m->cache_tab, (uint4 *)src, from, 2 * m->c.layers, m->c.kv_heads, m->c.max_ctx);
+  return hwk::launched("hwk_qwen3_import_rows");
+}
+
+HWK_API char *hwk_qwen3_position(hwk_qwen3 *m, uint32_t *pos) {
+  HWK_CHECK(m && pos, "hwk_qwen3_position: null argument");
+  *pos = m->host_pos;
+  return nullptr;
+}
+
+HWK_API char *hwk_qwen3_rewind(hwk_qwen3 *m, void *stream, uint32_t pos, int32_t next_token) {
+  HWK_CHECK(m, "hwk_qwen3_rewind: null model");
+  HWK_CHECK(pos + 1 < m->c.max_ctx, "hwk_qwen3_rewind: position %u leaves no step in %u", pos, m->c.max_ctx);
+  HWK_CHECK(next_token < 0 || (uint32_t)next_token < m->c.vocab, "hwk_qwen3_rewind: token %d out of vocab %u",
+            next_token, m->c.vocab);
+  hipLaunchKernelGGL(k_rewind, dim3(1), dim3(1), 0, (hipStream_t)stream, m->hist, m->pos, pos, next_token);
+  HWK_Q(hwk::launched("hwk_qwen3_rewind"));
+  m->host_pos = pos;
+  m->started = true;
+  m->verify_n = 0;
+  return nullptr;
+}
+
+HWK_API char *hwk_qwen3_verify(hwk_qwen3 *m, void *stream, const int32_t *tokens, uint32_t n, void **logits,
+                               void **argmax) {
+  HWK_CHECK(m && tokens, "hwk_qwen3_verify: null argument");
+  HWK_CHECK(m->started, "hwk_qwen3_verify: no prompt yet");
+  HWK_CHECK(n >= 1 && n <= kMaxVerify && n <= m->c.max_prompt, "hwk_qwen3_verify: %u tokens (1..%u, at most %u)", n,
+            kMaxVerify, m->c.max_prompt);
+  HWK_CHECK((uint64_t)m->host_pos + n < m->c.max_ctx, "hwk_qwen3_verify: positions %u+%u leave no room in %u",
+            m->host_pos, n, m->c.max_ctx);
+  for (uint32_t i = 0; i < n; i++)
+    HWK_CHECK(tokens[i] >= 0 && (uint32_t)tokens[i] < m->c.vocab, "hwk_qwen3_verify: token %d at %u out of vocab %u",
+              tokens[i], i, m->c.vocab);
+  hipStream_t st = (hipStream_t)stream;
+  HWK_TRY("hipStreamSynchronize", hipStreamSynchronize(st));
+  HWK_TRY("hipMemcpy", hipMemcpy(m->hist + m->host_pos, tokens, 4ull * n, hipMemcpyHostToDevice));
+  m->verify_n = 0;
+  HWK_Q(verify_piece(m, st, n, m->host_pos));
+  m->verify_start = m->host_pos;
+  m->verify_n = n;
+  if (logits) *logits = m->vlogits;
+  if (argmax) *argmax = m->vargmax;
+  return nullptr;
+}
+
+HWK_API char *hwk_qwen3_keep(hwk_qwen3 *m, void *stream, uint32_t kept) {
+  HWK_CHECK(m, "hwk_qwen3_keep: null model");
+  HWK_CHECK(m->verify_n > 0, "hwk_qwen3_keep: no verify to keep rows of");
+  HWK_CHECK(kept >= 1 && kept <= m->verify_n, "hwk_qwen3_keep: %u of %u rows kept", kept, m->verify_n);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_keep, dim3(1), dim3(1), 0, st, m->vargmax, kept, m->verify_start, m->hist, m->pos);
+  HWK_Q(hwk::launched("hwk_qwen3_keep"));
+  HWK_TRY("hipMemcpyAsync", hipMemcpyAsync(m->logits, m->vlogits + (size_t)(kept - 1) * m->c.vocab,
+                                           4ull * m->c.vocab, hipMemcpyDeviceToDevice, st));
+  m->host_pos = m->verify_start + kept;
+  m->verify_n = 0;
   return nullptr;
 }
 

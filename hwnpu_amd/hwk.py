@@ -12,7 +12,7 @@ import ctypes as C
 import os
 import threading
 
-ABI = 2
+ABI = 3
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libhwk.so")
@@ -49,10 +49,12 @@ class AttnParams(C.Structure):
 class MoeParams(C.Structure):
     """hwk_moe_params (include/hwk.h)."""
     _fields_ = [("tokens", U32), ("hidden", U32), ("inter", U32), ("experts", U32), ("k", U32),
-                ("out_mode", U32)]
+                ("out_mode", U32), ("act", U32), ("alpha_bits", U32), ("limit_bits", U32), ("score", U32),
+                ("norm", U32), ("scale_bits", U32)]
 
 
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+ACT_SILU, ACT_GPTOSS = 0, 1
 
 
 class KernelInfo(C.Structure):
@@ -115,6 +117,7 @@ SIGNATURES = {
     "hwk_mxfp4_gemv_rows": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int]),
     "hwk_i8_gemv": (ERR, [P, P, P, P, P, U32, U32, C.c_int]),
     "hwk_f16_gemv": (ERR, [P, P, P, P, U32, U32, C.c_int]),
+    "hwk_f16_gemv_rows": (ERR, [P, P, P, P, U32, U32, U32, C.c_int]),
     "hwk_rope_tables": (ERR, [U64, U32, U32, U32, P, P]),
     "hwk_rmsnorm": (ERR, [P, P, P, P, U32, U32, U64, C.c_int]),
     "hwk_rope": (ERR, [P, P, P, P, P, P, U32, U32, U32, U32, U32, U64, C.c_int]),
@@ -141,9 +144,17 @@ SIGNATURES = {
     "hwk_qwen3_step": (ERR, [P, P]),
     "hwk_qwen3_decode": (ERR, [P, P, U32]),
     "hwk_qwen3_capture": (ERR, [P]),
+    "hwk_qwen3_row_bytes": (ERR, [P, C.POINTER(SZ)]),
+    "hwk_qwen3_export_rows": (ERR, [P, P, U32, U32, P]),
+    "hwk_qwen3_import_rows": (ERR, [P, P, U32, P, SZ]),
+    "hwk_qwen3_position": (ERR, [P, C.POINTER(U32)]),
+    "hwk_qwen3_rewind": (ERR, [P, P, U32, I32]),
+    "hwk_qwen3_verify": (ERR, [P, P, C.POINTER(I32), U32, C.POINTER(P), C.POINTER(P)]),
+    "hwk_qwen3_keep": (ERR, [P, P, U32]),
     "hwk_moe_route": (ERR, [P, P, P, P, P, U32, U32, U32, C.c_int, C.c_int, U32]),
     "hwk_moe_workspace_bytes": (SZ, [C.POINTER(MoeParams)]),
-    "hwk_moe_experts": (ERR, [P, P, P, P, P, P, P, P, P, P, SZ, C.POINTER(MoeParams)]),
+    "hwk_moe_experts": (ERR, [P, P, P, P, P, P, P, P, P, P, P, P, SZ, C.POINTER(MoeParams)]),
+    "hwk_moe_layer": (ERR, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, SZ, C.POINTER(MoeParams)]),
     "hwk_synth_bytes": (ERR, [P, P, U64, U64]),
     "hwk_synth_uniform": (ERR, [P, P, U64, U64, I32, U32, C.c_int]),
     "hwk_synth_normal": (ERR, [P, P, U64, U64, U32, C.c_int]),

@@ -108,6 +108,17 @@ def f16_gemv(w, x, out_mode="f32", y=None):
     return y
 
 
+def f16_gemv_rows(w, x, out_mode="f32", y=None):
+    """Y (T, n) = X W^T for fp16 W (n, k) and T <= 8 fp16 vectors X (T, k), W read once for all."""
+    n, k = w.shape
+    T = x.shape[0]
+    _need(w, "w", torch.float16, (n, k))
+    _need(x, "x", torch.float16, (T, k))
+    y = _out2(y, T, n, out_mode, w.device)
+    hwk.load().hwk_f16_gemv_rows(_stream(), w.data_ptr(), x.data_ptr(), y.data_ptr(), n, k, T, OUT_MODES[out_mode])
+    return y
+
+
 def _out2(y, m, n, mode, device):
     dt = torch.float16 if mode == "f16" else torch.float32
     if y is None:
@@ -282,34 +293,85 @@ def moe_route(logits, k, score="softmax", norm=True, scale=0.0, bias=None):
     return idx, w
 
 
-def moe_experts(x, idx, w, gu_w, gu_e, dn_w, dn_e, out=None, out_mode="f32", workspace=None):
-    """The chosen experts' SwiGLU FFNs: x fp16 (T, H); gu_w uint8 (E, 2I, H/32, 16), gu_e (E, 2I, H/32);
-    dn_w (E, H, I/32, 16), dn_e (E, H, I/32); out fp32 (T, H)."""
+def _moe_params(T, H, I, E, k, out_mode, act, alpha, limit, score="softmax", norm=True, scale=0.0):
+    if act not in ("silu", "gptoss"):
+        raise ValueError(f"act {act!r}: 'silu' or 'gptoss'")
+    p = hwk.MoeParams()
+    p.tokens, p.hidden, p.inter, p.experts, p.k = T, H, I, E, k
+    p.out_mode = OUT_MODES[out_mode]
+    p.act = hwk.ACT_SILU if act == "silu" else hwk.ACT_GPTOSS
+    p.alpha_bits, p.limit_bits = f32_bits(alpha), f32_bits(limit)
+    p.score = hwk.SCORE_SOFTMAX if score == "softmax" else hwk.SCORE_SIGMOID
+    p.norm, p.scale_bits = 1 if norm else 0, f32_bits(scale)
+    return p
+
+
+def _moe_operands(x, gu_w, gu_e, dn_w, dn_e, gu_b, dn_b):
     T, H = x.shape
     E, I2 = gu_e.shape[0], gu_e.shape[1]
     I = I2 // 2
-    k = idx.shape[1]
     _need(x, "x", torch.float16, (T, H))
-    _need(idx, "idx", torch.int32, (T, k))
-    _need(w, "w", torch.float32, (T, k))
     _need(gu_w, "gu_w", torch.uint8, (E, I2, H // 32, 16))
     _need(gu_e, "gu_e", torch.uint8, (E, I2, H // 32))
     _need(dn_w, "dn_w", torch.uint8, (E, H, I // 32, 16))
     _need(dn_e, "dn_e", torch.uint8, (E, H, I // 32))
-    p = hwk.MoeParams()
-    p.tokens, p.hidden, p.inter, p.experts, p.k = T, H, I, E, k
-    p.out_mode = OUT_MODES[out_mode]
+    if gu_b is not None:
+        _need(gu_b, "gu_b", torch.float32, (E, I2))
+    if dn_b is not None:
+        _need(dn_b, "dn_b", torch.float32, (E, H))
+    return T, H, I, E
+
+
+def _moe_out(out, out_mode, T, H, device):
     if out is None:
         if out_mode == "add":
             raise ValueError("out_mode 'add' needs out")
-        out = torch.empty((T, H), dtype=torch.float32, device=x.device)
-    else:
-        _need(out, "out", torch.float32, (T, H))
+        return torch.empty((T, H), dtype=torch.float32, device=device)
+    _need(out, "out", torch.float32, (T, H))
+    return out
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def moe_experts(x, idx, w, gu_w, gu_e, dn_w, dn_e, out=None, out_mode="f32", workspace=None, gu_b=None, dn_b=None,
+                act="silu", alpha=1.702, limit=7.0):
+    """The chosen experts' gated FFNs: x fp16 (T, H); gu_w uint8 (E, 2I, H/32, 16), gu_e (E, 2I, H/32);
+    dn_w (E, H, I/32, 16), dn_e (E, H, I/32); optional fp32 biases gu_b (E, 2I), dn_b (E, H); act 'silu'
+    or 'gptoss' (alpha, limit); out fp32 (T, H)."""
+    T, H, I, E = _moe_operands(x, gu_w, gu_e, dn_w, dn_e, gu_b, dn_b)
+    k = idx.shape[1]
+    _need(idx, "idx", torch.int32, (T, k))
+    _need(w, "w", torch.float32, (T, k))
+    p = _moe_params(T, H, I, E, k, out_mode, act, alpha, limit)
+    out = _moe_out(out, out_mode, T, H, x.device)
     n = hwk.load().hwk_moe_workspace_bytes(p)
     ws = torch.empty(max(n, 16), dtype=torch.uint8, device=x.device) if workspace is None else workspace
     hwk.load().hwk_moe_experts(_stream(), x.data_ptr(), idx.data_ptr(), w.data_ptr(), gu_w.data_ptr(), gu_e.data_ptr(),
-                               dn_w.data_ptr(), dn_e.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), p)
+                               _ptr(gu_b), dn_w.data_ptr(), dn_e.data_ptr(), _ptr(dn_b), out.data_ptr(),
+                               ws.data_ptr(), ws.numel(), p)
     return out
+
+
+def moe_layer(x, logits, k, gu_w, gu_e, dn_w, dn_e, out=None, out_mode="f32", workspace=None, gu_b=None, dn_b=None,
+              act="silu", alpha=1.702, limit=7.0, score="softmax", norm=True, scale=0.0, router_bias=None):
+    """Route (Routing.Choose of fp32 logits (T, E)) and run the chosen experts in two launches;
+    returns (out, idx, w)."""
+    T, H, I, E = _moe_operands(x, gu_w, gu_e, dn_w, dn_e, gu_b, dn_b)
+    _need(logits, "logits", torch.float32, (T, E))
+    if router_bias is not None:
+        _need(router_bias, "router_bias", torch.float32, (E,))
+    p = _moe_params(T, H, I, E, k, out_mode, act, alpha, limit, score, norm, scale)
+    out = _moe_out(out, out_mode, T, H, x.device)
+    idx = torch.empty((T, k), dtype=torch.int32, device=x.device)
+    w = torch.empty((T, k), dtype=torch.float32, device=x.device)
+    n = hwk.load().hwk_moe_workspace_bytes(p)
+    ws = torch.empty(max(n, 16), dtype=torch.uint8, device=x.device) if workspace is None else workspace
+    hwk.load().hwk_moe_layer(_stream(), x.data_ptr(), logits.data_ptr(), _ptr(router_bias), idx.data_ptr(),
+                             w.data_ptr(), gu_w.data_ptr(), gu_e.data_ptr(), _ptr(gu_b), dn_w.data_ptr(),
+                             dn_e.data_ptr(), _ptr(dn_b), out.data_ptr(), ws.data_ptr(), ws.numel(), p)
+    return out, idx, w
 
 
 # ---------------- the decoder's small ops (K6) ----------------

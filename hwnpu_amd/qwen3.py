@@ -105,6 +105,83 @@ class Qwen3:
         """Captures both step graphs now (no replay), so that decode() afterwards only replays."""
         hwk.load().hwk_qwen3_capture(self._h)
 
+    # ---- the session's cache and position (reference decode.Session, internal/llm/decode/decode.go) ----
+
+    def row_bytes(self) -> int:
+        """Bytes of one position's rows in export_rows (RowBytes, decode.go:1849-1855)."""
+        n = C.c_size_t()
+        hwk.load().hwk_qwen3_row_bytes(self._h, C.byref(n))
+        return n.value
+
+    def export_rows(self, start: int, end: int) -> torch.Tensor:
+        """The cache rows of positions [start, end) packed as ExportRows packs them (decode.go:1857-1881),
+        a uint8 tensor on the GPU of (end - start) * row_bytes() bytes."""
+        out = torch.empty(max(end - start, 0) * self.row_bytes(), dtype=torch.uint8, device="cuda")
+        hwk.load().hwk_qwen3_export_rows(self._h, _stream(), start, end, out.data_ptr())
+        return out
+
+    def import_rows(self, start: int, rows: torch.Tensor) -> None:
+        """Writes rows from export_rows at positions start on (ImportRows, decode.go:1883-1914)."""
+        if rows.dtype != torch.uint8 or not rows.is_cuda or not rows.is_contiguous():
+            raise ValueError("rows: a contiguous uint8 tensor on the GPU")
+        hwk.load().hwk_qwen3_import_rows(self._h, _stream(), start, rows.data_ptr(), rows.numel())
+
+    def position(self) -> int:
+        """The position the next step takes (a Mark of the sequence, decode.go:1120-1137)."""
+        p = C.c_uint32()
+        hwk.load().hwk_qwen3_position(self._h, C.byref(p))
+        return p.value
+
+    def mark(self) -> int:
+        return self.position()
+
+    def rewind(self, pos: int, next_token: int = -1) -> None:
+        """Back to a mark (Rewind, decode.go:1190-1203); next_token >= 0 is written as the token the
+        next step takes."""
+        hwk.load().hwk_qwen3_rewind(self._h, _stream(), pos, next_token)
+
+    def save(self):
+        """A mark with the rows before it and the token the next step takes (Save, decode.go:1180-1188)."""
+        pos = self.position()
+        return pos, self.export_rows(0, pos), int(self.history(pos, 1)[0])
+
+    def resume(self, saved) -> None:
+        """Brings the sequence to a saved point, in this session or another of the same model (Resume,
+        decode.go:1930-1968)."""
+        pos, rows, tok = saved
+        if rows.numel() != pos * self.row_bytes():
+            raise ValueError(f"{rows.numel()} bytes of rows for a mark at {pos}, want {pos * self.row_bytes()}")
+        self.import_rows(0, rows)
+        self.rewind(pos, tok)
+
+    def verify(self, tokens):
+        """Runs tokens (the next step's token, then drafts; at most 8) at the next positions and
+        returns the logits after each (fp32 (n, vocab)) and each row's greedy token; the position
+        moves only with keep()."""
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        lg, am = C.c_void_p(), C.c_void_p()
+        hwk.load().hwk_qwen3_verify(self._h, _stream(), toks.ctypes.data_as(C.POINTER(C.c_int32)), toks.size,
+                                    C.byref(lg), C.byref(am))
+        n = toks.size
+        return d2h(lg.value, 4 * n * self.vocab, np.float32).reshape(n, self.vocab), d2h(am.value, 4 * n, np.int32)
+
+    def keep(self, kept: int) -> None:
+        hwk.load().hwk_qwen3_keep(self._h, _stream(), kept)
+
+    def speculate(self, drafts):
+        """Greedy speculative decoding (Speculate, decode.go:1235-1261): verifies the next step's token
+        followed by the drafts, keeps the rows whose draft is the greedy token of the row before, and
+        returns (kept, the greedy tokens of the rows up to the last kept)."""
+        pos = self.position()
+        first = int(self.history(pos, 1)[0])
+        toks = [first] + [int(t) for t in drafts]
+        _, am = self.verify(toks)
+        kept = 1
+        while kept < len(toks) and int(am[kept - 1]) == toks[kept]:
+            kept += 1
+        self.keep(kept)
+        return kept, [int(t) for t in am[:kept]]
+
     def logits(self) -> np.ndarray:
         return d2h(self._logits, 4 * self.vocab, np.float32)
 

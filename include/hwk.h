@@ -29,7 +29,7 @@ extern "C" {
 
 /* The ABI version: a binding refuses a library of another (reference xrtshim.h:25-26, the XS_ABI
  * check of internal/backend/amdxrt/shim.go:25-26). */
-#define HWK_ABI 2
+#define HWK_ABI 3
 
 typedef struct hwk_device hwk_device;
 typedef struct hwk_buf hwk_buf;
@@ -196,6 +196,12 @@ HWK_API char *hwk_mxfp4_gemm(void *stream, const void *x, const void *w, const v
  * internal/llm/qwen3/build.go:107-109). k a multiple of 8. */
 HWK_API char *hwk_f16_gemv(void *stream, const void *w, const void *x, void *y, uint32_t n,
                            uint32_t k, int out_mode);
+/* K7r: Y (T, n) = X (T, k) W^T for fp16 W (n, k) and T <= 8 fp16 vectors, each row of W read once
+ * for all of them: the tied head over the rows of a speculative verify (the head of
+ * internal/llm/qwen3/build.go:107-109 on every row, as decode.Session.Speculate asks for the logits
+ * after each token, internal/llm/decode/decode.go:1235-1261). k a multiple of 8, T*k*2 <= 64 KB. */
+HWK_API char *hwk_f16_gemv_rows(void *stream, const void *w, const void *x, void *y, uint32_t n,
+                                uint32_t k, uint32_t tokens, int out_mode);
 
 /* ---- the decoder's small ops (K6): what the reference's graph runs between the linears
  * (internal/llm/blocks/blocks.go, internal/llm/qwen3/build.go:107-311). Float scalars travel as
@@ -312,27 +318,46 @@ enum { HWK_SCORE_SOFTMAX = 0, HWK_SCORE_SIGMOID = 1 };
 HWK_API char *hwk_moe_route(void *stream, const void *logits, const void *bias, void *idx, void *w, uint32_t rows,
                             uint32_t experts, uint32_t k, int score, int norm, uint32_t scale_bits);
 
+/* Gated units of the experts (reference internal/llm/experts/host.go:44-57). */
+enum { HWK_ACT_SILU = 0, HWK_ACT_GPTOSS = 1 };
+
 typedef struct hwk_moe_params {
-  uint32_t tokens;   /* rows of x (1..8) */
-  uint32_t hidden;   /* H, a multiple of 32, at most 8192 */
-  uint32_t inter;    /* I, a multiple of 32, at most 8192 */
-  uint32_t experts;  /* E (<= 64) */
-  uint32_t k;        /* experts a token (tokens * k <= 64) */
-  uint32_t out_mode; /* HWK_OUT_F32 (out = the experts' sum) or HWK_OUT_ADD_F32 (out += it) */
+  uint32_t tokens;     /* rows of x (1..8) */
+  uint32_t hidden;     /* H, a multiple of 32, at most 8192 */
+  uint32_t inter;      /* I, a multiple of 32, at most 8192 */
+  uint32_t experts;    /* E (<= 64) */
+  uint32_t k;          /* experts a token (tokens * k <= 64) */
+  uint32_t out_mode;   /* HWK_OUT_F32 (out = the experts' sum) or HWK_OUT_ADD_F32 (out += it) */
+  uint32_t act;        /* HWK_ACT_SILU: silu(g)*u; HWK_ACT_GPTOSS: g = min(g, limit),
+                        * u = clamp(u, -limit, limit), g*sigmoid(alpha*g)*(u+1) (host.go:516-527) */
+  uint32_t alpha_bits; /* float32 bits of alpha (gpt-oss 1.702) */
+  uint32_t limit_bits; /* float32 bits of limit (gpt-oss 7) */
+  uint32_t score;      /* hwk_moe_layer's routing: HWK_SCORE_SOFTMAX or HWK_SCORE_SIGMOID */
+  uint32_t norm;       /* hwk_moe_layer's routing: 1 to normalize the chosen weights */
+  uint32_t scale_bits; /* hwk_moe_layer's routing: float32 bits of the weights' scale (0: none) */
 } hwk_moe_params;
 
-/* Device workspace of hwk_moe_experts: the SwiGLU activations, fp32 (tokens*k, I), then the
- * experts' unweighted down outputs, fp32 (tokens*k, H). */
+/* Device workspace of hwk_moe_experts / hwk_moe_layer: the gated activations, fp32 (tokens*k, I). */
 HWK_API size_t hwk_moe_workspace_bytes(const hwk_moe_params *p);
-/* K5b: the chosen experts of each token (reference experts.Host.Run, host.go:723-882, without
- * biases, SiLU unit): gate_up MXFP4 (E, 2I, H/32, 16) codes + (E, 2I, H/32) scales with the gate
- * on the even rows; act = silu(gate x) * (up x) in fp32; down MXFP4 (E, H, I/32, 16) + (E, H,
- * I/32); out[t] (+)= sum over its experts in ascending expert id of w * (down act). An expert's
- * rows are read once for all the tokens that chose it. x fp16 (tokens, H); idx int32 and w fp32
- * (tokens, k) as hwk_moe_route writes them; out fp32 (tokens, H). */
+/* K5b: the chosen experts of each token (reference experts.Host.Run / runRow, host.go:478-579,
+ * 723-882): gate_up MXFP4 (E, 2I, H/32, 16) codes + (E, 2I, H/32) scales with the gate on the even
+ * rows, plus the bias gu_b fp32 (E, 2I) (NULL: none); act = the gated unit of (gate, up) in fp32;
+ * down MXFP4 (E, H, I/32, 16) + (E, H, I/32); out[t] (+)= sum over its experts in ascending expert
+ * id of w * (down act + dn_b) with dn_b fp32 (E, H) (NULL: none). An expert's rows are read once for
+ * all the tokens that chose it. Two launches. x fp16 (tokens, H); idx int32 and w fp32 (tokens, k)
+ * as hwk_moe_route writes them; out fp32 (tokens, H). */
 HWK_API char *hwk_moe_experts(void *stream, const void *x, const void *idx, const void *w, const void *gu_w,
-                              const void *gu_e, const void *dn_w, const void *dn_e, void *out, void *workspace,
-                              size_t workspace_bytes, const hwk_moe_params *p);
+                              const void *gu_e, const void *gu_b, const void *dn_w, const void *dn_e,
+                              const void *dn_b, void *out, void *workspace, size_t workspace_bytes,
+                              const hwk_moe_params *p);
+/* The MoE layer as chain.moe.runHost runs it (internal/llm/chain/moe.go:582-610): Routing.Choose of
+ * the router logits fp32 (tokens, E) with router_bias (E) or NULL, per p's score, norm and scale
+ * (as hwk_moe_route), then hwk_moe_experts, in two launches: the route is folded into the gate_up
+ * launch. idx and w (tokens, k) are written for the caller. */
+HWK_API char *hwk_moe_layer(void *stream, const void *x, const void *logits, const void *router_bias, void *idx,
+                            void *w, const void *gu_w, const void *gu_e, const void *gu_b, const void *dn_w,
+                            const void *dn_e, const void *dn_b, void *out, void *workspace,
+                            size_t workspace_bytes, const hwk_moe_params *p);
 
 /* ---- the Qwen3 decoder on the device (the shape of reference internal/llm/qwen3, build.go:107-311,
  * driven the way internal/llm/iron/model.go:578 Step(token, pos) -> logits drives a device-resident
@@ -370,6 +395,7 @@ HWK_API char *hwk_qwen3_synth(hwk_qwen3 *m, void *stream, uint64_t seed, uint32_
  *   layers.{i}.down.blocks/.scales     MXFP4 (hidden, inter)
  *   layers.{i}.input_norm, .post_norm  fp32 (hidden); layers.{i}.q_norm, .k_norm fp32 (head_dim)
  *   norm fp32 (hidden); embed fp16 (vocab, hidden)
+ *   layers.{i}.k_cache, .v_cache       fp16 (kv_heads, max_ctx, head_dim)
  * blocks are (rows, cols/32, 16) bytes, scales (rows, cols/32) e8m0. */
 HWK_API char *hwk_qwen3_tensor(hwk_qwen3 *m, const char *name, void **ptr, size_t *bytes);
 /* The device state: logits fp32 (vocab) of the last processed row; the token history int32
@@ -388,6 +414,42 @@ HWK_API char *hwk_qwen3_decode(hwk_qwen3 *m, void *stream, uint32_t steps);
 /* Captures and instantiates both step graphs now, without running them, so that a later
  * hwk_qwen3_decode only replays (no capture inside a caller's timed region). */
 HWK_API char *hwk_qwen3_capture(hwk_qwen3 *m);
+
+/* ---- the session's cache and position (reference decode.Session, internal/llm/decode/
+ * decode.go:1107-1210, 1849-1968; the prompt store's rows, internal/chat/store.go) ---- */
+
+/* Bytes of one position's rows in hwk_qwen3_export_rows: K and V of every layer, kv_heads x
+ * head_dim fp16 each (RowBytes, decode.go:1849-1855). */
+HWK_API char *hwk_qwen3_row_bytes(hwk_qwen3 *m, size_t *bytes);
+/* Packs the cache rows of positions [from, to) into dst (device memory, (to-from) x row_bytes):
+ * per position, the caches in the order of their reference names kv_k_N_new / kv_v_N_new sorted as
+ * strings (kv_k_0, kv_k_1, kv_k_10, ...; decode.go:484), each kv_heads rows of head_dim fp16
+ * (ExportRows, decode.go:1857-1881). to <= max_ctx. */
+HWK_API char *hwk_qwen3_export_rows(hwk_qwen3 *m, void *stream, uint32_t from, uint32_t to, void *dst);
+/* Writes rows packed as export_rows packs them (bytes a multiple of row_bytes, device memory) at
+ * positions from on; the position does not move (ImportRows, decode.go:1883-1914). */
+HWK_API char *hwk_qwen3_import_rows(hwk_qwen3 *m, void *stream, uint32_t from, const void *src,
+                                   size_t bytes);
+/* The position the next step takes: a mark of the sequence (Mark, decode.go:1120-1137; the model
+ * has no rings or windows, so a mark is its position). */
+HWK_API char *hwk_qwen3_position(hwk_qwen3 *m, uint32_t *pos);
+/* Moves the sequence to position pos (< max_ctx - 1): the next step takes hist[pos] at pos, and
+ * next_token >= 0 is first written there. Back to a mark (Rewind, decode.go:1190-1203: the rows
+ * before pos must be those of the mark), or, after import_rows, to the end of imported rows
+ * (Resume, decode.go:1930-1968). */
+HWK_API char *hwk_qwen3_rewind(hwk_qwen3 *m, void *stream, uint32_t pos, int32_t next_token);
+/* Speculative verify (Speculate, decode.go:1235-1261; ironSession.SpeculateTokens,
+ * internal/chat/iron.go:169): runs n host tokens (1..8, at most max_prompt; the first is the
+ * token the next step would take, the rest drafts) at positions pos .. pos+n-1, writing their K/V,
+ * and gives the logits after each row (*logits: fp32 (n, vocab)) and each row's greedy token
+ * (*argmax: int32 (n)), device memory valid until the next verify. The position does not move
+ * until hwk_qwen3_keep. */
+HWK_API char *hwk_qwen3_verify(hwk_qwen3 *m, void *stream, const int32_t *tokens, uint32_t n,
+                               void **logits, void **argmax);
+/* Keeps the first kept (1..n) rows of the last verify: pos moves past them, hist[pos] = the greedy
+ * token of row kept-1 and the state's logits are that row's. The K/V of the rows not kept are
+ * never read: the steps after write each position before they attend to it. */
+HWK_API char *hwk_qwen3_keep(hwk_qwen3 *m, void *stream, uint32_t kept);
 
 /* ---- synthetic inputs, reproducible from (seed, name) alone: splitmix64 counter streams keyed
  * by seed ^ fnv64a(name) (the role of reference internal/llm/synth.go:12-56). Each element i

@@ -55,21 +55,34 @@ void or_choose(const float *logits, const float *bias, int n, int k, int score, 
   free(order);
 }
 
-/* host.go:543-547 / :836-840: silu(g)*u with exp in float64 rounded to float32 */
-static float act_silu(float g, float u) { return g / (1 + (float)exp((double)(-g))) * u; }
+/* The gated unit (host.go:516-527): SiLU g/(1+e^-g)*u, or gpt-oss's: g = min(g, limit),
+ * u = clamp(u, -limit, limit), g/(1+e^(-alpha*g))*(u+1); exp in float64 rounded to float32, every
+ * other step a float32 operation (Go evaluates left to right, no fused multiply-add on amd64). */
+static float act_unit(float g, float u, int act, float alpha, float limit) {
+  if (act == 1) {
+    g = g < limit ? g : limit;
+    u = u > -limit ? u : -limit;
+    u = u < limit ? u : limit;
+    float ag = alpha * g;
+    return g / (1 + (float)exp((double)(-ag))) * (u + 1);
+  }
+  return g / (1 + (float)exp((double)(-g))) * u;
+}
 
 /* The experts each row chose, run once for all the rows that chose them (host.go:769-773), added
  * to the rows' outputs in ascending expert id (host.go:566-578, :866-881 walks experts by id). */
 static void experts_common(int quantized, const float *x, int T, const int32_t *idx,
                            const float *w, int k, const uint8_t *gu_w, const uint8_t *gu_e,
-                           const uint8_t *dn_w, const uint8_t *dn_e, int E, int H, int I,
-                           float *out, int threads) {
+                           const float *gu_b, const uint8_t *dn_w, const uint8_t *dn_e,
+                           const float *dn_b, int E, int H, int I, int act_kind, float alpha,
+                           float limit, float *out, int threads) {
   if (threads <= 0) threads = or_max_threads();
   size_t gb = (size_t)2 * I * H / 2, ge = (size_t)2 * I * H / 32; /* an expert's gate_up bytes */
   size_t db = (size_t)H * I / 2, de = (size_t)H * I / 32;
   int nbG = H / 32, nbD = I / 32;
   float *gu = malloc(sizeof(float) * 2 * I);
   float *act = malloc(sizeof(float) * I);
+  const int actk = act_kind;
   float *y = malloc(sizeof(float) * H);
   float *rowbuf = malloc(sizeof(float) * (size_t)(H > I ? H : I));
   int8_t *qx = malloc((size_t)H), *qa = malloc((size_t)I);
@@ -96,7 +109,10 @@ static void experts_common(int quantized, const float *x, int T, const int32_t *
           gu[r] = acc;
         }
       }
-      for (int j = 0; j < I; j++) act[j] = act_silu(gu[2 * j], gu[2 * j + 1]); /* gate the even rows */
+      if (gu_b) /* host.go:505-512: the bias after the product */
+        for (int r = 0; r < 2 * I; r++) gu[r] += gu_b[(size_t)e * 2 * I + r];
+      for (int j = 0; j < I; j++) /* gate the even rows */
+        act[j] = act_unit(gu[2 * j], gu[2 * j + 1], actk, alpha, limit);
       if (quantized) {
         or_vec_quantize(qa, sa, act, I);
         or_mxfp4_run(y, dw, ds, H, nbD, qa, sa, 1, threads);
@@ -112,7 +128,8 @@ static void experts_common(int quantized, const float *x, int T, const int32_t *
       }
       float wt = w[t * k + kk];
       float *o = out + (size_t)t * H;
-      for (int c = 0; c < H; c++) o[c] += wt * y[c];
+      const float *b = dn_b ? dn_b + (size_t)e * H : NULL;
+      for (int c = 0; c < H; c++) o[c] += wt * (y[c] + (b ? b[c] : 0.0f)); /* host.go:570-577 */
     }
   }
   free(gu);
@@ -126,13 +143,17 @@ static void experts_common(int quantized, const float *x, int T, const int32_t *
 }
 
 void or_experts_f32(const float *x, int T, const int32_t *idx, const float *w, int k,
-                    const uint8_t *gu_w, const uint8_t *gu_e, const uint8_t *dn_w,
-                    const uint8_t *dn_e, int E, int H, int I, float *out, int threads) {
-  experts_common(0, x, T, idx, w, k, gu_w, gu_e, dn_w, dn_e, E, H, I, out, threads);
+                    const uint8_t *gu_w, const uint8_t *gu_e, const float *gu_b,
+                    const uint8_t *dn_w, const uint8_t *dn_e, const float *dn_b, int E, int H,
+                    int I, int act, float alpha, float limit, float *out, int threads) {
+  experts_common(0, x, T, idx, w, k, gu_w, gu_e, gu_b, dn_w, dn_e, dn_b, E, H, I, act, alpha,
+                 limit, out, threads);
 }
 
 void or_experts_host(const float *x, int T, const int32_t *idx, const float *w, int k,
-                     const uint8_t *gu_w, const uint8_t *gu_e, const uint8_t *dn_w,
-                     const uint8_t *dn_e, int E, int H, int I, float *out, int threads) {
-  experts_common(1, x, T, idx, w, k, gu_w, gu_e, dn_w, dn_e, E, H, I, out, threads);
+                     const uint8_t *gu_w, const uint8_t *gu_e, const float *gu_b,
+                     const uint8_t *dn_w, const uint8_t *dn_e, const float *dn_b, int E, int H,
+                     int I, int act, float alpha, float limit, float *out, int threads) {
+  experts_common(1, x, T, idx, w, k, gu_w, gu_e, gu_b, dn_w, dn_e, dn_b, E, H, I, act, alpha,
+                 limit, out, threads);
 }

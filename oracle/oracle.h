@@ -104,17 +104,21 @@ void or_attn_decode(const float *q, const float *k, const float *v, float *out, 
 /* score: 0 softmax, 1 sigmoid; bias may be NULL; scale 0 for none */
 void or_choose(const float *logits, const float *bias, int n, int k, int score, int norm,
                double scale, int32_t *idx, float *w);
-/* The experts of T rows, the parity form: gate_up/down dequantized, fp32 GEMV, SiLU-gated unit in
- * fp32, outputs added in ascending expert id. gu_w (E, 2I, H/32, 16), gu_e (E, 2I, H/32);
- * dn_w (E, H, I/32, 16), dn_e (E, H, I/32). x (T, H) floats; idx/w (T, k); out (T, H) added to. */
+/* The experts of T rows, the parity form: gate_up/down dequantized, fp32 GEMV, gate/up biases
+ * gu_b (E, 2I) after the product (NULL: none), the gated unit in fp32 (act 0 SiLU, 1 gpt-oss with
+ * alpha and limit), out += w * (y + dn_b) with dn_b (E, H) (NULL: none) in ascending expert id.
+ * gu_w (E, 2I, H/32, 16), gu_e (E, 2I, H/32); dn_w (E, H, I/32, 16), dn_e (E, H, I/32).
+ * x (T, H) floats; idx/w (T, k); out (T, H) added to. */
 void or_experts_f32(const float *x, int T, const int32_t *idx, const float *w, int k,
-                    const uint8_t *gu_w, const uint8_t *gu_e, const uint8_t *dn_w,
-                    const uint8_t *dn_e, int E, int H, int I, float *out, int threads);
+                    const uint8_t *gu_w, const uint8_t *gu_e, const float *gu_b,
+                    const uint8_t *dn_w, const uint8_t *dn_e, const float *dn_b, int E, int H,
+                    int I, int act, float alpha, float limit, float *out, int threads);
 /* The same with the reference's production numerics (Host.Run): x and the activations quantized
  * to int8 by blocks (Vec.Quantize), MXFP4 dot in int32 (dotGo). The timed CPU baseline. */
 void or_experts_host(const float *x, int T, const int32_t *idx, const float *w, int k,
-                     const uint8_t *gu_w, const uint8_t *gu_e, const uint8_t *dn_w,
-                     const uint8_t *dn_e, int E, int H, int I, float *out, int threads);
+                     const uint8_t *gu_w, const uint8_t *gu_e, const float *gu_b,
+                     const uint8_t *dn_w, const uint8_t *dn_e, const float *dn_b, int E, int H,
+                     int I, int act, float alpha, float limit, float *out, int threads);
 
 /* ---- model ops (internal/llm/blocks/blocks.go, internal/llm/qwen3, internal/chat/sample.go) ---- */
 /* rows of n: out = x * (1/sqrt(mean(x^2) + eps)) * w, in fp32 */

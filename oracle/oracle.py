@@ -55,10 +55,10 @@ def lib():
             "or_attn_decode": (None, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int,
                                       C.c_int]),
             "or_choose": (None, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, P, P]),
-            "or_experts_f32": (None, [P, C.c_int, P, P, C.c_int, P, P, P, P, C.c_int, C.c_int, C.c_int, P,
-                                      C.c_int]),
-            "or_experts_host": (None, [P, C.c_int, P, P, C.c_int, P, P, P, P, C.c_int, C.c_int, C.c_int, P,
-                                       C.c_int]),
+            "or_experts_f32": (None, [P, C.c_int, P, P, C.c_int, P, P, P, P, P, P, C.c_int, C.c_int, C.c_int,
+                                      C.c_int, C.c_float, C.c_float, P, C.c_int]),
+            "or_experts_host": (None, [P, C.c_int, P, P, C.c_int, P, P, P, P, P, P, C.c_int, C.c_int, C.c_int,
+                                       C.c_int, C.c_float, C.c_float, P, C.c_int]),
             "or_rmsnorm": (None, [P, P, P, C.c_int, C.c_int, C.c_float]),
             "or_rope_tables": (None, [P, P, C.c_double, C.c_int, C.c_int, C.c_int]),
             "or_apply_rope": (None, [P, C.c_int, C.c_int, P, P]),
@@ -263,18 +263,24 @@ def choose(logits, k, score="softmax", norm=True, scale=0.0, bias=None):
     return idx, w
 
 
-def experts(x, idx, w, gu_w, gu_e, dn_w, dn_e, quantized=False, threads=0) -> np.ndarray:
-    """x (T, H); idx/w (T, k); gu_w (E, 2I, H/32, 16) ... -> out (T, H) fp32."""
+def experts(x, idx, w, gu_w, gu_e, dn_w, dn_e, quantized=False, threads=0, gu_b=None, dn_b=None, act="silu",
+            alpha=1.702, limit=7.0) -> np.ndarray:
+    """x (T, H); idx/w (T, k); gu_w (E, 2I, H/32, 16) ...; optional biases gu_b (E, 2I), dn_b (E, H);
+    act 'silu' or 'gptoss' -> out (T, H) fp32."""
     x = _c(x, np.float32)
     idx, w = _c(idx, np.int32), _c(w, np.float32)
     gu_w, gu_e, dn_w, dn_e = (_c(a, np.uint8) for a in (gu_w, gu_e, dn_w, dn_e))
+    gb = None if gu_b is None else _c(gu_b, np.float32)
+    db = None if dn_b is None else _c(dn_b, np.float32)
     T, H = x.shape
     k = idx.shape[1]
     E = gu_e.shape[0]
     I = gu_e.shape[1] // 2
     out = np.zeros((T, H), np.float32)
     fn = lib().or_experts_host if quantized else lib().or_experts_f32
-    fn(_p(x), T, _p(idx), _p(w), k, _p(gu_w), _p(gu_e), _p(dn_w), _p(dn_e), E, H, I, _p(out), threads)
+    fn(_p(x), T, _p(idx), _p(w), k, _p(gu_w), _p(gu_e), None if gb is None else _p(gb), _p(dn_w), _p(dn_e),
+       None if db is None else _p(db), E, H, I, 0 if act == "silu" else 1, float(alpha), float(limit), _p(out),
+       threads)
     return out
 
 

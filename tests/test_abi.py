@@ -37,11 +37,11 @@ def test_binding_covers_header():
 
 
 def test_abi_version():
-    assert hwk.load().hwk_abi() == hwk.ABI == 2
+    assert hwk.load().hwk_abi() == hwk.ABI == 3
 
 
 def test_wrong_abi_refused(tmp_path, monkeypatch):
-    monkeypatch.setattr(hwk, "ABI", 3)
+    monkeypatch.setattr(hwk, "ABI", 4)
     monkeypatch.setattr(hwk, "_lib", None)
     with pytest.raises(hwk.HwkLibraryError):
         hwk.load()

@@ -176,6 +176,22 @@ def test_f16_gemv_parity(dev, orc, n, k):
     assert np.array_equal(y16.view(np.uint16), orc.f32_to_f16(y32))
 
 
+# K7r: the tied head over the T <= 8 rows of a speculative verify, each weight row read once
+@pytest.mark.parametrize("T,n,k", [(5, 151936, 2048), (8, 4099, 2048), (1, 77, 2056), (3, 1000, 4096), (2, 5, 8)])
+def test_f16_gemv_rows_parity(dev, orc, T, n, k):
+    print(f"f16_gemv_rows T={T} n={n} k={k}", flush=True)
+    w = synth.normal(n * k, f"k7r.{n}.{k}", std=0.02).view(n, k)
+    x = synth.normal(T * k, f"k7r.{T}.{n}.{k}.x").view(T, k)
+    want = orc.sgemm(x.cpu().numpy().astype(np.float32), w.cpu().numpy().astype(np.float32), transb=True)
+    y32 = ops.f16_gemv_rows(w, x, "f32").cpu().numpy()
+    for t in range(T):
+        check_close(y32[t], want[t])
+    y16 = ops.f16_gemv_rows(w, x, "f16").cpu().numpy()
+    assert np.array_equal(y16.view(np.uint16), orc.f32_to_f16(y32))
+    one = ops.f16_gemv(w, x[T - 1].contiguous(), "f32").cpu().numpy()
+    check_close(one, y32[T - 1], tol=1e-5)
+
+
 # ---------------- K1r: several vectors, weights read once ----------------
 
 @pytest.mark.parametrize("T,n,k", [(5, 8192, 2048), (1, 300, 6144), (2, 33, 96), (8, 2048, 2048), (3, 7, 4128),

@@ -109,3 +109,67 @@ def test_experts_small_shapes(dev, orc):
     want = orc.experts(x.cpu().numpy().astype(np.float32), idx.cpu().numpy(), w.cpu().numpy(), gw.cpu().numpy(),
                        ge.cpu().numpy(), dw.cpu().numpy(), de.cpu().numpy())
     check_close(out.cpu().numpy(), want)
+
+
+def _np(*ts):
+    return [t.cpu().numpy() for t in ts]
+
+
+@pytest.mark.parametrize("T", [1, 5, 8])
+def test_moe_layer_route_folded(dev, orc, T):
+    """hwk_moe_layer (route folded into the gate_up launch): idx bit-exact to the oracle's Choose, w
+    within one ulp, the output as hwk_moe_experts' on the same choice (and the oracle's)."""
+    print(f"moe layer T={T}", flush=True)
+    x, logits, gw, ge, dw, de = experts_case(T)
+    out, idx, w = ops.moe_layer(x, logits, 4, gw, ge, dw, de)
+    lg = logits.cpu().numpy()
+    ii, ww = idx.cpu().numpy(), w.cpu().numpy()
+    for t in range(T):
+        oi, ow = orc.choose(lg[t], 4)
+        assert np.array_equal(ii[t], oi), (t, ii[t], oi)
+        assert np.all(ulp_diff(ww[t], ow) <= 1)
+    want = orc.experts(x.cpu().numpy().astype(np.float32), ii, ww, *_np(gw, ge, dw, de))
+    check_close(out.cpu().numpy(), want)
+    same = ops.moe_experts(x, idx, w, gw, ge, dw, de)
+    check_close(out.cpu().numpy(), same.cpu().numpy(), tol=1e-6)
+
+
+@pytest.mark.parametrize("T,exp_hi", [(1, False), (5, False), (3, True)])
+def test_experts_gptoss_biases(dev, orc, T, exp_hi):
+    """The gpt-oss gated unit (alpha 1.702, limit 7) with gate/up and down biases (host.go:44-57,
+    505-527, 566-578), as gpt-oss's checkpoints run it; exp_hi: gate/up scales past the limit, so
+    that the clamps are taken."""
+    E, H, I = 32, 2048, 768
+    x, logits, gw, ge, dw, de = experts_case(T, E, H, I, name="c4g")
+    if exp_hi:
+        ge = (ge % 4 + 126).to(torch.uint8)
+    gb = synth.normal(E * 2 * I, "c4g.gu_bias", std=0.1, dtype=torch.float32).view(E, 2 * I)
+    db = synth.normal(E * H, "c4g.dn_bias", std=0.1, dtype=torch.float32).view(E, H)
+    kw = dict(gu_b=gb, dn_b=db, act="gptoss", alpha=1.702, limit=7.0)
+    out, idx, w = ops.moe_layer(x, logits, 4, gw, ge, dw, de, **kw)
+    want = orc.experts(x.cpu().numpy().astype(np.float32), *_np(idx, w, gw, ge, dw, de), gu_b=gb.cpu().numpy(),
+                       dn_b=db.cpu().numpy(), act="gptoss", alpha=1.702, limit=7.0)
+    check_close(out.cpu().numpy(), want)
+    # SiLU with the biases through hwk_moe_experts, add mode
+    base = synth.normal(T * H, "c4g.base", std=10.0, dtype=torch.float32).view(T, H)
+    b0 = base.cpu().numpy()
+    ops.moe_experts(x, idx, w, gw, ge, dw, de, out=base, out_mode="add", gu_b=gb, dn_b=db)
+    want2 = orc.experts(x.cpu().numpy().astype(np.float32), *_np(idx, w, gw, ge, dw, de), gu_b=gb.cpu().numpy(),
+                        dn_b=db.cpu().numpy())
+    check_close(base.cpu().numpy(), want2 + b0)
+
+
+def test_moe_layer_small_shapes_sigmoid(dev, orc):
+    """E=6, k=2, H=256, I=96, sigmoid routing with a router bias and a weight scale."""
+    T, E, H, I = 3, 6, 256, 96
+    x, logits, gw, ge, dw, de = experts_case(T, E, H, I, name="c4t")
+    rb = torch.tensor([0, 0.5, 0, 0, 1.0, 0], dtype=torch.float32, device="cuda")
+    out, idx, w = ops.moe_layer(x, logits, 2, gw, ge, dw, de, score="sigmoid", norm=True, scale=2.5,
+                                router_bias=rb)
+    lg = logits.cpu().numpy()
+    for t in range(T):
+        oi, ow = orc.choose(lg[t], 2, score="sigmoid", norm=True, scale=2.5, bias=rb.cpu().numpy())
+        assert np.array_equal(idx.cpu().numpy()[t], oi)
+        assert np.all(ulp_diff(w.cpu().numpy()[t], ow) <= 1)
+    want = orc.experts(x.cpu().numpy().astype(np.float32), *_np(idx, w, gw, ge, dw, de))
+    check_close(out.cpu().numpy(), want)

@@ -385,6 +385,94 @@ def test_experts_f32_vs_f64_and_host(orc):
         assert abs(np.linalg.norm(host[t]) / np.linalg.norm(want[t]) - 1) <= 0.02
 
 
+def experts_gptoss_f64(orc, x, idx, w, gu_w, gu_e, gu_b, dn_w, dn_e, dn_b, alpha=1.702, limit=7.0, clamp=True,
+                       plus_one=True, bias=True):
+    """TestHostRunSmall's float64 reference (internal/llm/experts/host_test.go:208-284): gate/up in
+    float64 plus their bias, g = min(g, 7), u = clamp(u, -7, 7), act = float32(g/(1+e^(-1.702 g))*(u+1)),
+    out += w * (down(act) + down bias). The switches drop a step, for the mutation checks."""
+    T, H = x.shape
+    E, I2 = gu_e.shape[:2]
+    I = I2 // 2
+    out = np.zeros((T, H))
+    for t in range(T):
+        for j in range(idx.shape[1]):
+            e = idx[t, j]
+            gu = orc.mxfp4_dequantize(gu_w[e].reshape(I2, -1), gu_e[e]).astype(np.float64) @ x[t].astype(np.float64)
+            if bias:
+                gu += gu_b[e]
+            g, u = gu[0::2], gu[1::2]
+            if clamp:
+                g, u = np.minimum(g, limit), np.clip(u, -limit, limit)
+            a = (g / (1 + np.exp(-alpha * g)) * ((u + 1) if plus_one else u)).astype(np.float32).astype(np.float64)
+            y = orc.mxfp4_dequantize(dn_w[e].reshape(H, -1), dn_e[e]).astype(np.float64) @ a
+            out[t] += w[t, j] * (y + (dn_b[e] if bias else 0))
+    return out
+
+
+@pytest.mark.parametrize("exp_lo", [118, 126])
+def test_experts_gptoss_unit_and_biases(orc, exp_lo):
+    """The gpt-oss gated unit and the expert biases against TestHostRunSmall's float64 form: the fp32
+    path within 1e-4 * RMS, the int8-activation path at cosine >= 0.999 and norms within 2 %, as that
+    test asks at its scales (exponents 118..123). Exponents from 126 put many gate/up sums past the limit (the clamp taken). Each
+    mutation (no clamp, no +1, no biases) of the float64 form moves it away from the oracle."""
+    rng = np.random.default_rng(21)
+    E, K, H, I = 4, 2, 128, 64
+    gu_w = rng.integers(0, 256, (E, 2 * I, H // 32, 16), dtype=np.uint8)
+    dn_w = rng.integers(0, 256, (E, H, I // 32, 16), dtype=np.uint8)
+    gu_e = rng.integers(exp_lo, exp_lo + 6, (E, 2 * I, H // 32), dtype=np.uint8)
+    dn_e = rng.integers(118, 124, (E, H, I // 32), dtype=np.uint8)
+    gu_b = (rng.standard_normal((E, 2 * I)) * 0.1).astype(np.float32)
+    dn_b = (rng.standard_normal((E, H)) * 0.1).astype(np.float32)
+    for n in (1, 3):
+        x = rng.standard_normal((n, H)).astype(np.float32)
+        idx = np.stack([rng.permutation(E)[:K] for _ in range(n)]).astype(np.int32)
+        w = np.tile(np.array([0.7, 0.3], np.float32), (n, 1))
+        kw = dict(gu_b=gu_b, dn_b=dn_b, act="gptoss", alpha=1.702, limit=7.0)
+        want = experts_gptoss_f64(orc, x, idx, w, gu_w, gu_e, gu_b, dn_w, dn_e, dn_b)
+        got = orc.experts(x, idx, w, gu_w, gu_e, dn_w, dn_e, **kw)
+        rms = np.sqrt(np.mean(want ** 2))
+        assert np.max(np.abs(got - want)) <= 1e-4 * rms
+        if exp_lo == 118:  # the reference test's scales (the int8 activations lose more past them)
+            host = orc.experts(x, idx, w, gu_w, gu_e, dn_w, dn_e, quantized=True, **kw)
+            for t in range(n):
+                cos = host[t] @ want[t] / np.linalg.norm(host[t]) / np.linalg.norm(want[t])
+                assert cos >= 0.999 and abs(np.linalg.norm(host[t]) / np.linalg.norm(want[t]) - 1) <= 0.02
+        muts = [dict(plus_one=False), dict(bias=False)] + ([dict(clamp=False)] if exp_lo >= 126 else [])
+        for mut in muts:
+            bad = experts_gptoss_f64(orc, x, idx, w, gu_w, gu_e, gu_b, dn_w, dn_e, dn_b, **mut)
+            assert np.max(np.abs(got - bad)) > 1e-2 * rms, mut
+    # the clamp is taken at the large exponents
+    if exp_lo >= 126:
+        gu = orc.mxfp4_dequantize(gu_w[0].reshape(2 * I, -1), gu_e[0]).astype(np.float64) @ x[0].astype(np.float64)
+        assert np.any(np.abs(gu) > 7)
+
+
+def test_experts_silu_with_biases(orc):
+    """The SiLU unit with biases: the fp32 path against a float64 brute force of silu(g+bg)*(u+bu)
+    and w * (y + bd)."""
+    rng = np.random.default_rng(22)
+    E, H, I = 5, 96, 64
+    gu_w = rng.integers(0, 256, (E, 2 * I, H // 32, 16), dtype=np.uint8)
+    gu_e = rng.integers(122, 126, (E, 2 * I, H // 32), dtype=np.uint8)
+    dn_w = rng.integers(0, 256, (E, H, I // 32, 16), dtype=np.uint8)
+    dn_e = rng.integers(118, 122, (E, H, I // 32), dtype=np.uint8)
+    gu_b = rng.standard_normal((E, 2 * I)).astype(np.float32)
+    dn_b = rng.standard_normal((E, H)).astype(np.float32)
+    x = rng.standard_normal((2, H)).astype(np.float32)
+    idx = np.array([[3, 0, 4], [1, 3, 2]], np.int32)
+    w = rng.uniform(0.1, 0.5, (2, 3)).astype(np.float32)
+    got = orc.experts(x, idx, w, gu_w, gu_e, dn_w, dn_e, gu_b=gu_b, dn_b=dn_b)
+    want = np.zeros((2, H))
+    for t in range(2):
+        for j in range(3):
+            e = idx[t, j]
+            gu = orc.mxfp4_dequantize(gu_w[e].reshape(2 * I, -1), gu_e[e]).astype(np.float64) @ x[t] + gu_b[e]
+            g, u = gu[0::2], gu[1::2]
+            y = orc.mxfp4_dequantize(dn_w[e].reshape(H, -1), dn_e[e]).astype(np.float64) @ (g / (1 + np.exp(-g)) * u)
+            want[t] += w[t, j] * (y + dn_b[e])
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.sqrt(np.mean(want ** 2))
+
+
 # ---------------- decoder ops ----------------
 
 def test_rmsnorm_closed_form(orc):
