@@ -29,6 +29,39 @@ __global__ void k_normal(void *__restrict__ out, uint64_t n, uint64_t key, float
 
 uint32_t grid_of(uint64_t n) { return (uint32_t)((n + 255) / 256); }
 
+// The reference's synthetic tensors (internal/llm/synth.go:17-35): seed = FNV-64a(name), then per
+// element seed = seed * A + C (Knuth's MMIX LCG) and v = float32(int64(seed >> 40) - 2^23) / 2^23 *
+// float32(0.2), uniform in [-0.2, 0.2) (the comment there says +-0.1; the code is followed). A thread
+// takes kRefRun consecutive elements: it jumps the
+// generator to its first element by composing the affine step with itself (binary powers), then
+// steps sequentially.
+constexpr uint64_t kLcgA = 6364136223846793005ull, kLcgC = 1442695040888963407ull;
+constexpr uint32_t kRefRun = 64;
+
+__global__ void k_synth_ref(void *__restrict__ out, uint64_t n, uint64_t seed, int f16out) {
+#pragma clang fp contract(off)
+  const uint64_t i0 = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * kRefRun;
+  if (i0 >= n) return;
+  // (a, c) = the step applied i0 times: x -> a x + c
+  uint64_t a = 1, c = 0, pa = kLcgA, pc = kLcgC;
+  for (uint64_t k = i0; k; k >>= 1) {
+    if (k & 1) {
+      c = pa * c + pc;
+      a = pa * a;
+    }
+    pc = pa * pc + pc;
+    pa = pa * pa;
+  }
+  uint64_t s = a * seed + c;
+  const uint64_t end = i0 + kRefRun < n ? i0 + kRefRun : n;
+  for (uint64_t i = i0; i < end; i++) {
+    s = s * kLcgA + kLcgC;
+    const float v = (float)((int64_t)(s >> 40) - (1 << 23)) / 8388608.0f * 0.2f;
+    if (f16out) ((f16 *)out)[i] = (f16)f32_value(v);
+    else ((float *)out)[i] = v;
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -63,6 +96,21 @@ HWK_API char *hwk_synth_normal(void *stream, void *out, uint64_t n, uint64_t key
   hipLaunchKernelGGL(k_normal, dim3(grid_of(n)), dim3(256), 0, (hipStream_t)stream, out, n, key,
                      hwk::f32_of_bits(std_bits), out_f16);
   return hwk::launched("hwk_synth_normal");
+}
+
+HWK_API char *hwk_synth_reference(void *stream, void *out, uint64_t n, const char *name, int out_f16) {
+  HWK_CHECK(out && name, "hwk_synth_reference: null pointer");
+  HWK_CHECK(hwk::aligned(out, out_f16 ? 2 : 4), "hwk_synth_reference: out misaligned");
+  HWK_CHECK(n < (1ull << 38), "hwk_synth_reference: n too large");
+  if (n == 0) return nullptr;
+  uint64_t h = 0xCBF29CE484222325ull;  // FNV-64a (Go hash/fnv New64a)
+  for (const unsigned char *q = (const unsigned char *)name; *q; q++) {
+    h ^= *q;
+    h *= 0x100000001B3ull;
+  }
+  const uint64_t threads = (n + kRefRun - 1) / kRefRun;
+  hipLaunchKernelGGL(k_synth_ref, dim3(grid_of(threads)), dim3(256), 0, (hipStream_t)stream, out, n, h, out_f16);
+  return hwk::launched("hwk_synth_reference");
 }
 
 }  // extern "C"

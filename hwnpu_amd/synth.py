@@ -76,3 +76,12 @@ def uniform_real(n: int, lo: float, hi: float, name: str, seed: int = 0, dtype=t
     rounded to dtype (RNE): the per-channel scales of the int8 configuration."""
     u = uniform_int(n, 0, 1 << 24, name, seed, torch.int32, device).to(torch.float64)
     return (lo + (hi - lo) * u / float(1 << 24)).to(torch.float32).to(dtype)
+
+
+def reference(name: str, n: int, dtype=torch.float32) -> torch.Tensor:
+    """The reference's synthetic values of tensor `name` (llm.Synthetic.Get, internal/llm/synth.go:17-35):
+    n values uniform in [-0.2, 0.2) (the code's range; its comment says +-0.1) from FNV-64a(name) and
+    the MMIX LCG, fp32 or fp16, made on the GPU."""
+    out = torch.empty(n, dtype=dtype, device="cuda")
+    hwk.load().hwk_synth_reference(_stream(), out.data_ptr(), n, name.encode(), 1 if dtype == torch.float16 else 0)
+    return out

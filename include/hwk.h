@@ -469,6 +469,11 @@ HWK_API char *hwk_synth_normal(void *stream, void *out, uint64_t n, uint64_t key
  * internal/mxfp4/encode.go:11-78), never materialized in fp32. */
 HWK_API char *hwk_synth_mxfp4(void *stream, void *w, void *e, uint32_t rows, uint32_t k,
                               uint64_t key, uint32_t std_bits);
+/* The reference's own synthetic checkpoint values (llm.Synthetic.Get, internal/llm/synth.go:17-35):
+ * n values of the tensor called name (a NUL-terminated string), seeded by FNV-64a(name) and
+ * stepped by the MMIX LCG, uniform in [-0.2, 0.2) (the code's range; its comment says +-0.1),
+ * as fp32 or fp16 (RNE of the fp32 value). */
+HWK_API char *hwk_synth_reference(void *stream, void *out, uint64_t n, const char *name, int out_f16);
 /* Encode an fp32 matrix (rows, k) to MXFP4 (reference internal/mxfp4/encode.go:11-78). */
 HWK_API char *hwk_mxfp4_encode(void *stream, const void *x, void *w, void *e, uint32_t rows,
                                uint32_t k);

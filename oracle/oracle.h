@@ -151,6 +151,11 @@ void or_qwen3_checksums(const or_qwen3 *m, uint64_t out[3]);
  * cached): logits (vocab) of the last row, returns the greedy token */
 int32_t or_qwen3_run(or_qwen3 *m, const int32_t *tokens, int T, int start, float *logits);
 
+/* ---- the reference's synthetic checkpoint (internal/llm/synth.go:17-35) ---- */
+/* n values of tensor name: FNV-64a seed, MMIX LCG, uniform in [-0.2, 0.2) (synth.go's comment
+ * says +-0.1; its code gives +-0.2) */
+void or_synth_reference(const char *name, size_t n, float *out);
+
 /* ---- threads ---- */
 int or_max_threads(void);
 

@@ -63,6 +63,8 @@ def lib():
             "or_rope_tables": (None, [P, P, C.c_double, C.c_int, C.c_int, C.c_int]),
             "or_apply_rope": (None, [P, C.c_int, C.c_int, P, P]),
             "or_silu_mul": (None, [P, P, P, sz]),
+            "or_fnv64a": (C.c_uint64, [C.c_char_p]),
+            "or_synth_reference": (None, [C.c_char_p, sz, P]),
             "or_argmax": (C.c_int32, [P, sz]),
             "or_max_threads": (C.c_int, []),
             "or_normal_at": (C.c_double, [C.c_uint64, C.c_uint64]),
@@ -361,3 +363,14 @@ def normal_at(key: int, i: int) -> float:
 
 def fnv64a(name: str) -> int:
     return lib().or_fnv64a(name.encode())
+
+
+# ---- the reference's synthetic checkpoint (internal/llm/synth.go:17-35) ----
+def fnv64a(name: str) -> int:
+    return int(lib().or_fnv64a(name.encode()))
+
+
+def synth_reference(name: str, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().or_synth_reference(name.encode(), n, _p(out))
+    return out

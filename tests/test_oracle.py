@@ -511,3 +511,34 @@ def test_silu_and_argmax(orc):
     assert np.allclose(orc.silu_mul(g, u), want, rtol=1e-6)
     x = np.array([0, 3, 1, 3, 2], np.float32)
     assert orc.argmax(x) == 1  # ties to the lowest index (internal/chat/sample.go:80-87)
+
+
+# ---------------- the reference's synthetic checkpoint (internal/llm/synth.go:17-35) ----------------
+
+def test_fnv64a_published_vectors(orc):
+    """FNV-1a 64-bit test vectors from the algorithm's authors (the seed of Synthetic.Get)."""
+    assert orc.fnv64a("") == 0xCBF29CE484222325
+    assert orc.fnv64a("a") == 0xAF63DC4C8601EC8C
+    assert orc.fnv64a("foobar") == 0x85944171F73967E8
+
+
+def test_synth_reference_sequence_and_distribution(orc):
+    """The first values against the recurrence evaluated with Python integers mod 2^64 (another
+    implementation of Knuth's MMIX LCG), and the distribution of 2^20 values: inside [-0.2, 0.2),
+    mean near 0, 64 equal bins within a chi-square bound."""
+    name = "model.layers.3.mlp.down_proj.weight"
+    got = orc.synth_reference(name, 1 << 20)
+    seed = orc.fnv64a(name)
+    for i in range(64):
+        seed = (seed * 6364136223846793005 + 1442695040888963407) % (1 << 64)
+        want = np.float32(np.float32((seed >> 40) - (1 << 23)) / np.float32(1 << 23)) * np.float32(0.2)
+        assert got[i] == want, i
+    assert got.min() >= -0.2 and got.max() < 0.2
+    assert abs(float(got.astype(np.float64).mean())) < 5 * 0.2 / np.sqrt(3) / np.sqrt(got.size)
+    hist, _ = np.histogram(got, bins=64, range=(-0.2, 0.2))
+    e = got.size / 64
+    chi2 = float(((hist - e) ** 2 / e).sum())
+    assert chi2 < 120, chi2  # 63 degrees of freedom: p < 1e-5 past 120
+    # names give independent streams
+    other = orc.synth_reference(name + "x", 1024)
+    assert not np.array_equal(other, got[:1024])
