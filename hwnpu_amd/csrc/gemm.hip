@@ -1,15 +1,28 @@
 // Prefill / verify GEMM (K3) on gfx950: Y (M, N) = X (M, K) W^T, X fp16, W int8 per output channel
-// or MXFP4, fp32 accumulation on the fp16 MFMA.
+// or MXFP4, fp32 accumulation on the fp16 MFMA (v_mfma_f32_16x16x32_f16).
 //
-// A workgroup computes a 128 x 128 tile of Y with eight waves (2 x 4, 64 x 32 each, 8 MFMA
-// 16x16x32 tiles a wave; two waves a SIMD). K goes 64 at a time, double-buffered in LDS: while the
-// waves multiply
-// one buffer, the next step's X rows and weight rows are already loading into registers; the
-// weights are dequantized to fp16 on their way into LDS (int8 exactly, with the channel scale
-// applied in the epilogue; MXFP4 with the hardware fp4 -> fp16 conversion, its 32-value block
-// scale folded in, exact for e8m0 exponents within [-23, 13] where every code times the scale is
-// an fp16 value). Tile order is XCD-aware: the workgroups that share a weight panel run on the
-// same XCD, so its L2 holds the panel once.
+// A workgroup of 4 waves (one a SIMD, 2 x 2) computes a BM x BN tile of Y; a wave holds a
+// (BM/2) x (BN/2) block of 16 x 16 accumulator tiles. K goes 128 at a time:
+//   X: the tile's 128-column slab goes through LDS (two buffers, one barrier a step), 16-byte chunks
+//      placed at chunk ^ (row & 15) so that the 16 rows one MFMA operand load touches fall in 16
+//      different bank groups (a row is 256 bytes, the width of the 64 banks);
+//   W: each wave loads its own columns' codes straight into registers (16 or 32 bytes a lane per 16
+//      columns a step) and converts them there: int8 exactly to fp16 (the channel scale applied to
+//      the fp32 result), MXFP4 by the hardware fp4 conversion with the block scale folded in.
+// Loads run two steps ahead of the multiply (register stages), so a step's global latency hides
+// behind the two steps before it. A lane's 32 values of K a step are the same set in its X and W
+// operands, so each MFMA sums 32 true products (which lane holds which k is a free choice of the
+// kernel, made for contiguous loads).
+//
+// MXFP4 exactness: a code times its block scale is an fp16 value when the scale's exponent is in
+// [-23, 13]. A row (output channel) whose finite block exponents leave that range is shifted by a
+// power of two s0 chosen per row (the largest exponent mapped to 13) and its fp32 result scaled back
+// by 2^s0, which is exact; rows whose exponents span more than 36 lose the low bits of their
+// smallest blocks (values below 2^-24 of the shifted scale). Scale e = 0 is 0 and e = 255 is +Inf,
+// as in the reference's Dequantize (internal/mxfp4/mxfp4.go:77).
+//
+// Tile order is XCD-aware: the workgroups that share a weight panel run on the same XCD, so its L2
+// holds the panel once; the host picks the tile shape that fills the 256 CUs best.
 #include "hwk_common.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -17,7 +30,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64, LDSK = BK + 8;  // row stride padded against bank conflicts
+constexpr int KS = 128;     // K a step
+constexpr int CH = KS / 8;  // 16-byte chunks of an X row a step
+constexpr int KK = KS / 32;  // MFMAs a step for one (16-row, 16-column) tile
+constexpr int NS = 2;       // register stages: loads run NS steps ahead
+constexpr int NT = 256;     // threads a workgroup (2 x 2 waves)
 
 // 4 int8 codes (one dword) as 4 exact fp16 values (two dwords).
 __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t w) {
@@ -28,73 +45,150 @@ __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t w) {
   return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
 }
 
-template <int SEL>
-__device__ __forceinline__ uint32_t fp4x2_scaled(uint32_t w, float s) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, SEL));
+// 8 int8 codes (two dwords) as a half8 operand.
+__device__ __forceinline__ half8 i8x8_to_half8(uint32_t a, uint32_t b) {
+  const uint2 p = i8x4_to_f16x4(a), q = i8x4_to_f16x4(b);
+  const u32x4 v = {p.x, p.y, q.x, q.y};
+  return __builtin_bit_cast(half8, v);
 }
 
-constexpr int NT = 512;  // threads a workgroup: 8 waves, 2 a SIMD
+// 8 e2m1 codes (one dword, even element in the low nibble) times scale s as a half8 operand.
+__device__ __forceinline__ half8 fp4x8_to_half8(uint32_t w, float s) {
+  const u32x4 v = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 1)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 2)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 3))};
+  return __builtin_bit_cast(half8, v);
+}
 
-// The step's global loads (BK = 64 values of K), held in registers until they go to LDS.
+__device__ __forceinline__ u32x4 load16(const void *p) { return *(const u32x4 *)p; }
+
+// The X chunk (of CH a row a step) that MFMA kk of lane group q reads: the k offsets of a lane's
+// operands in the step. int8: two 16-byte weight loads a lane at q*16 and 64 + q*16 (each 16 rows x 64
+// contiguous bytes a load instruction); MXFP4: one 32-value block a lane at q*32.
 template <bool MX>
-struct Stage {
-  uint4 a[2];  // X: chunks t and t+512 of the 128 x 64 tile (row c/8, 8 halves at (c%8)*8)
-  uint4 b;     // W int8: row t/4, 16 codes at (t%4)*16; MXFP4 (t < 256): row t/2, block t%2
-  uint32_t e;  // MXFP4 scale byte of that block
+__device__ __forceinline__ int xchunk(int q, int kk) {
+  if constexpr (MX) return 4 * q + kk;
+  return kk < 2 ? 2 * q + kk : 8 + 2 * q + (kk - 2);
+}
+
+template <int BM, int BN, bool MX>
+struct Cfg {
+  static constexpr int TM = BM / 2 / 16, TN = BN / 2 / 16;  // 16 x 16 tiles a wave
+  static constexpr int AL = BM * CH / NT;                   // X chunks a thread stages a step
+  static constexpr int BL = MX ? 1 : 2;                     // 16-byte weight loads a lane a step a tile
+  static_assert(BM * CH % NT == 0, "X chunks a thread");
 };
 
-template <bool MX>
-__device__ __forceinline__ void load_stage(Stage<MX> &s, const uint4 *__restrict__ X, const uint8_t *__restrict__ W,
-                                           const uint8_t *__restrict__ E, uint32_t M, uint32_t N, uint32_t K,
-                                           uint32_t m0, uint32_t n0, uint32_t k0, int t) {
+template <int BM, int BN, bool MX>
+struct Stage {
+  u32x4 a[Cfg<BM, BN, MX>::AL];
+  u32x4 b[Cfg<BM, BN, MX>::TN][Cfg<BM, BN, MX>::BL];
+  uint32_t e[Cfg<BM, BN, MX>::TN];  // MXFP4 block scale bytes
+  uint32_t k0;                      // the step's K offset
+};
+
+// Issue the global loads of the step at K offset k0 into s: X (load_x) and the weights (load_w).
+// Out-of-range rows and columns read the last row/column (their results are not stored); K past the
+// end reads in-range data, which zero_tail clears when the stage is consumed (a select here would wait
+// for the load at once). Every load is issued unconditionally (a load under a branch would be waited
+// for at the join).
+template <int BM, int BN, bool MX>
+__device__ __forceinline__ void load_x(Stage<BM, BN, MX> &s, const u32x4 *__restrict__ X, uint32_t M, uint32_t K,
+                                       uint32_t m0, uint32_t k0, int t) {
+  using C = Cfg<BM, BN, MX>;
+  s.k0 = k0;
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int c = t + NT * i, row = c >> 3, q = c & 7;
-    s.a[i] = (m0 + row < M && k0 + q * 8 < K) ? X[((size_t)(m0 + row) * K + k0) / 8 + q] : make_uint4(0, 0, 0, 0);
-  }
-  if constexpr (MX) {
-    const uint32_t row = n0 + (t >> 1);
-    const bool kin = k0 + (t & 1) * 32 < K;  // a K that is an odd multiple of 32 ends on a half step
-    if (t < 256 && row < N && kin) {
-      const uint32_t blk = k0 / 32 + (t & 1);
-      s.b = load_stream((const uint4 *)(W + ((size_t)row * (K / 32) + blk) * 16));
-      s.e = E[(size_t)row * (K / 32) + blk];
-    } else {
-      s.b = make_uint4(0, 0, 0, 0);
-      s.e = 0;
-    }
-  } else {
-    const uint32_t row = n0 + (t >> 2), col = k0 + (t & 3) * 16;
-    s.b = (row < N && col < K) ? load_stream((const uint4 *)(W + (size_t)row * K + col)) : make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < C::AL; i++) {
+    const int c = t + NT * i, row = c / CH, ch = c % CH;
+    const uint32_t m = min(m0 + row, M - 1);
+    s.a[i] = X[((size_t)m * K + min(k0 + ch * 8, K - 8)) / 8];
   }
 }
 
-template <bool MX>
-__device__ __forceinline__ void store_stage(const Stage<MX> &s, f16 (*As)[LDSK], f16 (*Bs)[LDSK], int t) {
-#pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int c = t + NT * i, row = c >> 3, q = c & 7;
-    *(uint4 *)&As[row][q * 8] = s.a[i];
-  }
+template <int BM, int BN, bool MX>
+__device__ __forceinline__ void load_w(Stage<BM, BN, MX> &s, const uint8_t *__restrict__ W,
+                                       const uint8_t *__restrict__ E, uint32_t K, uint32_t k0,
+                                       const uint32_t (&brow)[Cfg<BM, BN, MX>::TN], int q) {
+  using C = Cfg<BM, BN, MX>;
   if constexpr (MX) {
-    if (t < 256) {
-      const int row = t >> 1, col = (t & 1) * 32;
-      const float sc = e8m0_scale(s.e);
-      const uint32_t cw[4] = {s.b.x, s.b.y, s.b.z, s.b.w};
+    const uint32_t blk = min(k0 + q * 32, K - 32) / 32;
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        uint4 v = make_uint4(fp4x2_scaled<0>(cw[q], sc), fp4x2_scaled<1>(cw[q], sc), fp4x2_scaled<2>(cw[q], sc),
-                             fp4x2_scaled<3>(cw[q], sc));
-        *(uint4 *)&Bs[row][col + q * 8] = v;
-      }
+    for (int j = 0; j < C::TN; j++) {
+      const size_t bi = (size_t)brow[j] * (K / 32) + blk;
+      s.b[j][0] = load16(W + bi * 16);
+      s.e[j] = E[bi];
     }
   } else {
-    const int row = t >> 2, col = (t & 3) * 16;
-    const uint2 v0 = i8x4_to_f16x4(s.b.x), v1 = i8x4_to_f16x4(s.b.y);
-    const uint2 v2 = i8x4_to_f16x4(s.b.z), v3 = i8x4_to_f16x4(s.b.w);
-    *(uint4 *)&Bs[row][col] = make_uint4(v0.x, v0.y, v1.x, v1.y);
-    *(uint4 *)&Bs[row][col + 8] = make_uint4(v2.x, v2.y, v3.x, v3.y);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const uint32_t kc = min(k0 + h * 64 + q * 16, K - 16);
+#pragma unroll
+      for (int j = 0; j < C::TN; j++) s.b[j][h] = load16(W + (size_t)brow[j] * K + kc);
+    }
   }
+}
+
+// A step reaching past K: its X chunks and weight loads past K become zeros (MXFP4: scale 0).
+template <int BM, int BN, bool MX>
+__device__ __forceinline__ void zero_tail(Stage<BM, BN, MX> &s, uint32_t K, int t, int q) {
+  using C = Cfg<BM, BN, MX>;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < C::AL; i++)
+    if (s.k0 + ((t + NT * i) % CH) * 8 >= K) s.a[i] = zero;
+#pragma unroll
+  for (int j = 0; j < C::TN; j++) {
+    if constexpr (MX) {
+      if (s.k0 + q * 32 >= K) {
+        s.b[j][0] = zero;
+        s.e[j] = 0u;
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+        if (s.k0 + h * 64 + q * 16 >= K) s.b[j][h] = zero;
+    }
+  }
+}
+
+// The block scale of exponent byte e in a row shifted by 2^-s0 (see the header): 0 for e = 0 or a
+// shifted exponent below the float range, +Inf for e = 255.
+__device__ __forceinline__ float shifted_scale(uint32_t e, int s0) {
+  const float v = __uint_as_float((uint32_t)max((int)e - s0, 0) << 23);  // below the float range: +0
+  return e == 255u ? __builtin_inff() : e == 0u ? 0.0f : v;
+}
+
+// The row shift s0 of weight row n: 0 when every finite, nonzero block exponent of the row is in
+// [-23, 13]; else the largest mapped to 13. Lanes q = 0..3 of a row scan a quarter of its scale bytes
+// each (dwords when the rows are dword-aligned) and combine by lane swaps.
+__device__ __forceinline__ int row_shift(const uint8_t *__restrict__ E, uint32_t n, uint32_t K, bool words, int q) {
+  const uint32_t nb = K / 32;
+  uint32_t hi = 0, lo = 255;
+  auto take = [&](uint32_t e) {
+    if (e != 0u && e != 255u) {
+      hi = max(hi, e);
+      lo = min(lo, e);
+    }
+  };
+  if (words) {
+    const uint32_t *row = (const uint32_t *)(E + (size_t)n * nb);
+    for (uint32_t w = q; w < nb / 4; w += 4) {
+      const uint32_t v = row[w];
+#pragma unroll
+      for (int b = 0; b < 4; b++) take((v >> (8 * b)) & 255u);
+    }
+  } else {
+    for (uint32_t b = q; b < nb; b += 4) take(E[(size_t)n * nb + b]);
+  }
+#pragma unroll
+  for (int off = 16; off < 64; off <<= 1) {
+    hi = max(hi, (uint32_t)__shfl_xor((int)hi, off, 64));
+    lo = min(lo, (uint32_t)__shfl_xor((int)lo, off, 64));
+  }
+  if (hi == 0u) return 0;  // no finite nonzero scale
+  const int emax = (int)hi - 127, emin = (int)lo - 127;
+  return (emax <= 13 && emin >= -23) ? 0 : emax - 13;
 }
 
 // Workgroup id -> tile: consecutive ids go round the XCDs, so ids x, x+8, x+16, ... share an XCD;
@@ -111,71 +205,157 @@ __device__ __forceinline__ void tile_of(uint32_t id, uint32_t mt, uint32_t nt, u
   tm = lin % mt;
 }
 
-template <bool MX>
-__global__ __launch_bounds__(NT) void k_gemm(const uint4 *__restrict__ X, const uint8_t *__restrict__ W,
+template <int BM, int BN, bool MX>
+__global__ __launch_bounds__(NT) void k_gemm(const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
                                              const uint8_t *__restrict__ E, const uint16_t *__restrict__ S,
-                                             void *__restrict__ Y, uint32_t M, uint32_t N, uint32_t K, int mode) {
-  __shared__ __attribute__((aligned(16))) f16 As[2][BM][LDSK];
-  __shared__ __attribute__((aligned(16))) f16 Bs[2][BN][LDSK];
+                                             void *__restrict__ Y, uint32_t M, uint32_t N, uint32_t K, int mode,
+                                             bool ewords) {
+  using C = Cfg<BM, BN, MX>;
+  constexpr int TM = C::TM, TN = C::TN;
+  __shared__ __attribute__((aligned(16))) u32x4 As[2][BM * CH];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves of 64 x 32
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r16 = lane & 15, q = lane >> 4;
   uint32_t tm, tn;
   tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const uint32_t nw = n0 + wn * (BN / 2);  // the wave's first column
+  uint32_t brow[TN];
+#pragma unroll
+  for (int j = 0; j < TN; j++) brow[j] = min(nw + j * 16 + r16, N - 1);
 
-  floatx4 acc[4][2];
+  const uint32_t steps = (K + KS - 1) / KS;
+  auto kofs = [&](uint32_t j) -> uint32_t { return min(j, steps) * KS; };  // past the end: reads zeros
+  Stage<BM, BN, MX> st[NS];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
-
-  // K steps: LDS holds step it (being multiplied) and step it+1 (written at the end of step it from
-  // registers whose global loads were issued a step earlier).
-  const uint32_t steps = (K + BK - 1) / BK;
-  Stage<MX> st;
-  load_stage<MX>(st, X, W, E, M, N, K, m0, n0, 0, t);
-  store_stage<MX>(st, As[0], Bs[0], t);
-  if (steps > 1) load_stage<MX>(st, X, W, E, M, N, K, m0, n0, BK, t);
-  __syncthreads();
-  const int r16 = lane & 15, kq = (lane >> 4) * 8;
-  for (uint32_t it = 0; it < steps; it++) {
-    const int buf = it & 1;
-    // both 32-wide substeps' fragments first, then the 16 MFMAs
-    half8 a[2][4], b[2][2];
-#pragma unroll
-    for (int kk = 0; kk < 2; kk++) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) a[kk][i] = *(const half8 *)&As[buf][wm * 64 + i * 16 + r16][kk * 32 + kq];
-#pragma unroll
-      for (int j = 0; j < 2; j++) b[kk][j] = *(const half8 *)&Bs[buf][wn * 32 + j * 16 + r16][kk * 32 + kq];
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; kk++)
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[kk][i], b[kk][j], acc[i][j], 0, 0, 0);
-    if (it + 1 < steps) {
-      store_stage<MX>(st, As[buf ^ 1], Bs[buf ^ 1], t);
-      if (it + 2 < steps) load_stage<MX>(st, X, W, E, M, N, K, m0, n0, (it + 2) * BK, t);
-    }
-    __syncthreads();
+  for (int s = 0; s < NS; s++) {
+    load_x<BM, BN, MX>(st[s], X, M, K, m0, kofs(s), t);
+    load_w<BM, BN, MX>(st[s], W, E, K, kofs(s), brow, q);
   }
-  // D of tile (i, j): lane holds rows (lane/16)*4 + r, column lane%16
+  int s0[TN];
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const uint32_t n = n0 + wn * 32 + j * 16 + r16;
+  for (int j = 0; j < TN; j++) s0[j] = MX ? row_shift(E, brow[j], K, ewords, q) : 0;
+
+  floatx4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Steps in groups of NS (a partial last group multiplies zeros: its loads read past K). A step:
+  // its X slab into LDS, barrier, the next X loads of its stage, then for each kk its weight operands
+  // converted next to the MFMAs that take them (the VALU work overlaps the matrix core), then the
+  // next weight loads of its stage. Issue order is pinned: the wait counter is in order, so a stage
+  // consumed before the loads behind it is waited for without waiting for them.
+  for (uint32_t j0 = 0; j0 < steps; j0 += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+      const uint32_t j = j0 + s;
+      u32x4 *buf = As[s & 1];  // NS is even: step j uses buffer j & 1
+      if (st[s].k0 + KS > K) zero_tail<BM, BN, MX>(st[s], K, t, q);  // uniform: only a ragged step
+#pragma unroll
+      for (int i = 0; i < C::AL; i++) {
+        const int c = t + NT * i, row = c / CH, ch = c % CH;
+        buf[row * CH + (ch ^ (row & 15))] = st[s].a[i];
+      }
+      __syncthreads();
+      issue_order();
+      load_x<BM, BN, MX>(st[s], X, M, K, m0, kofs(j + NS), t);
+      issue_order();
+      float sc[TN];
+#pragma unroll
+      for (int jn = 0; jn < TN; jn++) sc[jn] = MX ? shifted_scale(st[s].e[jn], s0[jn]) : 0.0f;
+#pragma unroll
+      for (int kk = 0; kk < KK; kk++) {
+        half8 af[TM], bf[TN];
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          const int row = wm * (BM / 2) + i * 16 + r16;
+          af[i] = __builtin_bit_cast(half8, buf[row * CH + (xchunk<MX>(q, kk) ^ (row & 15))]);
+        }
+#pragma unroll
+        for (int jn = 0; jn < TN; jn++) {
+          if constexpr (MX) {
+            bf[jn] = fp4x8_to_half8(st[s].b[jn][0][kk], sc[jn]);
+          } else {
+            const u32x4 v = st[s].b[jn][kk >> 1];
+            bf[jn] = i8x8_to_half8(v[(kk & 1) * 2], v[(kk & 1) * 2 + 1]);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int jn = 0; jn < TN; jn++)
+            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
+      }
+      issue_order();
+      load_w<BM, BN, MX>(st[s], W, E, K, kofs(j + NS), brow, q);
+      issue_order();
+    }
+  }
+  // D of tile (i, j): lane holds rows q*4 + r, column r16
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const uint32_t n = nw + j * 16 + r16;
     if (n >= N) continue;
     const float sc = MX ? 1.0f : (float)__builtin_bit_cast(f16, S[n]);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const uint32_t m = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
-        if (m < M) store_out(Y, (size_t)m * N + n, acc[i][j][r] * sc, mode);
+        const uint32_t m = m0 + wm * (BM / 2) + i * 16 + q * 4 + r;
+        if (m < M) store_out(Y, (size_t)m * N + n, MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc, mode);
       }
   }
+}
+
+// The tile shape for (m, n): the fewest rounds of workgroups over the CUs, a round weighted by the
+// tile's work and its per-tile overheads (larger tiles reuse their loads more).
+struct Shape {
+  int bm, bn;
+};
+Shape pick_shape(uint32_t m, uint32_t n, int cus) {
+  const Shape cand[] = {{128, 128}, {128, 96}, {64, 128}};
+  Shape best = cand[0];
+  double best_cost = 1e300;
+  for (const Shape &s : cand) {
+    const uint64_t tiles = (uint64_t)((m + s.bm - 1) / s.bm) * ((n + s.bn - 1) / s.bn);
+    const uint64_t rounds = (tiles + cus - 1) / cus;
+    const double cost = (double)rounds * s.bm * s.bn * (1.0 + 32.0 / s.bm + 32.0 / s.bn);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = s;
+    }
+  }
+  return best;
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess || cus <= 0)
+    cus = 256;
+  return cus;
+}
+
+template <bool MX>
+char *launch(hipStream_t st, const void *x, const void *w, const void *e, const void *s, void *y, uint32_t m,
+             uint32_t n, uint32_t k, int mode, const char *what) {
+  static const int cus = device_cus();
+  const Shape sh = pick_shape(m, n, cus);
+  const uint32_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn);
+  const bool ewords = MX && (k / 32) % 4 == 0 && hwk::aligned(e, 4);
+  const dim3 grid(tiles), block(NT);
+  const u32x4 *X = (const u32x4 *)x;
+  const uint8_t *W = (const uint8_t *)w, *E = (const uint8_t *)e;
+  const uint16_t *S = (const uint16_t *)s;
+  if (sh.bm == 128 && sh.bn == 128)
+    hipLaunchKernelGGL((k_gemm<128, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, ewords);
+  else if (sh.bm == 128)
+    hipLaunchKernelGGL((k_gemm<128, 96, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, ewords);
+  else
+    hipLaunchKernelGGL((k_gemm<64, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, ewords);
+  return hwk::launched(what);
 }
 
 }  // namespace
@@ -189,10 +369,7 @@ HWK_API char *hwk_i8_gemm(void *stream, const void *x, const void *q, const void
   HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "hwk_i8_gemm: out_mode %d", out_mode);
   HWK_CHECK(hwk::aligned(x, 16) && hwk::aligned(q, 16), "hwk_i8_gemm: x and q must be 16-byte aligned");
   if (m == 0 || n == 0) return nullptr;
-  const uint32_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  hipLaunchKernelGGL((k_gemm<false>), dim3(tiles), dim3(NT), 0, (hipStream_t)stream, (const uint4 *)x,
-                     (const uint8_t *)q, nullptr, (const uint16_t *)scale16, y, m, n, k, out_mode);
-  return hwk::launched("hwk_i8_gemm");
+  return launch<false>((hipStream_t)stream, x, q, nullptr, scale16, y, m, n, k, out_mode, "hwk_i8_gemm");
 }
 
 HWK_API char *hwk_mxfp4_gemm(void *stream, const void *x, const void *w, const void *e, void *y, uint32_t m,
@@ -202,10 +379,7 @@ HWK_API char *hwk_mxfp4_gemm(void *stream, const void *x, const void *w, const v
   HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "hwk_mxfp4_gemm: out_mode %d", out_mode);
   HWK_CHECK(hwk::aligned(x, 16) && hwk::aligned(w, 16), "hwk_mxfp4_gemm: x and w must be 16-byte aligned");
   if (m == 0 || n == 0) return nullptr;
-  const uint32_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  hipLaunchKernelGGL((k_gemm<true>), dim3(tiles), dim3(NT), 0, (hipStream_t)stream, (const uint4 *)x,
-                     (const uint8_t *)w, (const uint8_t *)e, nullptr, y, m, n, k, out_mode);
-  return hwk::launched("hwk_mxfp4_gemm");
+  return launch<true>((hipStream_t)stream, x, w, e, nullptr, y, m, n, k, out_mode, "hwk_mxfp4_gemm");
 }
 
 }  // extern "C"

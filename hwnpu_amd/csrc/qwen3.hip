@@ -13,11 +13,10 @@
 // h += down(act) in fp32. The greedy token is the first index of the largest logit.
 //
 // A decode step is five kernels a layer: the norm-fused qkv GEMV; the attention with the q/k norm,
-// RoPE and KV append in its prologue (a few workgroups a kv head, merged by the last to finish);
-// o_proj; the norm- and SwiGLU-fused gate_up GEMV; down. Then four more: embed, final norm, head,
-// argmax. Its token
-// and position are read on the device (hist[pos], pos), and the argmax writes the next token
-// and advances pos, so one captured graph replays for every step.
+// RoPE and KV append in its prologue (partials over chunks of the cache); o_proj, which merges the
+// partials in its prologue; the norm- and SwiGLU-fused gate_up GEMV; down. Then four more: embed,
+// final norm, head, argmax. Its token and position are read on the device (hist[pos], pos), and the
+// argmax writes the next token and advances pos, so one captured graph replays for every step.
 #include <math.h>
 #include <algorithm>
 #include <string>

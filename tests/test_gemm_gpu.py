@@ -67,3 +67,34 @@ def test_mxfp4_gemm_uniform_codes(dev, orc):
     wd = orc.mxfp4_dequantize(w.cpu().numpy(), e.cpu().numpy())
     want = orc.sgemm(x.cpu().numpy().astype(np.float32), wd, transb=True)
     check_close(ops.mxfp4_gemm(x, w, e, "f32").cpu().numpy(), want)
+
+
+def test_mxfp4_gemm_edge_exponents(dev, orc):
+    """Block exponents outside [-23, 13], where a code times its scale is no fp16 value: rows whose
+    scales reach 2^20 (6 * 2^20 overflows fp16) or fall to 2^-40, rows spanning 36 and 50 exponents,
+    zero scales (e = 0) among normal ones. Each output column (one weight row) is checked against the
+    oracle's fp32 Dequantize + sgemm relative to its own size."""
+    m, n, k = 33, 96, 256
+    rng = np.random.default_rng(11)
+    x = synth.normal(m * k, "k3edge.x").view(m, k)
+    w = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    e = np.empty((n, k // 32), np.int64)
+    nb = k // 32
+    e[0:16] = rng.integers(127 + 10, 127 + 21, (16, nb))   # scales up to 2^20
+    e[16:32] = rng.integers(127 - 40, 127 - 29, (16, nb))  # down to 2^-40
+    e[32:48] = rng.integers(127 - 21, 127 + 16, (16, nb))  # a span of 36
+    e[48:64] = rng.integers(127 - 4, 127 + 3, (16, nb))    # the usual range
+    e[64:80] = rng.integers(127 - 4, 127 + 3, (16, nb))
+    e[64:80, ::3] = 0                                       # zero scales among them
+    e[80:96] = rng.integers(127 - 4, 127 + 3, (16, nb))
+    e[80:96, 0] = 127 + 20                                  # a span of 50: the 2^-30 blocks lose
+    e[80:96, 1] = 127 - 30                                  # bits below 2^-24 of the shifted scale
+    e = e.astype(np.uint8)
+    wd = orc.mxfp4_dequantize(w, e)
+    want = orc.sgemm(x.cpu().numpy().astype(np.float32), wd, transb=True)
+    got = ops.mxfp4_gemm(x, torch.from_numpy(w).cuda(), torch.from_numpy(e).cuda(), "f32").cpu().numpy()
+    assert np.all(np.isfinite(got))
+    for j in range(n):
+        col_rms = rms(want[:, j])
+        err = float(np.max(np.abs(got[:, j].astype(np.float64) - want[:, j])))
+        assert err <= TOL * col_rms, f"column {j}: max|d|={err:.4g} rms={col_rms:.4g}"
