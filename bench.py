@@ -23,7 +23,9 @@ counter's reading of a plain device copy of the same bytes) before this process 
 null, with the reason, when rocprofv3 is unavailable.
 
 gemv: only that GEMV measurement. copy: a plain device copy of the same 8,933,376 bytes timed the
-same way (the calibration run for the FETCH_SIZE / WRITE_SIZE counters).
+same way (the calibration run for the FETCH_SIZE / WRITE_SIZE counters). floor: hwk_read_floor, one
+launch that only reads the same bytes, over a sweep of waves a CU and loads a lane in flight: the
+shortest time a single launch needs for them (roofline.read_floor carries its best of three shapes).
 
 The other configurations (each a graph of back-to-back launches over distinct input copies, timed
 with HIP events; the decode line carries them under "configs" without CPU baselines, and the
@@ -122,6 +124,36 @@ def gemv_roofline(steps: int, warmup: int, eager: bool = False):
 
     us, launches, wall = _graph_time(launch_all, steps, warmup, eager)
     return {"us": us, "launches": launches, "wall_s": wall, "gbs": GEMV_BYTES / (us * 1e-6) / 1e9}
+
+
+FLOOR_SHAPES = [(wpc, lpl) for wpc in (8, 16, 32) for lpl in (1, 2, 4)]
+
+
+def read_floor(steps: int = 1280, warmup: int = 128, shapes=FLOOR_SHAPES):
+    """The read floor of the GEMV configuration's bytes: hwk_read_floor over 64 distinct buffers of
+    GEMV_BYTES each (one launch each, in a graph, as the GEMV is timed), for each (waves a CU, loads a
+    lane in flight); the fastest is the shortest time in which one launch reads those bytes here."""
+    import torch
+
+    from hwnpu_amd import hwk
+
+    lib = hwk.load()
+    src = [torch.empty(GEMV_BYTES, dtype=torch.uint8, device="cuda") for _ in range(COPIES)]
+    for t in src:
+        t.random_(0, 255)
+    out = torch.zeros(16, dtype=torch.int32, device="cuda")
+    rows = []
+    for wpc, lpl in shapes:
+        def launch_all():
+            s = torch.cuda.current_stream().cuda_stream
+            for t in src:
+                lib.hwk_read_floor(s, t.data_ptr(), GEMV_BYTES, out.data_ptr(), wpc, lpl)
+
+        us, _, _ = _graph_time(launch_all, steps, warmup)
+        rows.append({"waves_per_cu": wpc, "loads_per_lane": lpl, "us": round(us, 3),
+                     "gbs": round(GEMV_BYTES / (us * 1e-6) / 1e9, 1)})
+    best = min(rows, key=lambda r: r["us"])
+    return best, rows
 
 
 def copy_roofline(steps: int, warmup: int, eager: bool = False):
@@ -532,7 +564,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "copy", "gemm", "attn", "moe"])
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "gemv", "copy", "floor", "gemm", "attn", "moe"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager", action="store_true", help="gemv/copy: launch one by one, no graph (counter runs)")
     ap.add_argument("--no-counters", action="store_true", help="decode: skip the rocprofv3 traffic runs")
@@ -570,6 +603,10 @@ def main():
         cpu = None if args.no_cpu else [moe_cpu(T) for T in (1, 5)]
         print(json.dumps({"workload": "moe", "results": rows, "cpu_baseline": cpu}))
         return
+    if args.workload == "floor":
+        best, rows = read_floor()
+        print(json.dumps({"workload": "floor", "bytes": GEMV_BYTES, "best": best, "sweep": rows}))
+        return
     if args.workload == "gemv":
         r = gemv_roofline(args.steps or 3200, 320 if args.warmup is None else args.warmup, args.eager)
         print(json.dumps({"workload": "gemv", "launches": r["launches"], "us_per_launch": round(r["us"], 3),
@@ -579,6 +616,7 @@ def main():
     warmup = args.warmup if args.warmup is not None else 16
     d = decode_rate(steps, warmup)
     g = gemv_roofline(3200, 320)
+    floor, _ = read_floor(shapes=[(16, 1), (32, 1), (32, 2)])
     configs = {"c2_int8_gemm": gemm_rate(4),
                "c3_attention": [attn_rate(L, i8) for L in (2048, 32768) for i8 in (False, True)],
                "c4_moe": [moe_rate(T, 2) for T in (1, 5)]}
@@ -615,7 +653,10 @@ def main():
                      "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_detail": traffic_detail,
                      "kernel": f"{GEMV_KERNEL} (MXFP4 GEMV 8192x2048, 64 distinct copies, graph)",
-                     "us_per_launch": round(g["us"], 3), "bytes_per_launch": GEMV_BYTES},
+                     "us_per_launch": round(g["us"], 3), "bytes_per_launch": GEMV_BYTES,
+                     "read_floor": dict(floor, frac=round(GEMV_BYTES / (floor["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                        gemv_over_floor=round(floor["us"] / g["us"], 4),
+                                        kernel="hwk_read_floor: one launch reading the same bytes, no compute")},
         "cpu_baseline": cpu,
         "configs": configs,
     }

@@ -645,16 +645,16 @@ void launch_rpw(hipStream_t st, const void *w, const void *e, const void *x, voi
   }
 }
 
-// K1 for rows of 33..256 blocks (64 lanes a row): 8 waves a workgroup, 2 rows a wave for matrices of
-// 4096 rows or more, else 1 (twice the waves for the short matrices of the decode step).
+// K1 for rows of 33..256 blocks (64 lanes a row), one row a wave: the most waves in flight, which is
+// what a single launch's read of a few MB needs (16 waves a workgroup for matrices of 4096 rows or
+// more, measured fastest on C1; else 8 waves).
 template <int BPL, int MODE>
 void launch_lds_m(hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n, uint32_t nb) {
-  constexpr int W = 8;
   if (n >= 4096) {
-    hipLaunchKernelGGL((k_mxfp4_gemv_lds<W, 2, BPL, MODE>), dim3((n + 2 * W - 1) / (2 * W)), dim3(64 * W), 0, st,
+    hipLaunchKernelGGL((k_mxfp4_gemv_lds<16, 1, BPL, MODE>), dim3((n + 15) / 16), dim3(64 * 16), 0, st,
                        (const uint4 *)w, (const uint8_t *)e, (const uint4 *)x, y, n, nb);
   } else {
-    hipLaunchKernelGGL((k_mxfp4_gemv_lds<W, 1, BPL, MODE>), dim3((n + W - 1) / W), dim3(64 * W), 0, st,
+    hipLaunchKernelGGL((k_mxfp4_gemv_lds<8, 1, BPL, MODE>), dim3((n + 7) / 8), dim3(64 * 8), 0, st,
                        (const uint4 *)w, (const uint8_t *)e, (const uint4 *)x, y, n, nb);
   }
 }

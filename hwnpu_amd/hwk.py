@@ -160,6 +160,7 @@ SIGNATURES = {
     "hwk_synth_normal": (ERR, [P, P, U64, U64, U32, C.c_int]),
     "hwk_synth_mxfp4": (ERR, [P, P, P, U32, U32, U64, U32]),
     "hwk_mxfp4_encode": (ERR, [P, P, P, P, U32, U32]),
+    "hwk_read_floor": (ERR, [P, P, SZ, P, U32, U32]),
     "hwk_synth_reference": (ERR, [P, P, U64, C.c_char_p, C.c_int]),
 }
 

@@ -478,6 +478,16 @@ HWK_API char *hwk_synth_reference(void *stream, void *out, uint64_t n, const cha
 HWK_API char *hwk_mxfp4_encode(void *stream, const void *x, void *w, void *e, uint32_t rows,
                                uint32_t k);
 
+/* ---- measurement (no counterpart in the reference) ---- */
+
+/* The read floor: one launch that reads bytes (a multiple of 16, 16-byte aligned) from src once in
+ * 16-byte loads and computes nothing, with waves_per_cu (1..32) waves a CU each holding
+ * loads_per_lane (1, 2, 4 or 8) loads in flight; *out (device) is written only for data that
+ * practically never occurs. Its time is the shortest in which a single launch streams that many
+ * bytes, the bound for the batch-1 GEMV (K1) of the same bytes. */
+HWK_API char *hwk_read_floor(void *stream, const void *src, size_t bytes, uint32_t *out,
+                             uint32_t waves_per_cu, uint32_t loads_per_lane);
+
 #ifdef __cplusplus
 }
 #endif
