@@ -622,25 +622,27 @@ __global__ void k_kv_quantize_i8(const f16 *__restrict__ x, int8_t *__restrict__
   }
 }
 
-// The split of hwk_attn_decode: workgroups of 4 waves, each wave kpw keys (a multiple of 16), chunk =
-// 4*kpw keys a workgroup. kpw is sized so that the launch runs about 2048 waves (8 a CU, each with two
-// tiles of loads in flight), between 32 and 256 keys, more when a head would exceed kMaxChunks chunks.
-// A caller's split (a multiple of 64) is the chunk.
-constexpr int kDecodeWaves = 4;
+// The split of hwk_attn_decode: workgroups of W waves (8 for int8 caches of 8,192 keys or more, else
+// 4: measured fastest for each), each wave kpw keys (a multiple of 16), chunk = W*kpw keys a
+// workgroup. kpw is sized so that the launch runs about 2048 waves (8 a CU, each with two tiles of
+// loads in flight), between 32 and 256 keys, more when a head would exceed kMaxChunks chunks. A
+// caller's split (a multiple of 64) is the chunk.
+uint32_t decode_waves(const hwk_attn_params *p) { return p->kv_int8 && p->len >= 8192 ? 8u : 4u; }
 
 uint32_t pick_kpw(const hwk_attn_params *p) {
-  if (p->split) return p->split / kDecodeWaves;
+  const uint32_t W = decode_waves(p);
+  if (p->split) return p->split / W;
   const uint64_t keys = (uint64_t)p->len * p->kv_heads;
   uint64_t kpw = (keys + 2047) / 2048;
   kpw = (kpw + 15) / 16 * 16;
   if (kpw < 32) kpw = 32;
   if (kpw > 256) kpw = 256;
-  const uint64_t min_kpw = ((uint64_t)p->len + (uint64_t)kMaxChunks * kDecodeWaves - 1) / ((uint64_t)kMaxChunks * kDecodeWaves);
+  const uint64_t min_kpw = ((uint64_t)p->len + (uint64_t)kMaxChunks * W - 1) / ((uint64_t)kMaxChunks * W);
   if (kpw < min_kpw) kpw = (min_kpw + 15) / 16 * 16;
   return (uint32_t)kpw;
 }
 
-uint32_t pick_chunk(const hwk_attn_params *p) { return pick_kpw(p) * kDecodeWaves; }
+uint32_t pick_chunk(const hwk_attn_params *p) { return pick_kpw(p) * decode_waves(p); }
 
 uint32_t chunks_of(const hwk_attn_params *p, uint32_t chunk) { return p->len ? (p->len + chunk - 1) / chunk : 1; }
 
@@ -694,17 +696,20 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
   HWK_CHECK(!pos || p->len == p->capacity, "attn_decode_dev: a device length needs the grid of the capacity");
   const uint32_t len = pos ? len_add : p->len;
-  constexpr int W = kDecodeWaves;
+  const uint32_t W = decode_waves(p);
   const uint32_t kpw = chunk / W;
   const dim3 grid(p->kv_heads * nchunk), block(64 * W);
   const uint16_t *ks = (const uint16_t *)k_scale, *vs = (const uint16_t *)v_scale;
   const int mode = (int)p->out_mode;
 #define HWK_ATTN_LAUNCH(GG)                                                                                          \
-  if (p->kv_int8)                                                                                                    \
-    hipLaunchKernelGGL((k_attn_decode<GG, true, W>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,   \
+  if (p->kv_int8 && W == 8)                                                                                          \
+    hipLaunchKernelGGL((k_attn_decode<GG, true, 8>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,   \
+                       ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, kpw, scale_log2);                      \
+  else if (p->kv_int8)                                                                                               \
+    hipLaunchKernelGGL((k_attn_decode<GG, true, 4>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,   \
                        ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, kpw, scale_log2);                      \
   else                                                                                                               \
-    hipLaunchKernelGGL((k_attn_decode<GG, false, W>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,  \
+    hipLaunchKernelGGL((k_attn_decode<GG, false, 4>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,  \
                        ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, kpw, scale_log2);
   if (G == 1) {
     HWK_ATTN_LAUNCH(1)
