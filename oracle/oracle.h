@@ -29,8 +29,16 @@
  *   or_choose                    TestChooseSigmoidBias KAT (experts/weights_test.go:11-26);
  *                                top-k equals a full stable sort's first k.
  *   or_experts_*                 f64 dequantized-experts brute force; the int8-activation path
- *                                against the fp32 path (cosine >= 0.999, experts/host_test.go:211-285).
+ *                                against the fp32 path (cosine >= 0.999, experts/host_test.go:211-285);
+ *                                with biases and the gpt-oss gated unit, TestHostRunSmall's float64
+ *                                form (host_test.go:208-284), which fails when the clamp, the +1 on
+ *                                up, alpha or a bias is dropped.
  *   or_rmsnorm/rope/silu/argmax  closed forms (rotation preserves norms, RMS of output = |w|).
+ *   or_fnv64a / or_synth_reference  FNV-1a 64 published test vectors; the MMIX LCG sequence against
+ *                                its recurrence and the [-0.2, 0.2) range and mean of the values.
+ *   or_qwen3_*                   a float64 forward written from the model's semantics on the same
+ *                                weights (relative RMS < 5e-3 at every position); cached stepping
+ *                                equals the full prompt; fails when RoPE is dropped or gate/up swap.
  */
 #ifndef HWNPU_ORACLE_H
 #define HWNPU_ORACLE_H
