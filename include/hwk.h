@@ -62,7 +62,9 @@ HWK_API char *hwk_device_count(uint32_t *count);
 /* Fails unless the device is gfx950: the code objects in this library are built for it alone. */
 HWK_API char *hwk_device_open(uint32_t index, hwk_device **out);
 HWK_API void hwk_device_free(hwk_device *d);
-/* Writes the value, NUL terminated, into buf of n bytes; *need is its length with the NUL. */
+/* The device's value for key (an HWK_INFO_* string: name, gfx arch, PCI bus id, CU count, memory
+ * bytes), copied into buf (n bytes, always terminated when n > 0); *need receives the bytes the whole
+ * string takes, its terminating zero included, so a caller can size buf and ask again. */
 HWK_API char *hwk_device_info(hwk_device *d, int key, char *buf, size_t n, size_t *need);
 HWK_API char *hwk_device_synchronize(hwk_device *d);
 
