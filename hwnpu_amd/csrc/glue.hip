@@ -1,131 +1,17 @@
 // The decoder's small ops as C-ABI entry points (K6): RMSNorm, the per-head norm + RoPE, KV append,
-// SiLU(gate)*up, the residual add, the embedding gather and the greedy argmax. The fused decode
-// step runs the same arithmetic inside its GEMV prologues/epilogues and the attention prologue;
-// these are the standalone forms a caller composes (prefill pieces, other models, tests).
-//
-// Numerics, identical to the fused forms:
-//   RMSNorm   r = float(1 / sqrt(sum(x^2) / n + eps)), the sum of squares in float64; y = (x * r) * w
-//             (reference internal/llm/blocks/blocks.go:351-395)
-//   RoPE      rotate_half over cat(freqs, freqs) tables: y[j] = x[j] c[j] - x[j+h] s[j] for j < h,
-//             y[j+h] = x[j+h] c[j] + x[j] s[j] (blocks.go:412-445), no fused multiply-add
-//   SiLU*up   g / (1 + float(exp(-g))) * u with exp in float64 (blocks.go:395-401; the reference's
-//             expert act, internal/llm/experts/host.go:45-57)
-//   argmax    strict > from index 0 (internal/chat/sample.go:80-87): the lowest index of the
-//             largest value; NaNs never win except at index 0, where the reference keeps it.
+// SiLU(gate)*up, the residual add, the embedding gather and the greedy argmax. Their kernels (but the
+// argmax's) are the model's own (glue_kernels.h): the decode step's prompt path, final norm and
+// embedding launch them, and its attention prologue computes the per-head norm + RoPE with the same
+// function. The argmax: strict > from index 0 (internal/chat/sample.go:80-87), the lowest index of
+// the largest value; NaNs never win except at index 0, where the reference keeps it.
 #include <math.h>
 
+#include "glue_kernels.h"
 #include "hwk_common.h"
 
 namespace {
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-// One workgroup a row.
-template <bool F16OUT>
-__global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, double eps,
-                                                 void *__restrict__ out, uint32_t n) {
-#pragma clang fp contract(off)
-  __shared__ double red[4];
-  const int t = threadIdx.x, lane = t & 63;
-  const float *xr = x + (size_t)blockIdx.x * n;
-  double ss = 0.0;
-  for (uint32_t i = t; i < n; i += 256) {
-    const double v = (double)xr[i];
-    ss += v * v;
-  }
-  ss = wave_sum_d(ss);
-  if (lane == 0) red[t >> 6] = ss;
-  __syncthreads();
-  ss = ((red[0] + red[1]) + red[2]) + red[3];
-  const float r = (float)(1.0 / sqrt(ss / (double)n + eps));
-  for (uint32_t i = t; i < n; i += 256) {
-    const float y = f32_value((xr[i] * r) * w[i]);
-    if (F16OUT)
-      ((f16 *)out)[(size_t)blockIdx.x * n + i] = (f16)y;
-    else
-      ((float *)out)[(size_t)blockIdx.x * n + i] = y;
-  }
-}
-
-// One wave a (token, head) of 128 dims: lane l holds dims l and l + 64, the pair rotate_half mixes.
-// The head's RMSNorm (when nw is given) then RoPE at position pos0 + token.
-template <bool F16OUT>
-__global__ __launch_bounds__(256) void k_norm_rope(const float *__restrict__ x, const float *__restrict__ nw,
-                                                   const float *__restrict__ cos_t, const float *__restrict__ sin_t,
-                                                   double eps, void *__restrict__ out, uint32_t heads, uint32_t rows,
-                                                   uint32_t pos0) {
-#pragma clang fp contract(off)
-  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;  // whole waves leave together
-  const uint32_t l = threadIdx.x & 63, t = row / heads;
-  const float *xr = x + (size_t)row * 128;
-  float y0 = xr[l], y1 = xr[l + 64];
-  if (nw) {
-    double ss = (double)y0 * (double)y0 + (double)y1 * (double)y1;
-    ss = wave_sum_d(ss);
-    const float r = (float)(1.0 / sqrt(ss / 128.0 + eps));
-    y0 = (y0 * r) * nw[l];
-    y1 = (y1 * r) * nw[l + 64];
-  }
-  const size_t p = (size_t)pos0 + t;
-  const float c = cos_t[p * 64 + l], s = sin_t[p * 64 + l];
-  const float o0 = f32_value(y0 * c + (-y1) * s), o1 = f32_value(y1 * c + y0 * s);
-  if (F16OUT) {
-    ((f16 *)out)[(size_t)row * 128 + l] = (f16)o0;
-    ((f16 *)out)[(size_t)row * 128 + l + 64] = (f16)o1;
-  } else {
-    ((float *)out)[(size_t)row * 128 + l] = o0;
-    ((float *)out)[(size_t)row * 128 + l + 64] = o1;
-  }
-}
-
-// kc/vc (kvh, cap, dim) rows pos0 + t of k/v (T, kvh, dim), fp16, 16 bytes a thread.
-__global__ __launch_bounds__(256) void k_kv_append(const uint4 *__restrict__ k, const uint4 *__restrict__ v,
-                                                   uint4 *__restrict__ kc, uint4 *__restrict__ vc, uint32_t kvh,
-                                                   uint32_t cap, uint32_t vecs, uint32_t pos0, uint64_t total) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
-  const uint64_t row = i / vecs, c = i % vecs;  // row = t * kvh + head
-  const uint64_t t = row / kvh, hd = row % kvh;
-  const uint64_t dst = (hd * cap + pos0 + t) * vecs + c;
-  kc[dst] = k[i];
-  vc[dst] = v[i];
-}
-
-template <bool F16OUT>
-__global__ __launch_bounds__(256) void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u,
-                                                  void *__restrict__ out, uint64_t n, uint32_t stride) {
-#pragma clang fp contract(off)
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float gv = g[i * stride], uv = u[i * stride];
-  const float y = f32_value(gv / (1.0f + (float)exp(-(double)gv)) * uv);
-  if (F16OUT)
-    ((f16 *)out)[i] = (f16)y;
-  else
-    ((float *)out)[i] = y;
-}
-
-__global__ __launch_bounds__(256) void k_add(float *__restrict__ y, const float *__restrict__ x, uint64_t n) {
-#pragma clang fp contract(off)
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n) y[i] = y[i] + x[i];
-}
-
-// out (T, hidden) fp32 = rows ids[t] of the fp16 table; a row whose id is outside [0, vocab) is NaN.
-__global__ __launch_bounds__(256) void k_embed_ids(const int32_t *__restrict__ ids, const f16 *__restrict__ table,
-                                                   float *__restrict__ out, uint32_t hidden, uint32_t vocab) {
-  const uint32_t t = blockIdx.y;
-  const int32_t id = ids[t];
-  const bool ok = id >= 0 && (uint32_t)id < vocab;
-  const f16 *row = table + (size_t)(ok ? id : 0) * hidden;
-  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < hidden; i += gridDim.x * 256)
-    out[(size_t)t * hidden + i] = ok ? (float)row[i] : __builtin_nanf("");
-}
+using namespace hwk_glue;
 
 constexpr uint32_t kArgParts = 64;  // workgroups a row
 
@@ -294,9 +180,8 @@ HWK_API char *hwk_embed(void *stream, const void *table, const void *ids, void *
   HWK_CHECK(vocab > 0 && hidden > 0, "hwk_embed: empty table");
   HWK_CHECK(tokens <= 65535, "hwk_embed: %u tokens (at most 65535)", tokens);
   if (tokens == 0) return nullptr;
-  const uint32_t bx = (hidden + 255) / 256 < 8 ? (hidden + 255) / 256 : 8;
-  hipLaunchKernelGGL(k_embed_ids, dim3(bx, tokens), dim3(256), 0, (hipStream_t)stream, (const int32_t *)ids,
-                     (const f16 *)table, (float *)out, hidden, vocab);
+  hipLaunchKernelGGL(k_embed_ids, dim3(embed_blocks(hidden), tokens), dim3(256), 0, (hipStream_t)stream,
+                     (const int32_t *)ids, nullptr, 0u, (const f16 *)table, (float *)out, hidden, vocab);
   return hwk::launched("hwk_embed");
 }
 
@@ -321,3 +206,11 @@ HWK_API char *hwk_argmax(void *stream, const void *x, void *out, uint32_t rows, 
 }
 
 }  // extern "C"
+
+char *hwk::rmsnorm_f16(hipStream_t st, const float *h, const float *nw, double eps, void *out, uint32_t rows,
+                       uint32_t k) {
+  HWK_CHECK(h && nw && out, "rmsnorm_f16: null pointer");
+  if (rows == 0 || k == 0) return nullptr;
+  hipLaunchKernelGGL(k_rmsnorm<true>, dim3(rows), dim3(256), 0, st, h, nw, eps, out, k);
+  return hwk::launched("rmsnorm_f16");
+}

@@ -474,25 +474,6 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_rows(const uint4 *__restrict
   }
 }
 
-// RMSNorm of fp32 rows to fp16, one workgroup a row (the rounding of k_mxfp4_gemv_x's NORM).
-__global__ __launch_bounds__(256) void k_rmsnorm_f16(const float *__restrict__ h, const float *__restrict__ nw,
-                                                     double eps, f16 *__restrict__ out, uint32_t k) {
-  __shared__ double red[4];
-  const int t = threadIdx.x, lane = t & 63;
-  const float *hr = h + (size_t)blockIdx.x * k;
-  double ss = 0.0;
-  for (uint32_t i = t; i < k; i += 256) {
-    const double v = (double)hr[i];
-    ss += v * v;
-  }
-  ss = wave_sum_f64(ss);
-  if (lane == 0) red[t >> 6] = ss;
-  __syncthreads();
-  ss = ((red[0] + red[1]) + red[2]) + red[3];
-  const float r = (float)(1.0 / sqrt(ss / (double)k + eps));
-  for (uint32_t i = t; i < k; i += 256) out[(size_t)blockIdx.x * k + i] = (f16)f32_value((hr[i] * r) * nw[i]);
-}
-
 // ---- the encoder (reference internal/mxfp4/encode.go:11-78), one thread a block, in float64
 // with every product and sum rounded on its own, as the reference computes it ----
 
@@ -923,13 +904,6 @@ char *synth_mxfp4_rows(hipStream_t st, void *w, void *e, uint32_t rows, uint32_t
   hipLaunchKernelGGL(k_synth_mxfp4, dim3((uint32_t)((nblocks + 127) / 128)), dim3(128), 0, st, (uint8_t *)w,
                      (uint8_t *)e, nblocks, key, stdv, k / 32, stride, row0);
   return launched("synth_mxfp4_rows");
-}
-
-char *rmsnorm_f16(hipStream_t st, const float *h, const float *nw, double eps, void *out, uint32_t rows, uint32_t k) {
-  HWK_CHECK(h && nw && out, "rmsnorm_f16: null pointer");
-  if (rows == 0 || k == 0) return nullptr;
-  hipLaunchKernelGGL(k_rmsnorm_f16, dim3(rows), dim3(256), 0, st, h, nw, eps, (f16 *)out, k);
-  return launched("rmsnorm_f16");
 }
 
 }  // namespace hwk

@@ -22,24 +22,19 @@
 #include <string>
 #include <vector>
 
+#include "glue_kernels.h"
 #include "hwk_common.h"
 #include "internal.h"
 #include "synth.h"
 
 namespace {
 
-// ---- glue kernels (K6) ----
+// ---- glue kernels (K6): the embedding gather, RMSNorm and SiLU*up are hwk_glue's (glue_kernels.h),
+// the same kernels as the hwk_embed / hwk_rmsnorm / hwk_silu_mul entry points ----
 
-// h[t] = fp32 of embedding row hist[*pos + base + t]
-__global__ __launch_bounds__(256) void k_embed(const int32_t *__restrict__ hist, const int32_t *__restrict__ pos,
-                                               uint32_t base, const f16 *__restrict__ emb, float *__restrict__ h,
-                                               uint32_t hidden, uint32_t vocab) {
-  const uint32_t t = blockIdx.x;
-  uint32_t tok = (uint32_t)hist[(uint32_t)*pos + base + t];
-  if (tok >= vocab) tok = vocab - 1;  // memory safety only: tokens are checked on the host
-  const f16 *row = emb + (size_t)tok * hidden;
-  for (uint32_t i = threadIdx.x; i < hidden; i += 256) h[(size_t)t * hidden + i] = (float)row[i];
-}
+using hwk_glue::embed_blocks;
+using hwk_glue::k_embed_ids;
+using hwk_glue::k_silu_mul;
 
 // One wave a (token t, head slot): slots [0, heads) are query heads, [heads, heads+kvh) key heads,
 // then value heads. A lane holds dims l and l+64, the pair rotate_half mixes. q and k: per-head
@@ -74,15 +69,6 @@ __global__ __launch_bounds__(256) void k_qk_rope(const float *__restrict__ qkv, 
                           : kc + ((size_t)(slot - heads) * cap + p) * 128;
   dst[l] = (f16)o0;
   dst[l + 64] = (f16)o1;
-}
-
-// act (T, inter) fp16 = silu(gate) * up of gu (T, 2*inter) fp32, gate at even columns.
-__global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, f16 *__restrict__ act, uint64_t n) {
-#pragma clang fp contract(off)
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float g = gu[2 * i], u = gu[2 * i + 1];
-  act[i] = (f16)f32_value(g / (1.0f + (float)exp(-(double)g)) * u);
 }
 
 __global__ void k_set_i32(int32_t *__restrict__ p, int32_t v) { *p = v; }
@@ -370,7 +356,8 @@ char *capture(hwk_qwen3 *m, int i, uint32_t n);
 // The decode step on stream st: the token hist[*pos] at position *pos.
 char *step(hwk_qwen3 *m, hipStream_t st) {
   const hwk_qwen3_config &c = m->c;
-  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed, m->h, c.hidden, c.vocab);
+  hipLaunchKernelGGL(k_embed_ids, dim3(embed_blocks(c.hidden), 1), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed,
+                     m->h, c.hidden, c.vocab);
   HWK_Q(hwk::launched("qwen3 embed"));
   for (auto &ly : m->L) {
     HWK_Q(hwk::mxfp4_gemv_x(st, ly.qkv.w, ly.qkv.e, nullptr, m->h, ly.in_norm, m->eps, m->qkv, m->qkv_n, c.hidden,
@@ -412,7 +399,8 @@ char *capture(hwk_qwen3 *m, int i, uint32_t n) {
 char *prefill_piece(hwk_qwen3 *m, hipStream_t st, uint32_t T, uint32_t start, bool last_piece) {
   const hwk_qwen3_config &c = m->c;
   hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(1), 0, st, m->pos, (int32_t)start);
-  hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed, m->h, c.hidden, c.vocab);
+  hipLaunchKernelGGL(k_embed_ids, dim3(embed_blocks(c.hidden), T), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed,
+                     m->h, c.hidden, c.vocab);
   HWK_Q(hwk::launched("qwen3 embed"));
   const uint32_t slots = c.heads + 2 * c.kv_heads;
   hwk_attn_params pp = m->ap;
@@ -429,7 +417,8 @@ char *prefill_piece(hwk_qwen3 *m, hipStream_t st, uint32_t T, uint32_t start, bo
     HWK_Q(hwk::rmsnorm_f16(st, m->h, ly.post_norm, m->eps, m->x16, T, c.hidden));
     HWK_Q(hwk_mxfp4_gemm(st, m->x16, ly.gu.w, ly.gu.e, m->gu, T, 2 * c.inter, c.hidden, HWK_OUT_F32));
     const uint64_t n = (uint64_t)T * c.inter;
-    hipLaunchKernelGGL(k_swiglu, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, m->gu, m->a16, n);
+    hipLaunchKernelGGL(k_silu_mul<true>, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, m->gu, m->gu + 1, m->a16, n,
+                       2u);
     HWK_Q(hwk::launched("qwen3 swiglu"));
     HWK_Q(hwk_mxfp4_gemm(st, m->a16, ly.down.w, ly.down.e, m->h, T, c.hidden, c.inter, HWK_OUT_ADD_F32));
   }
@@ -463,7 +452,8 @@ char *rows_linear(hipStream_t st, const f16 *x, const hwk_qwen3::Lin &l, float *
 char *verify_piece(hwk_qwen3 *m, hipStream_t st, uint32_t T, uint32_t start) {
   const hwk_qwen3_config &c = m->c;
   hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(1), 0, st, m->pos, (int32_t)start);
-  hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed, m->h, c.hidden, c.vocab);
+  hipLaunchKernelGGL(k_embed_ids, dim3(embed_blocks(c.hidden), T), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed,
+                     m->h, c.hidden, c.vocab);
   HWK_Q(hwk::launched("qwen3 verify embed"));
   const uint32_t slots = c.heads + 2 * c.kv_heads;
   hwk_attn_params pp = m->ap;
@@ -480,7 +470,8 @@ char *verify_piece(hwk_qwen3 *m, hipStream_t st, uint32_t T, uint32_t start) {
     HWK_Q(hwk::rmsnorm_f16(st, m->h, ly.post_norm, m->eps, m->x16, T, c.hidden));
     HWK_Q(rows_linear(st, m->x16, ly.gu, m->gu, T, HWK_OUT_F32));
     const uint64_t n = (uint64_t)T * c.inter;
-    hipLaunchKernelGGL(k_swiglu, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, m->gu, m->a16, n);
+    hipLaunchKernelGGL(k_silu_mul<true>, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, m->gu, m->gu + 1, m->a16, n,
+                       2u);
     HWK_Q(hwk::launched("qwen3 verify swiglu"));
     HWK_Q(rows_linear(st, m->a16, ly.down, m->h, T, HWK_OUT_ADD_F32));
   }

@@ -117,3 +117,69 @@ def test_qwen3_c5_greedy_64(dev):
         pytest.fail(f"first diverging step {first}: got {got[first]} want {gold['tokens'][first]}, "
                     f"oracle top-2 gap there {gold['top2_gaps'][first]}")
     m.close()
+
+
+def test_decode_argmax_ties_and_nan(dev):
+    """The decode step's greedy pick (the step graph's own argmax kernel) through the model: strict >
+    from index 0 (internal/chat/sample.go:80-87), so a tie goes to the lowest index and a NaN never
+    wins except at index 0, where the reference keeps it. Rows of the tied embedding are edited on the
+    device to make the logits tie or hold NaN; the inputs never use an edited row (the table is also
+    the input embedding), and the same position is stepped again after a rewind."""
+    from hwnpu_amd.qwen3 import d2d, d2h
+
+    cfg = dict(SMALL, layers=1, vocab=1024)
+    H, V = cfg["hidden"], cfg["vocab"]
+    m = Qwen3(**cfg, max_ctx=96, max_prompt=64)
+    try:
+        m.synth(seed=1, std=0.02)
+        ptr, nbytes = m.tensor("embed")
+        table = d2h(ptr, nbytes, np.uint16).reshape(V, H)
+
+        def put_row(r, row):
+            t = torch.from_numpy(np.ascontiguousarray(row, dtype=np.uint16)).cuda()
+            d2d(ptr + r * H * 2, t.data_ptr(), H * 2)
+
+        prompt = np.arange(200, 240, dtype=np.int32)
+        m.prefill(prompt, 0)
+        P = m.position()
+        t0 = int(m.history(P, 1)[0])
+        used = set(prompt.tolist()) | {t0}
+
+        def pick():
+            m.rewind(P)
+            m.step()
+            return int(m.history(P + 1, 1)[0]), m.logits()
+
+        a, logits = pick()
+        assert a == int(np.argmax(logits)), "the step's token is the first index of the largest logit"
+        free = [r for r in range(V) if r not in used and r != a]
+        # a tie with a later row: the lower index (a) stays
+        b = next(r for r in free if r > a)
+        put_row(b, table[a])
+        tok, lg = pick()
+        assert lg[a] == lg[b] and tok == a, (a, b, tok)
+        put_row(b, table[b])
+        # a tie with an earlier row: the earlier one wins
+        below = [r for r in free if 0 < r < a]
+        if below:
+            c = below[0]
+            put_row(c, table[a])
+            tok, lg = pick()
+            assert lg[a] == lg[c] and tok == c, (a, c, tok)
+            put_row(c, table[c])
+        # a NaN logit away from index 0 never wins
+        d = next(r for r in free if r > 0)
+        put_row(d, np.full(H, 0x7E00, np.uint16))
+        tok, lg = pick()
+        assert np.isnan(lg[d]) and tok == a, (d, tok)
+        put_row(d, table[d])
+        # a NaN at index 0 is kept
+        if 0 not in used:
+            put_row(0, np.full(H, 0x7E00, np.uint16))
+            tok, lg = pick()
+            assert np.isnan(lg[0]) and tok == 0, tok
+            put_row(0, table[0])
+        tok, _ = pick()
+        assert tok == a
+    finally:
+        m.close()
