@@ -57,36 +57,6 @@ __device__ __forceinline__ half8 i8x8_to_half8(uint2 w) {
 // Every load is issued unconditionally from a clamped row (a predicated load makes the compiler wait
 // for it before issuing the next), and the terms of keys past the attended range are dropped.
 
-// The two permlane swaps: v_permlane16_swap exchanges the odd rows (16 lanes) of its first operand
-// with the even rows of its second, v_permlane32_swap the upper half of the first with the lower
-// half of the second. On two copies of v, the two results hold v and its row (half) partner in every
-// lane. Issued as inline asm after two wait states (the hazard the compiler inserts before them):
-// the compiler builtin's second result is not usable (it is folded into the first).
-__device__ __forceinline__ void swap_rows16(float &a, float &b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap_rows32(float &a, float &b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-// Sum / max over the 4 row groups (l, l^16, l^32, l^48); every lane gets the result.
-__device__ __forceinline__ float row_groups_sum(float v) {
-  float a = v, b = v;
-  swap_rows16(a, b);
-  v = a + b;
-  a = v;
-  b = v;
-  swap_rows32(a, b);
-  return a + b;
-}
-__device__ __forceinline__ float row_groups_max(float v) {
-  float a = v, b = v;
-  swap_rows16(a, b);
-  v = fmaxf(a, b);
-  a = v;
-  b = v;
-  swap_rows32(a, b);
-  return fmaxf(a, b);
-}
 // The value of lane (l & ~3) + Q of the lane's quad (DPP quad_perm broadcast).
 template <int Q>
 __device__ __forceinline__ float quad_lane(float v) {

@@ -4,105 +4,157 @@
 // causal mask (internal/llm/paged/paged.go:70-203 at tokens > 1, internal/llm/blocks/blocks.go:
 // 516-540): every query sees the keys at or before its own position.
 //
-// A workgroup owns one kv head and a block of 64/G query positions; each of its four waves takes
-// 16 positions of one query head. Key tiles of 32 go through LDS once for all four waves (K row
-// major, V transposed). On the fp16 MFMA (v_mfma_f32_16x16x32_f16) a wave computes the scores
-// transposed, S^T = K Q^T, so that a lane holds eight scores of one query: the online softmax
-// (fp32, base 2) reduces them in-lane and across its four lane groups, and the probabilities
-// already sit where the B operand of O^T = V^T P^T wants them (the MFMA's k index is permuted to
-// the keys the lane holds, consistently in A and B). P is split into an fp16 high part and an
-// fp16 residual, two MFMAs, so that P.V keeps the precision of fp32 probabilities.
+// A workgroup of four waves owns one kv head and a block of 64/G query positions (G query heads a kv
+// head); each wave takes 16 positions of one query head over all of the block's keys in tiles of 32,
+// in key order. The kv head is the workgroup index modulo kv_heads, so that with 8 kv heads every
+// workgroup of a head runs on the same XCD and the head's K and V stay in that XCD's L2. The tiles go
+// through LDS in three stages (rows padded so that every operand read is free of bank conflicts and
+// addressed by one per-lane register plus constant offsets), loaded into registers two tiles ahead.
+// On the fp16 MFMA (v_mfma_f32_16x16x32_f16) a wave computes the scores transposed, S^T = K Q^T, so
+// that a lane holds eight scores of one query: the online softmax (fp32, base 2) reduces them
+// in-lane and across its four lane groups (permlane swaps), and the probabilities already sit where
+// the B operand of O^T = V^T P^T wants them (the MFMA's k index is permuted to the keys the lane
+// holds, consistently in A and B); V^T's operand comes from the row-major tile by LDS transpose reads
+// (ds_read_b64_tr_b16). P is split into an fp16 high part and an fp16 residual, two MFMAs, so that
+// P.V keeps the precision of fp32 probabilities. The scores of the next tile are issued before the
+// softmax of the current one, so that their MFMAs run beside it.
 #include "hwk_common.h"
+#include "internal.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int KT = 32;           // keys a tile
-constexpr int KS = 128 + 8;      // K row stride in LDS (halves)
-constexpr int VS = KT + 8;       // transposed V row stride in LDS (halves)
+constexpr int KT = 32;  // keys a tile
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int NST = 3;                        // LDS stages
+constexpr uint32_t KROW = 272, VROW = 288;    // bytes of a K / V row in LDS (256 + padding)
+constexpr uint32_t KBYTES = KT * KROW;        // a stage: K rows, then V rows
+constexpr uint32_t STAGE = KBYTES + KT * VROW;
+constexpr int PER = KT * 16 / 256;            // 16-byte chunks of K (and of V) a thread moves a tile
 
-__device__ __forceinline__ half8 half8_of(uint4 u) { return __builtin_bit_cast(half8, u); }
+__device__ __forceinline__ half8 half8_of(u32x4 u) { return __builtin_bit_cast(half8, u); }
+
+// LDS transpose read: in each 16-lane group, lane 4a + c receives element c of the 8-byte
+// segments addressed by lanes a, a + 4, a + 8, a + 12 of the group.
+typedef __attribute__((address_space(3))) char lds_char;
+__device__ __forceinline__ short4v tr_read(const lds_char *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v *)p);
+}
 
 template <int G>
-__global__ __launch_bounds__(256) void k_attn_prefill(const f16 *__restrict__ q, const f16 *__restrict__ kc,
-                                                      const f16 *__restrict__ vc, void *__restrict__ out, int mode,
-                                                      uint32_t T, uint32_t start, uint32_t heads, uint32_t cap,
-                                                      float scale_log2) {
+__global__ __launch_bounds__(256) void k_attn_prefill(const u32x4 *__restrict__ q, const u32x4 *__restrict__ kc,
+                                                      const u32x4 *__restrict__ vc, void *__restrict__ out, int mode,
+                                                      uint32_t T, uint32_t start, uint32_t heads, uint32_t kvh,
+                                                      uint32_t cap, float scale_log2) {
   constexpr uint32_t QB = 64 / G;  // query positions a workgroup
-  __shared__ __attribute__((aligned(16))) f16 Ks[KT][KS];
-  __shared__ __attribute__((aligned(16))) f16 Vt[128][VS];
+  __shared__ __attribute__((aligned(16))) char lds[NST * STAGE];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int n = lane & 15, grp = lane >> 4;
   const uint32_t nqb = (T + QB - 1) / QB;
-  const uint32_t qb = nqb - 1 - blockIdx.x;  // the longest blocks first
-  const uint32_t h = blockIdx.y;
+  const uint32_t h = blockIdx.x % kvh;             // consecutive workgroups go to different XCDs
+  const uint32_t qb = nqb - 1 - blockIdx.x / kvh;  // the longest blocks first
   const uint32_t head = h * G + wave % G;
-  const uint32_t tq = qb * QB + (wave / G) * 16 + n;  // this lane's query row
+  const uint32_t tq0 = qb * QB + (wave / G) * 16;  // the wave's first query row
+  const uint32_t tq = tq0 + n;                     // this lane's query row
   const bool qlive = tq < T;
   const uint32_t qpos = start + tq;
-  const uint32_t last = start + (qb * QB + QB < T ? qb * QB + QB : T);  // keys [0, last) seen by the block
-  const size_t head_base = (size_t)h * cap;
+  const uint32_t wmax = start + min(tq0 + 15, T - 1);  // the wave's last position
+  // a tile needs the causal mask from this key on (or always, when the wave has rows past T)
+  const uint32_t wfull = tq0 + 16 <= T ? start + tq0 : 0;
+  const uint32_t last = start + min(qb * QB + QB, T);  // keys [0, last) seen by the block
+  const uint32_t tiles = (last + KT - 1) / KT;
+  const u32x4 *kh = kc + (size_t)h * cap * 16, *vh = vc + (size_t)h * cap * 16;
 
   half8 qv[4];
 #pragma unroll
   for (int s = 0; s < 4; s++)
-    qv[s] = half8_of(qlive ? *(const uint4 *)(q + ((size_t)tq * heads + head) * 128 + s * 32 + grp * 8)
-                           : make_uint4(0, 0, 0, 0));
+    qv[s] = half8_of(qlive ? q[((size_t)tq * heads + head) * 16 + s * 4 + grp] : (u32x4){0u, 0u, 0u, 0u});
+
+  // the chunks thread t moves: c = t + 256 i of a tile (key c/16, 16-byte chunk c%16)
+  uint32_t gofs[PER], kst[PER], vst[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const uint32_t c = t + 256 * i, key = c / 16, ch = c % 16;
+    gofs[i] = c;
+    kst[i] = key * KROW + ch * 16;
+    vst[i] = KBYTES + key * VROW + ch * 16;
+  }
+  // loads of tile `it` into r (K chunks, then V chunks); chunks past the keys [0, last) are clamped
+  // to the last one (in bounds, finite, masked out of the scores), and tiles past the end reload the
+  // last one, so that every load is unconditional
+  const uint32_t lim = last * 16 - 1;
+  auto load = [&](u32x4 *r, uint32_t it) __attribute__((always_inline)) {
+    const uint32_t base = min(it, tiles - 1) * KT * 16;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const uint32_t c = min(base + gofs[i], lim);
+      r[i] = kh[c];
+      r[PER + i] = vh[c];
+    }
+  };
+  auto store = [&](const u32x4 *r, uint32_t it) __attribute__((always_inline)) {
+    char *st = lds + (it % NST) * STAGE;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      *(u32x4 *)(st + kst[i]) = r[i];
+      *(u32x4 *)(st + vst[i]) = r[PER + i];
+    }
+  };
+
+  // the lane's operand addresses in a stage: K rows kt*16 + n, chunks s*4 + grp; the V^T transpose
+  // reads: source lane s of group g addresses key g*4 + s/4 (+16 for the second read), dims
+  // d*16 + 4*(s%4) .. +3
+  const uint32_t kofs = n * KROW + grp * 16;
+  const uint32_t vofs = KBYTES + (grp * 4 + n / 4) * VROW + (n % 4) * 8;
+
   floatx4 acc[8];
 #pragma unroll
   for (int d = 0; d < 8; d++) acc[d] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
   float m = -__builtin_inff(), l = 0.0f;
 
-  // the tile's global loads: thread t takes chunks t and t+256 (key c/16, dims (c%16)*8 .. +8)
-  uint4 kr[2], vr[2];
-  auto load = [&](uint32_t key0) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t c = t + 256 * i, key = key0 + c / 16, d8 = (c % 16) * 8;
-      const bool ok = key < last;
-      kr[i] = ok ? *(const uint4 *)(kc + (head_base + key) * 128 + d8) : make_uint4(0, 0, 0, 0);
-      vr[i] = ok ? *(const uint4 *)(vc + (head_base + key) * 128 + d8) : make_uint4(0, 0, 0, 0);
-    }
-  };
-  const uint32_t tiles = (last + KT - 1) / KT;
-  load(0);
-  for (uint32_t ti = 0; ti < tiles; ti++) {
-    const uint32_t key0 = ti * KT;
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t c = t + 256 * i, key = c / 16, d8 = (c % 16) * 8;
-      *(uint4 *)&Ks[key][d8] = kr[i];
-      const half8 vv = half8_of(vr[i]);
-#pragma unroll
-      for (int j = 0; j < 8; j++) Vt[d8 + j][key] = vv[j];
-    }
-    __syncthreads();
-    if (ti + 1 < tiles) load(key0 + KT);
-    // S^T: keys kt*16 + grp*4 + r of this lane's query n
-    floatx4 sc[2];
+  // S^T of tile `it`: keys it*32 + kt*16 + grp*4 + r of this lane's query n (skipped, as the update,
+  // for a tile wholly past the wave's queries)
+  auto scores = [&](floatx4 *sc, uint32_t it) __attribute__((always_inline)) {
+    if (it >= tiles || it * KT > wmax) return;
+    const char *kb = lds + (it % NST) * STAGE + kofs;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
       sc[kt] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < 4; s++)
-        sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8 *)&Ks[kt * 16 + n][s * 32 + grp * 8], qv[s],
-                                                        sc[kt], 0, 0, 0);
+        sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(half8_of(*(const u32x4 *)(kb + kt * 16 * KROW + s * 64)),
+                                                        qv[s], sc[kt], 0, 0, 0);
     }
+  };
+  // the online softmax over tile `it`'s scores, then O^T += V^T P^T
+  auto update = [&](const floatx4 *sc, uint32_t it) __attribute__((always_inline)) {
+    const uint32_t key0 = it * KT;
+    if (key0 > wmax) return;
     float s2[2][4], tmax = -__builtin_inff();
+    if (key0 + KT - 1 >= wfull) {
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const uint32_t key = key0 + kt * 16 + grp * 4 + r;
+          s2[kt][r] = (qlive && key <= qpos) ? sc[kt][r] * scale_log2 : -__builtin_inff();
+        }
+    } else {  // every key of the tile is at or before every query of the wave
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) s2[kt][r] = sc[kt][r] * scale_log2;
+    }
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint32_t key = key0 + kt * 16 + grp * 4 + r;
-        s2[kt][r] = (qlive && key <= qpos) ? sc[kt][r] * scale_log2 : -__builtin_inff();
-        tmax = fmaxf(tmax, s2[kt][r]);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      for (int r = 0; r < 4; r++) tmax = fmaxf(tmax, s2[kt][r]);
+    tmax = row_groups_max(tmax);
     const float mnew = fmaxf(m, tmax);
     float p[2][4], psum = 0.0f, alpha = 1.0f;
     if (mnew == -__builtin_inff()) {
@@ -120,8 +172,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const f16 *__restrict__ q,
           psum += p[kt][r];
         }
     }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
+    psum = row_groups_sum(psum);
     l = l * alpha + psum;
     m = mnew;
     half8 bhi, blo;
@@ -132,15 +183,46 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const f16 *__restrict__ q,
       bhi[i] = hi;
       blo[i] = (f16)(pv - (float)hi);
     }
+    if (__ballot(alpha != 1.0f)) {  // scaling by 1 is exact: skipped when no lane's max moved
+#pragma unroll
+      for (int d = 0; d < 8; d++) acc[d] *= alpha;
+    }
+    const lds_char *vb = (const lds_char *)lds + (it % NST) * STAGE + vofs;
 #pragma unroll
     for (int d = 0; d < 8; d++) {
-      acc[d] *= alpha;
-      const uint2 a0 = *(const uint2 *)&Vt[d * 16 + n][grp * 4];
-      const uint2 a1 = *(const uint2 *)&Vt[d * 16 + n][16 + grp * 4];
-      const half8 av = half8_of(make_uint4(a0.x, a0.y, a1.x, a1.y));
+      const short4v a0 = tr_read(vb + d * 32);
+      const short4v a1 = tr_read(vb + d * 32 + 16 * VROW);
+      const half8 av = __builtin_bit_cast(half8, __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7));
       acc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bhi, acc[d], 0, 0, 0);
       acc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, blo, acc[d], 0, 0, 0);
     }
+  };
+
+  // Tile it is in LDS stage it % 3 from the end of step it-2 on. Step it computes tile it+1's scores
+  // (so that their MFMAs run beside this tile's softmax), updates with tile it, and stores tile it+2
+  // into the stage tile it-1 left (read for the last time in step it-1). Two register sets: ra
+  // holds even tiles, rb odd ones, each refilled (two tiles ahead) right after it is stored.
+  u32x4 ra[2 * PER], rb[2 * PER];
+  floatx4 sa[2], sb[2];
+  load(ra, 0);
+  load(rb, 1);
+  store(ra, 0);
+  load(ra, 2);
+  store(rb, 1);
+  load(rb, 3);
+  __syncthreads();
+  scores(sa, 0);
+  for (uint32_t it = 0; it < tiles; it += 2) {
+    scores(sb, it + 1);
+    update(sa, it);
+    store(ra, it + 2);
+    load(ra, it + 4);
+    __syncthreads();
+    if (it + 1 >= tiles) break;
+    scores(sa, it + 2);
+    update(sb, it + 1);
+    store(rb, it + 3);
+    load(rb, it + 5);
     __syncthreads();
   }
   if (!qlive) return;
@@ -183,12 +265,12 @@ HWK_API char *hwk_attn_prefill(void *stream, const void *q, const void *k, const
             "hwk_attn_prefill: q, k, v 16-byte and out 8-byte aligned");
   if (tokens == 0) return nullptr;
   const uint32_t QB = 64 / G;
-  const dim3 grid((tokens + QB - 1) / QB, p->kv_heads);
+  const dim3 grid((tokens + QB - 1) / QB * p->kv_heads);
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
   hipStream_t st = (hipStream_t)stream;
 #define HWK_PF(GG)                                                                                                 \
-  hipLaunchKernelGGL((k_attn_prefill<GG>), grid, dim3(256), 0, st, (const f16 *)q, (const f16 *)k, (const f16 *)v, \
-                     out, (int)p->out_mode, tokens, start, p->heads, p->capacity, scale_log2)
+  hipLaunchKernelGGL((k_attn_prefill<GG>), grid, dim3(256), 0, st, (const u32x4 *)q, (const u32x4 *)k, \
+                     (const u32x4 *)v, out, (int)p->out_mode, tokens, start, p->heads, p->kv_heads, p->capacity, scale_log2)
   if (G == 1) HWK_PF(1);
   else if (G == 2) HWK_PF(2);
   else HWK_PF(4);
