@@ -159,35 +159,56 @@ __device__ __forceinline__ float shifted_scale(uint32_t e, int s0) {
   return e == 255u ? __builtin_inff() : e == 0u ? 0.0f : v;
 }
 
-// The row shift s0 of weight row n: 0 when every finite, nonzero block exponent of the row is in
-// [-23, 13]; else the largest mapped to 13. Lanes q = 0..3 of a row scan a quarter of its scale bytes
-// each (dwords when the rows are dword-aligned) and combine by lane swaps.
-__device__ __forceinline__ int row_shift(const uint8_t *__restrict__ E, uint32_t n, uint32_t K, bool words, int q) {
-  const uint32_t nb = K / 32;
-  uint32_t hi = 0, lo = 255;
-  auto take = [&](uint32_t e) {
-    if (e != 0u && e != 255u) {
-      hi = max(hi, e);
-      lo = min(lo, e);
-    }
+// The row shifts s0 of the tile's BN weight rows (n0 .. n0+BN-1, clamped to N-1): 0 for a row whose
+// finite, nonzero block exponents are all in [-23, 13]; else the largest mapped to 13. The workgroup's
+// threads scan the rows' scale bytes (16-byte chunks when every row starts 16-byte aligned, all of a
+// thread's loads issued before any is used; bytes otherwise) and combine per row in LDS (hs: the
+// largest exponent byte other than 255, ls: the smallest other than 0 and 255). hs and ls are set
+// to 0 and 255 by the caller before a barrier; another barrier follows before they are read.
+template <int BN>
+__device__ __forceinline__ void scan_shifts(const uint8_t *__restrict__ E, uint32_t n0, uint32_t N, uint32_t nb,
+                                            bool quads, int t, int *hs, int *ls) {
+  auto take = [&](uint32_t e, uint32_t &h, uint32_t &l) {
+    h = max(h, e == 255u ? 0u : e);
+    l = min(l, (e == 0u || e == 255u) ? 255u : e);
   };
-  if (words) {
-    const uint32_t *row = (const uint32_t *)(E + (size_t)n * nb);
-    for (uint32_t w = q; w < nb / 4; w += 4) {
-      const uint32_t v = row[w];
+  if (quads) {
+    const uint32_t nch = nb / 16, total = BN * nch;
+    for (uint32_t base = 0; base < total; base += 4 * NT) {
+      u32x4 v[4];
 #pragma unroll
-      for (int b = 0; b < 4; b++) take((v >> (8 * b)) & 255u);
+      for (int i = 0; i < 4; i++) {
+        const uint32_t c = min(base + t + NT * i, total - 1), row = c / nch;
+        v[i] = *(const u32x4 *)(E + (size_t)min(n0 + row, N - 1) * nb + (c % nch) * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t c = base + t + NT * i;
+        if (c >= total) continue;
+        uint32_t h = 0, l = 255;
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+#pragma unroll
+          for (int b = 0; b < 4; b++) take((v[i][w] >> (8 * b)) & 255u, h, l);
+        atomicMax(&hs[c / nch], (int)h);
+        atomicMin(&ls[c / nch], (int)l);
+      }
     }
   } else {
-    for (uint32_t b = q; b < nb; b += 4) take(E[(size_t)n * nb + b]);
+    for (uint32_t c = t; c < BN * nb; c += NT) {
+      const uint32_t row = c / nb;
+      uint32_t h = 0, l = 255;
+      take(E[(size_t)min(n0 + row, N - 1) * nb + c % nb], h, l);
+      atomicMax(&hs[row], (int)h);
+      atomicMin(&ls[row], (int)l);
+    }
   }
-#pragma unroll
-  for (int off = 16; off < 64; off <<= 1) {
-    hi = max(hi, (uint32_t)__shfl_xor((int)hi, off, 64));
-    lo = min(lo, (uint32_t)__shfl_xor((int)lo, off, 64));
-  }
-  if (hi == 0u) return 0;  // no finite nonzero scale
-  const int emax = (int)hi - 127, emin = (int)lo - 127;
+}
+
+// The shift of a row from its scanned bytes.
+__device__ __forceinline__ int shift_of(int hi, int lo) {
+  if (hi == 0) return 0;  // no finite nonzero scale
+  const int emax = hi - 127, emin = lo - 127;
   return (emax <= 13 && emin >= -23) ? 0 : emax - 13;
 }
 
@@ -206,13 +227,14 @@ __device__ __forceinline__ void tile_of(uint32_t id, uint32_t mt, uint32_t nt, u
 }
 
 template <int BM, int BN, bool MX>
-__global__ __launch_bounds__(NT) void k_gemm(const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))) void k_gemm(const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
                                              const uint8_t *__restrict__ E, const uint16_t *__restrict__ S,
                                              void *__restrict__ Y, uint32_t M, uint32_t N, uint32_t K, int mode,
-                                             bool ewords) {
+                                             bool equads) {
   using C = Cfg<BM, BN, MX>;
   constexpr int TM = C::TM, TN = C::TN;
   __shared__ __attribute__((aligned(16))) u32x4 As[2][BM * CH];
+  __shared__ int hs[MX ? BN : 1], ls[MX ? BN : 1];  // the row shift scan (MXFP4)
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int r16 = lane & 15, q = lane >> 4;
@@ -234,7 +256,21 @@ __global__ __launch_bounds__(NT) void k_gemm(const u32x4 *__restrict__ X, const 
   }
   int s0[TN];
 #pragma unroll
-  for (int j = 0; j < TN; j++) s0[j] = MX ? row_shift(E, brow[j], K, ewords, q) : 0;
+  for (int j = 0; j < TN; j++) s0[j] = 0;
+  if constexpr (MX) {
+    if (t < BN) {
+      hs[t] = 0;
+      ls[t] = 255;
+    }
+    __syncthreads();
+    scan_shifts<BN>(E, n0, N, K / 32, equads, t, hs, ls);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const uint32_t r = brow[j] - n0;
+      s0[j] = shift_of(hs[r], ls[r]);
+    }
+  }
 
   floatx4 acc[TM][TN];
 #pragma unroll
@@ -265,9 +301,8 @@ __global__ __launch_bounds__(NT) void k_gemm(const u32x4 *__restrict__ X, const 
       float sc[TN];
 #pragma unroll
       for (int jn = 0; jn < TN; jn++) sc[jn] = MX ? shifted_scale(st[s].e[jn], s0[jn]) : 0.0f;
-#pragma unroll
-      for (int kk = 0; kk < KK; kk++) {
-        half8 af[TM], bf[TN];
+      // the operands of kk + 1 (X from LDS, weights converted) are fetched before the MFMAs of kk
+      auto operands = [&](half8 (&af)[TM], half8 (&bf)[TN], int kk) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
           const int row = wm * (BM / 2) + i * 16 + r16;
@@ -282,11 +317,17 @@ __global__ __launch_bounds__(NT) void k_gemm(const u32x4 *__restrict__ X, const 
             bf[jn] = i8x8_to_half8(v[(kk & 1) * 2], v[(kk & 1) * 2 + 1]);
           }
         }
+      };
+      half8 af[2][TM], bf[2][TN];
+      operands(af[0], bf[0], 0);
+#pragma unroll
+      for (int kk = 0; kk < KK; kk++) {
+        if (kk + 1 < KK) operands(af[(kk + 1) & 1], bf[(kk + 1) & 1], kk + 1);
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
           for (int jn = 0; jn < TN; jn++)
-            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
+            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[kk & 1][i], bf[kk & 1][jn], acc[i][jn], 0, 0, 0);
       }
       issue_order();
       load_w<BM, BN, MX>(st[s], W, E, K, kofs(j + NS), brow, q);
@@ -344,17 +385,17 @@ char *launch(hipStream_t st, const void *x, const void *w, const void *e, const 
   static const int cus = device_cus();
   const Shape sh = pick_shape(m, n, cus);
   const uint32_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn);
-  const bool ewords = MX && (k / 32) % 4 == 0 && hwk::aligned(e, 4);
+  const bool equads = MX && (k / 32) % 16 == 0 && hwk::aligned(e, 16);
   const dim3 grid(tiles), block(NT);
   const u32x4 *X = (const u32x4 *)x;
   const uint8_t *W = (const uint8_t *)w, *E = (const uint8_t *)e;
   const uint16_t *S = (const uint16_t *)s;
   if (sh.bm == 128 && sh.bn == 128)
-    hipLaunchKernelGGL((k_gemm<128, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, ewords);
+    hipLaunchKernelGGL((k_gemm<128, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
   else if (sh.bm == 128)
-    hipLaunchKernelGGL((k_gemm<128, 96, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, ewords);
+    hipLaunchKernelGGL((k_gemm<128, 96, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
   else
-    hipLaunchKernelGGL((k_gemm<64, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, ewords);
+    hipLaunchKernelGGL((k_gemm<64, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
   return hwk::launched(what);
 }
 
