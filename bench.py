@@ -1,6 +1,6 @@
 """Benchmark of the MI355X decode path (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|gemv|copy|gemm|attn|moe] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill|gemv|copy|floor|gemm|attn|moe] [--no-cpu]
 
 Prints one JSON line.
 
@@ -30,6 +30,8 @@ shortest time a single launch needs for them (roofline.read_floor carries its be
 The other configurations (each a graph of back-to-back launches over distinct input copies, timed
 with HIP events; the decode line carries them under "configs" without CPU baselines, and the
 workloads below print them with theirs):
+- prefill: the C5 prefill alone, the 1024-token prompt through the 28-layer model (median of K runs),
+  tokens/s and TFLOP/s against the fp16 MFMA peak (linears 2.886 TFLOP + causal attention 0.120).
 - gemm: the int8 weight-only prefill GEMM, M=512 K=2048 N=6144 (fp16 X, int8 W, fp16 per-row
   scale, fp16 Y): 12.88 GFLOP a launch, TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak; CPU:
   the oracle's shiftScale dequant (cached, as milcpu caches constants) + blocked fp32 sgemm on 64
@@ -416,6 +418,44 @@ def decode_rate(steps: int, warmup: int):
             "decode_tokens": total, "untimed": untimed, "timed_positions": [first, first + steps - 1]}
 
 
+# C5 prefill work (algorithmic): the linears 2 * 1024 * 1,409,286,144 FLOP and the causal attention
+# (QK^T and PV over the lower triangle: 4 * 128 * 16 heads * 1024 * 1025 / 2 FLOP a layer)
+PREFILL_LIN_FLOP = 2 * PROMPT * 1_409_286_144
+PREFILL_ATT_FLOP = C5["layers"] * 4 * 128 * C5["heads"] * PROMPT * (PROMPT + 1) // 2
+
+
+def prefill_rate(reps: int):
+    """The C5 prefill alone: the 1024-token prompt run `reps` times through the 28-layer model (each
+    run overwrites the cache positions 0..1023), each timed with HIP events."""
+    import numpy as np
+    import torch
+
+    from hwnpu_amd import synth
+    from hwnpu_amd.qwen3 import Qwen3
+
+    m = Qwen3(**C5, max_ctx=PROMPT + 8, max_prompt=PROMPT)
+    m.synth(seed=0, std=0.02)
+    prompt = synth.uniform_int(PROMPT, 0, C5["vocab"], "c5.prompt").cpu().numpy().astype(np.int32)
+    s = torch.cuda.current_stream()
+    m.prefill(prompt, 0)  # first use: code objects load outside the timed runs
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        m.prefill(prompt, 0)
+        b.record(s)
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    m.close()
+    ms = sorted(times)[len(times) // 2]
+    flop = PREFILL_LIN_FLOP + PREFILL_ATT_FLOP
+    return {"workload": "prefill", "tokens": PROMPT, "reps": reps, "ms_median": round(ms, 3),
+            "ms_all": [round(t, 3) for t in times], "tok_s": round(PROMPT / ms * 1e3, 1),
+            "tflops": round(flop / ms / 1e9, 1), "frac_mfma": round(flop / ms / 1e9 / MFMA_PEAK_TFLOPS, 4),
+            "flop": flop}
+
+
 def host_cpu():
     """The host's CPU model (/proc/cpuinfo) and the cores this process may use."""
     model = "unknown"
@@ -565,7 +605,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "gemv", "copy", "floor", "gemm", "attn", "moe"])
+                    choices=["decode", "prefill", "gemv", "copy", "floor", "gemm", "attn", "moe"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager", action="store_true", help="gemv/copy: launch one by one, no graph (counter runs)")
     ap.add_argument("--no-counters", action="store_true", help="decode: skip the rocprofv3 traffic runs")
@@ -602,6 +642,9 @@ def main():
         rows = [moe_rate(T) for T in (1, 5)]
         cpu = None if args.no_cpu else [moe_cpu(T) for T in (1, 5)]
         print(json.dumps({"workload": "moe", "results": rows, "cpu_baseline": cpu}))
+        return
+    if args.workload == "prefill":
+        print(json.dumps(prefill_rate(args.steps or 5)))
         return
     if args.workload == "floor":
         best, rows = read_floor()

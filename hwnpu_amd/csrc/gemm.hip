@@ -356,7 +356,7 @@ struct Shape {
   int bm, bn;
 };
 Shape pick_shape(uint32_t m, uint32_t n, int cus) {
-  const Shape cand[] = {{128, 128}, {128, 96}, {64, 128}};
+  const Shape cand[] = {{128, 128}, {128, 96}, {128, 64}, {64, 128}};
   Shape best = cand[0];
   double best_cost = 1e300;
   for (const Shape &s : cand) {
@@ -392,8 +392,10 @@ char *launch(hipStream_t st, const void *x, const void *w, const void *e, const 
   const uint16_t *S = (const uint16_t *)s;
   if (sh.bm == 128 && sh.bn == 128)
     hipLaunchKernelGGL((k_gemm<128, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
-  else if (sh.bm == 128)
+  else if (sh.bm == 128 && sh.bn == 96)
     hipLaunchKernelGGL((k_gemm<128, 96, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
+  else if (sh.bm == 128)
+    hipLaunchKernelGGL((k_gemm<128, 64, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
   else
     hipLaunchKernelGGL((k_gemm<64, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
   return hwk::launched(what);
