@@ -35,6 +35,7 @@ constexpr int CH = KS / 8;  // 16-byte chunks of an X row a step
 constexpr int KK = KS / 32;  // MFMAs a step for one (16-row, 16-column) tile
 constexpr int NS = 2;       // register stages: loads run NS steps ahead
 constexpr int NT = 256;     // threads a workgroup (2 x 2 waves)
+constexpr int kOutSwiGLU = HWK_OUT_SWIGLU_F16;
 
 // 4 int8 codes (one dword) as 4 exact fp16 values (two dwords).
 __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t w) {
@@ -335,6 +336,25 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))
     }
   }
   // D of tile (i, j): lane holds rows q*4 + r, column r16
+  if (mode == kOutSwiGLU) {
+    // columns (2c, 2c+1) are (gate, up) of output c: the even lane takes its odd neighbour's value.
+    // Every lane joins the swap; columns past N (a tile wider than N) store nothing, and with N % 16
+    // == 0 an even column below N has its partner below N too.
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const uint32_t n = nw + j * 16 + r16;
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const uint32_t m = m0 + wm * (BM / 2) + i * 16 + q * 4 + r;
+          const float v = MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * (float)__builtin_bit_cast(f16, S[min(n, N - 1)]);
+          const float up = __shfl_xor(v, 1, 64);
+          if ((n & 1) == 0 && n < N && m < M) ((f16 *)Y)[(size_t)m * (N / 2) + n / 2] = (f16)swiglu_value(v, up);
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < TN; j++) {
     const uint32_t n = nw + j * 16 + r16;
@@ -409,7 +429,8 @@ HWK_API char *hwk_i8_gemm(void *stream, const void *x, const void *q, const void
                           uint32_t n, uint32_t k, int out_mode) {
   HWK_CHECK(x && q && scale16 && y, "hwk_i8_gemm: null pointer");
   HWK_CHECK(k % 32 == 0 && k > 0, "hwk_i8_gemm: k=%u is not a positive multiple of 32", k);
-  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "hwk_i8_gemm: out_mode %d", out_mode);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_SWIGLU_F16, "hwk_i8_gemm: out_mode %d", out_mode);
+  HWK_CHECK(out_mode != HWK_OUT_SWIGLU_F16 || n % 16 == 0, "hwk_i8_gemm: SwiGLU output needs n %% 16 == 0 (n=%u)", n);
   HWK_CHECK(hwk::aligned(x, 16) && hwk::aligned(q, 16), "hwk_i8_gemm: x and q must be 16-byte aligned");
   if (m == 0 || n == 0) return nullptr;
   return launch<false>((hipStream_t)stream, x, q, nullptr, scale16, y, m, n, k, out_mode, "hwk_i8_gemm");
@@ -419,7 +440,8 @@ HWK_API char *hwk_mxfp4_gemm(void *stream, const void *x, const void *w, const v
                              uint32_t n, uint32_t k, int out_mode) {
   HWK_CHECK(x && w && e && y, "hwk_mxfp4_gemm: null pointer");
   HWK_CHECK(k % 32 == 0 && k > 0, "hwk_mxfp4_gemm: k=%u is not a positive multiple of 32", k);
-  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "hwk_mxfp4_gemm: out_mode %d", out_mode);
+  HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_SWIGLU_F16, "hwk_mxfp4_gemm: out_mode %d", out_mode);
+  HWK_CHECK(out_mode != HWK_OUT_SWIGLU_F16 || n % 16 == 0, "hwk_mxfp4_gemm: SwiGLU output needs n %% 16 == 0 (n=%u)", n);
   HWK_CHECK(hwk::aligned(x, 16) && hwk::aligned(w, 16), "hwk_mxfp4_gemm: x and w must be 16-byte aligned");
   if (m == 0 || n == 0) return nullptr;
   return launch<true>((hipStream_t)stream, x, w, e, nullptr, y, m, n, k, out_mode, "hwk_mxfp4_gemm");

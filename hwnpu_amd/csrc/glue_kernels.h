@@ -100,8 +100,7 @@ __global__ __launch_bounds__(256) void k_silu_mul(const float *__restrict__ g, c
 #pragma clang fp contract(off)
   const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
-  const float gv = g[i * stride], uv = u[i * stride];
-  const float y = f32_value(gv / (1.0f + (float)exp(-(double)gv)) * uv);
+  const float y = swiglu_value(g[i * stride], u[i * stride]);
   if (F16OUT)
     ((f16 *)out)[i] = (f16)y;
   else

@@ -122,6 +122,13 @@ __device__ __forceinline__ float f32_value(float v) {
   return v;
 }
 
+// SwiGLU of one (gate, up) pair: silu(g) * u with silu(g) = g / (1 + float(exp(-g))), exp in float64,
+// each step rounded to float32 on its own (the reference's SiLU, internal/llm/blocks/blocks.go:395-401).
+__device__ __forceinline__ float swiglu_value(float g, float u) {
+#pragma clang fp contract(off)
+  return f32_value(g / (1.0f + (float)exp(-(double)g)) * u);
+}
+
 // A scheduling barrier: the instruction scheduler moves nothing across it, so loads written before
 // it are issued before those written after it (no wait is implied: the wait counter still waits
 // only where a value is used).

@@ -415,11 +415,7 @@ char *prefill_piece(hwk_qwen3 *m, hipStream_t st, uint32_t T, uint32_t start, bo
     HWK_Q(hwk_attn_prefill(st, m->q16, ly.kc, ly.vc, m->att16, T, start, &pp));
     HWK_Q(hwk_mxfp4_gemm(st, m->att16, ly.o.w, ly.o.e, m->h, T, c.hidden, m->att_n, HWK_OUT_ADD_F32));
     HWK_Q(hwk::rmsnorm_f16(st, m->h, ly.post_norm, m->eps, m->x16, T, c.hidden));
-    HWK_Q(hwk_mxfp4_gemm(st, m->x16, ly.gu.w, ly.gu.e, m->gu, T, 2 * c.inter, c.hidden, HWK_OUT_F32));
-    const uint64_t n = (uint64_t)T * c.inter;
-    hipLaunchKernelGGL(k_silu_mul<true>, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, m->gu, m->gu + 1, m->a16, n,
-                       2u);
-    HWK_Q(hwk::launched("qwen3 swiglu"));
+    HWK_Q(hwk_mxfp4_gemm(st, m->x16, ly.gu.w, ly.gu.e, m->a16, T, 2 * c.inter, c.hidden, HWK_OUT_SWIGLU_F16));
     HWK_Q(hwk_mxfp4_gemm(st, m->a16, ly.down.w, ly.down.e, m->h, T, c.hidden, c.inter, HWK_OUT_ADD_F32));
   }
   if (!last_piece) return nullptr;

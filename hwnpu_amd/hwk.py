@@ -24,7 +24,7 @@ BUF_MIRRORED, BUF_DEVICE = 0, 1
 SYNC_TO_DEVICE, SYNC_FROM_DEVICE = 0, 1
 INFO_NAME, INFO_ARCH, INFO_PCI_BUS, INFO_CUS, INFO_MEM_BYTES = 0, 1, 2, 3, 4
 STATE_DONE, STATE_PENDING = 0, 1
-OUT_F32, OUT_F16, OUT_ADD_F32 = 0, 1, 2
+OUT_F32, OUT_F16, OUT_ADD_F32, OUT_SWIGLU_F16 = 0, 1, 2, 3
 ATTN_SCRATCH_BYTES = 4 << 20  # HWK_ATTN_SCRATCH_BYTES
 
 

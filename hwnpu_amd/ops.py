@@ -13,7 +13,7 @@ import torch
 
 from . import hwk
 
-OUT_MODES = {"f32": hwk.OUT_F32, "f16": hwk.OUT_F16, "add": hwk.OUT_ADD_F32}
+OUT_MODES = {"f32": hwk.OUT_F32, "f16": hwk.OUT_F16, "add": hwk.OUT_ADD_F32, "swiglu": hwk.OUT_SWIGLU_F16}
 
 
 def f32_bits(v: float) -> int:
@@ -120,7 +120,9 @@ def f16_gemv_rows(w, x, out_mode="f32", y=None):
 
 
 def _out2(y, m, n, mode, device):
-    dt = torch.float16 if mode == "f16" else torch.float32
+    dt = torch.float16 if mode in ("f16", "swiglu") else torch.float32
+    if mode == "swiglu":
+        n //= 2
     if y is None:
         if mode == "add":
             raise ValueError("out_mode 'add' needs y")
@@ -130,7 +132,8 @@ def _out2(y, m, n, mode, device):
 
 
 def i8_gemm(x, q, scale16, out_mode="f32", y=None):
-    """Y (m, n) = X W^T for fp16 X (m, k) and int8 W (n, k) with fp16 per-row scales."""
+    """Y (m, n) = X W^T for fp16 X (m, k) and int8 W (n, k) with fp16 per-row scales; out_mode "swiglu":
+    Y (m, n/2) fp16, the SwiGLU of the column pairs."""
     m, k = x.shape
     n = q.shape[0]
     _need(x, "x", torch.float16, (m, k))
@@ -143,7 +146,8 @@ def i8_gemm(x, q, scale16, out_mode="f32", y=None):
 
 
 def mxfp4_gemm(x, w, e, out_mode="f32", y=None):
-    """Y (m, n) = X W^T for fp16 X (m, k) and MXFP4 W: codes w (n, k/2), scales e (n, k/32)."""
+    """Y (m, n) = X W^T for fp16 X (m, k) and MXFP4 W: codes w (n, k/2), scales e (n, k/32); out_mode
+    "swiglu": Y (m, n/2) fp16, the SwiGLU of the column pairs."""
     m, k = x.shape
     n = w.shape[0]
     _need(x, "x", torch.float16, (m, k))

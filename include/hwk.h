@@ -51,8 +51,11 @@ enum { HWK_INFO_NAME = 0, HWK_INFO_ARCH = 1, HWK_INFO_PCI_BUS = 2, HWK_INFO_CUS 
 enum { HWK_STATE_DONE = 0, HWK_STATE_PENDING = 1 };
 
 /* Output modes of the GEMV/GEMM ops: fp32 or fp16 (RNE of the fp32 accumulator), or the fp32
- * result added into y (y += W x), for a residual stream. */
-enum { HWK_OUT_F32 = 0, HWK_OUT_F16 = 1, HWK_OUT_ADD_F32 = 2 };
+ * result added into y (y += W x), for a residual stream. HWK_OUT_SWIGLU_F16 (the GEMMs only): y is
+ * (m, n/2) fp16 with y[:, c] = fp16(silu(g) * u) of the fp32 result's column pairs (g, u) = (2c, 2c+1),
+ * silu as hwk_silu_mul's (internal/llm/blocks/blocks.go:395-401), n a multiple of 16: a gate/up
+ * projection with interleaved rows and its SwiGLU in one launch. */
+enum { HWK_OUT_F32 = 0, HWK_OUT_F16 = 1, HWK_OUT_ADD_F32 = 2, HWK_OUT_SWIGLU_F16 = 3 };
 
 HWK_API int hwk_abi(void);
 HWK_API void hwk_free_error(char *err);
@@ -188,7 +191,8 @@ HWK_API char *hwk_i8_gemm(void *stream, const void *x, const void *q, const void
                           uint32_t n, uint32_t k, int out_mode);
 /* MXFP4 W (n, k): codes (n, k/32, 16), scales (n, k/32) (replaces mxfp4.Dequantize + sgemm,
  * internal/mxfp4/mxfp4.go:120-128 with internal/sgemm/sgemm.go:127-163). The block scale is folded
- * into the fp16 dequantization: exact for e8m0 exponents in [-23, 13]. */
+ * into the fp16 dequantization; a row whose finite block exponents leave [-23, 13] is shifted by a
+ * power of two and scaled back in fp32, exact while its exponents span at most 36. */
 HWK_API char *hwk_mxfp4_gemm(void *stream, const void *x, const void *w, const void *e, void *y, uint32_t m,
                              uint32_t n, uint32_t k, int out_mode);
 

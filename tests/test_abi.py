@@ -145,3 +145,15 @@ def test_rope_tables_on_host_match_oracle():
     assert np.all(c[0] == 1) and np.all(s[0] == 0)
     with pytest.raises(hwk.HwkError, match="theta"):
         hwk.load().hwk_rope_tables(ops.f64_bits(0.5), 0, 1, d, c.ctypes.data, s.ctypes.data)
+
+
+def test_gemm_rejects_bad_out_modes():
+    L = hwk.load()
+    with pytest.raises(hwk.HwkError, match="SwiGLU output needs n % 16"):
+        L.hwk_mxfp4_gemm(None, FAKE, FAKE, FAKE, FAKE, 4, 24, 64, hwk.OUT_SWIGLU_F16)
+    with pytest.raises(hwk.HwkError, match="SwiGLU output needs n % 16"):
+        L.hwk_i8_gemm(None, FAKE, FAKE, FAKE, FAKE, 4, 40, 64, hwk.OUT_SWIGLU_F16)
+    with pytest.raises(hwk.HwkError, match="out_mode 4"):
+        L.hwk_mxfp4_gemm(None, FAKE, FAKE, FAKE, FAKE, 4, 32, 64, 4)
+    with pytest.raises(hwk.HwkError, match="out_mode"):  # the GEMVs have no SwiGLU output
+        L.hwk_mxfp4_gemv(None, FAKE, FAKE, FAKE, FAKE, 32, 64, hwk.OUT_SWIGLU_F16)

@@ -98,3 +98,34 @@ def test_mxfp4_gemm_edge_exponents(dev, orc):
         col_rms = rms(want[:, j])
         err = float(np.max(np.abs(got[:, j].astype(np.float64) - want[:, j])))
         assert err <= TOL * col_rms, f"column {j}: max|d|={err:.4g} rms={col_rms:.4g}"
+
+
+@pytest.mark.parametrize("kind,m,n,k", [("mx", 1024, 3072, 2048), ("mx", 33, 96, 256), ("mx", 5, 512, 6144),
+                                        ("i8", 200, 1536, 2048), ("i8", 7, 32, 96)])
+def test_gemm_swiglu_output(dev, kind, m, n, k):
+    """out_mode "swiglu" (the prompt's gate/up projection with its SwiGLU in the epilogue) equals the
+    fp32 output followed by hwk_silu_mul over the column pairs (g, u) = (2c, 2c+1), bit for bit; both
+    of those are pinned to the oracle on their own (the parity tests above, test_glue_gpu)."""
+    print(f"gemm swiglu {kind} m={m} n={n} k={k}", flush=True)
+    name = f"k3sw.{kind}.{m}.{n}.{k}"
+    x = synth.normal(m * k, name + ".x").view(m, k)
+    if kind == "mx":
+        w, e = synth.mxfp4_normal(n, k, name + ".w", std=0.02)
+        run = lambda mode: ops.mxfp4_gemm(x, w, e, mode)  # noqa: E731
+    else:
+        q = synth.uniform_int(n * k, -127, 255, name + ".q", dtype=torch.int8).view(n, k)
+        s = synth.uniform_real(n, 0.002, 0.02, name + ".s")
+        run = lambda mode: ops.i8_gemm(x, q, s, mode)  # noqa: E731
+    y32 = run("f32")
+    flat = y32.view(-1)
+    want = ops.silu_mul(flat, flat[1:], "f16", stride=2, n=m * n // 2).view(m, n // 2)
+    got = run("swiglu")
+    assert got.shape == (m, n // 2) and got.dtype == torch.float16
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_gemm_swiglu_rejects_ragged_n(dev):
+    x = synth.normal(4 * 64, "k3swr.x").view(4, 64)
+    w, e = synth.mxfp4_normal(24, 64, "k3swr.w", std=0.02)
+    with pytest.raises(Exception, match="SwiGLU"):
+        ops.mxfp4_gemm(x, w, e, "swiglu")
