@@ -337,21 +337,27 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))
   }
   // D of tile (i, j): lane holds rows q*4 + r, column r16
   if (mode == kOutSwiGLU) {
-    // columns (2c, 2c+1) are (gate, up) of output c: the even lane takes its odd neighbour's value.
-    // Every lane joins the swap; columns past N (a tile wider than N) store nothing, and with N % 16
-    // == 0 an even column below N has its partner below N too.
+    // columns (2c, 2c+1) are (gate, up) of output c, held by lanes r16 and r16 ^ 1 for the same four
+    // rows: the gate lane takes the up values of rows 0, 1 and computes those outputs, the up lane
+    // takes the gate values of rows 2, 3 and computes those. Every lane joins the swaps; columns past
+    // N (a tile wider than N) store nothing, and with N % 16 == 0 a pair is wholly below N or not.
+    const bool gate = (r16 & 1) == 0;
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-      const uint32_t n = nw + j * 16 + r16;
+      const uint32_t n = nw + j * 16 + r16, c = n / 2;
+      const float sc = MX ? 1.0f : (float)__builtin_bit_cast(f16, S[min(n, N - 1)]);
 #pragma unroll
-      for (int i = 0; i < TM; i++)
+      for (int i = 0; i < TM; i++) {
+        float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const uint32_t m = m0 + wm * (BM / 2) + i * 16 + q * 4 + r;
-          const float v = MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * (float)__builtin_bit_cast(f16, S[min(n, N - 1)]);
-          const float up = __shfl_xor(v, 1, 64);
-          if ((n & 1) == 0 && n < N && m < M) ((f16 *)Y)[(size_t)m * (N / 2) + n / 2] = (f16)swiglu_value(v, up);
-        }
+        for (int r = 0; r < 4; r++) v[r] = MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc;
+        const float o0 = __shfl_xor(gate ? v[2] : v[0], 1, 64), o1 = __shfl_xor(gate ? v[3] : v[1], 1, 64);
+        const uint32_t mr = m0 + wm * (BM / 2) + i * 16 + q * 4 + (gate ? 0 : 2);  // the lane's first row
+        const float y0 = gate ? swiglu_value(v[0], o0) : swiglu_value(o0, v[2]);
+        const float y1 = gate ? swiglu_value(v[1], o1) : swiglu_value(o1, v[3]);
+        if (n < N && mr < M) ((f16 *)Y)[(size_t)mr * (N / 2) + c] = (f16)y0;
+        if (n < N && mr + 1 < M) ((f16 *)Y)[(size_t)(mr + 1) * (N / 2) + c] = (f16)y1;
+      }
     }
     return;
   }
