@@ -568,6 +568,44 @@ __global__ __launch_bounds__(256) void k_attn_merge_fast(const float *__restrict
   }
 }
 
+// The merge of hwk_attn_decode's partials with one wave a (query head, 16 dims), for at most 4*U
+// chunks: lane = (dim lane % 16, chunk group lane / 16), group g takes chunks g, g+4, ..., all its
+// loads (o, m, l) issued at once; the reference's Merge rule (paged.go:252-310) as k_attn_merge_fast:
+// top = the largest m among chunks with l > 0, w = exp(m - top), out = sum(w o) / sum(w l), a chunk
+// with w = 0 (l <= 0) adding nothing (its o is never multiplied); the sums reduced over the four
+// groups by permlane swaps. No LDS, no barrier.
+template <int U>
+__global__ __launch_bounds__(64) void k_attn_merge_wave(const float *__restrict__ o, const float *__restrict__ m,
+                                                        const float *__restrict__ l, void *__restrict__ out,
+                                                        uint32_t chunks, uint32_t G, int mode) {
+  const uint32_t row = blockIdx.x, lane = threadIdx.x, g = lane >> 4;
+  const uint32_t d = blockIdx.y * 16 + (lane & 15);
+  const size_t base = (size_t)(row / G) * chunks * G + row % G;  // slot of chunk c: base + c*G
+  float ov[U], mv[U], lv[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const size_t slot = base + (size_t)min(g + 4 * u, chunks - 1) * G;
+    ov[u] = o[slot * 128 + d];
+    mv[u] = m[slot];
+    lv[u] = l[slot];
+  }
+  float top = -__builtin_inff();
+#pragma unroll
+  for (int u = 0; u < U; u++)
+    if (g + 4 * u < chunks && lv[u] > 0.0f) top = fmaxf(top, mv[u]);
+  top = row_groups_max(top);
+  float den = 0.0f, num = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const float w = (g + 4 * u < chunks && lv[u] > 0.0f && top != -__builtin_inff()) ? expf(mv[u] - top) : 0.0f;
+    den += w * lv[u];
+    num += w > 0.0f ? w * ov[u] : 0.0f;
+  }
+  den = row_groups_sum(den);
+  num = row_groups_sum(num);
+  if (g == 0) store_out(out, (size_t)row * 128 + d, den > 0.0f ? num / den : 0.0f, mode);
+}
+
 // One wave a row of head_dim (<= 512) fp16 values: absmax over the row, scale rounded to fp16,
 // codes rounded to even against that scale.
 __global__ void k_kv_quantize_i8(const f16 *__restrict__ x, int8_t *__restrict__ q, f16 *__restrict__ scale,
@@ -691,8 +729,13 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
 #undef HWK_ATTN_LAUNCH
   if (char *err = hwk::launched("hwk_attn_decode")) return err;
   if (nchunk == 1) return nullptr;
-  if (nchunk <= 4 * 16)
-    hipLaunchKernelGGL((k_attn_merge_fast<16>), dim3(p->heads, 2), dim3(256), 0, st, ws_o, ws_m, ws_l, out, nchunk, G, mode);
+  const dim3 mgrid(p->heads, 8);
+  if (nchunk <= 4 * 4)
+    hipLaunchKernelGGL((k_attn_merge_wave<4>), mgrid, dim3(64), 0, st, ws_o, ws_m, ws_l, out, nchunk, G, mode);
+  else if (nchunk <= 4 * 8)
+    hipLaunchKernelGGL((k_attn_merge_wave<8>), mgrid, dim3(64), 0, st, ws_o, ws_m, ws_l, out, nchunk, G, mode);
+  else if (nchunk <= 4 * 16)
+    hipLaunchKernelGGL((k_attn_merge_wave<16>), mgrid, dim3(64), 0, st, ws_o, ws_m, ws_l, out, nchunk, G, mode);
   else
     hipLaunchKernelGGL((k_attn_merge_fast<32>), dim3(p->heads, 2), dim3(256), 0, st, ws_o, ws_m, ws_l, out, nchunk, G, mode);
   return hwk::launched("hwk_attn_decode (merge)");
