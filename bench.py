@@ -1,6 +1,6 @@
 """Benchmark of the MI355X decode path (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill|gemv|copy|floor|gemm|attn|moe] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill|gemv|gemv_i8|gemv_rows|copy|floor|gemm|attn|moe] [--no-cpu]
 
 Prints one JSON line.
 
@@ -32,6 +32,8 @@ with HIP events; the decode line carries them under "configs" without CPU baseli
 workloads below print them with theirs):
 - prefill: the C5 prefill alone, the 1024-token prompt through the 28-layer model (median of K runs),
   tokens/s and TFLOP/s against the fp16 MFMA peak (linears 2.886 TFLOP + causal attention 0.120).
+- gemv_i8: K2, the int8 GEMV 8192 x 2048 with fp16 row scales (16,814,080 B), 64 copies; gemv_rows:
+  K1r, C1's MXFP4 matrix times T = 1, 2, 4, 8 fp16 vectors (the verify form), the matrix read once.
 - gemm: the int8 weight-only prefill GEMM, M=512 K=2048 N=6144 (fp16 X, int8 W, fp16 per-row
   scale, fp16 Y): 12.88 GFLOP a launch, TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak; CPU:
   the oracle's shiftScale dequant (cached, as milcpu caches constants) + blocked fp32 sgemm on 64
@@ -126,6 +128,52 @@ def gemv_roofline(steps: int, warmup: int, eager: bool = False):
 
     us, launches, wall = _graph_time(launch_all, steps, warmup, eager)
     return {"us": us, "launches": launches, "wall_s": wall, "gbs": GEMV_BYTES / (us * 1e-6) / 1e9}
+
+
+# K2, the int8 GEMV on C1's shape (SURVEY's "C1 int8 GEMV"): codes + fp16 row scales + x + fp16 y
+GEMV_I8_BYTES = GEMV_N * GEMV_K + GEMV_N * 2 + GEMV_K * 2 + GEMV_N * 2
+
+
+def gemv_i8_rate(steps: int = 1280, warmup: int = 128):
+    """K2 (hwk_i8_gemv) on 8192 x 2048 int8 rows with fp16 scales, 64 distinct copies in a graph."""
+    import torch
+
+    from hwnpu_amd import ops, synth
+
+    ws = [(synth.uniform_int(GEMV_N * GEMV_K, -127, 255, f"bench.k2.q{i}", dtype=torch.int8).view(GEMV_N, GEMV_K),
+           synth.uniform_real(GEMV_N, 0.002, 0.02, f"bench.k2.s{i}")) for i in range(COPIES)]
+    x = synth.normal(GEMV_K, "bench.k2.x", dtype=torch.float16)
+    y = torch.empty(GEMV_N, dtype=torch.float16, device="cuda")
+
+    def launch_all():
+        for q, s in ws:
+            ops.i8_gemv(q, s, x, "f16", y=y)
+
+    us, launches, _ = _graph_time(launch_all, steps, warmup)
+    gbs = GEMV_I8_BYTES / (us * 1e-6) / 1e9
+    return {"config": "int8 GEMV 8192x2048, fp16 scales, fp16 x and y", "us": round(us, 3),
+            "bytes": GEMV_I8_BYTES, "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def gemv_rows_rate(T: int, steps: int = 640, warmup: int = 64):
+    """K1r (hwk_mxfp4_gemv_rows): C1's MXFP4 matrix times T fp16 vectors (the verify step's form),
+    each weight row read once for all T; 64 distinct matrices in a graph."""
+    import torch
+
+    from hwnpu_amd import ops, synth
+
+    ws = [synth.mxfp4_uniform(GEMV_N, GEMV_K, f"bench.c1.{i}") for i in range(COPIES)]
+    x = synth.normal(T * GEMV_K, f"bench.k1r.x{T}", dtype=torch.float16).view(T, GEMV_K)
+    y = torch.empty((T, GEMV_N), dtype=torch.float16, device="cuda")
+
+    def launch_all():
+        for w, e in ws:
+            ops.mxfp4_gemv_rows(w, e, x, "f16", y=y)
+
+    us, _, _ = _graph_time(launch_all, steps, warmup)
+    nbytes = GEMV_N * GEMV_K // 2 + GEMV_N * GEMV_K // 32 + T * (GEMV_K * 2 + GEMV_N * 2)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"T": T, "us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 FLOOR_SHAPES = [(wpc, lpl) for wpc in (8, 16, 32) for lpl in (1, 2, 4)]
@@ -605,7 +653,8 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "prefill", "gemv", "copy", "floor", "gemm", "attn", "moe"])
+                    choices=["decode", "prefill", "gemv", "gemv_i8", "gemv_rows", "copy", "floor", "gemm", "attn",
+                             "moe"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager", action="store_true", help="gemv/copy: launch one by one, no graph (counter runs)")
     ap.add_argument("--no-counters", action="store_true", help="decode: skip the rocprofv3 traffic runs")
@@ -646,6 +695,12 @@ def main():
     if args.workload == "prefill":
         print(json.dumps(prefill_rate(args.steps or 5)))
         return
+    if args.workload == "gemv_i8":
+        print(json.dumps(dict(gemv_i8_rate(), workload="gemv_i8")))
+        return
+    if args.workload == "gemv_rows":
+        print(json.dumps({"workload": "gemv_rows", "results": [gemv_rows_rate(T) for T in (1, 2, 4, 8)]}))
+        return
     if args.workload == "floor":
         best, rows = read_floor()
         print(json.dumps({"workload": "floor", "bytes": GEMV_BYTES, "best": best, "sweep": rows}))
@@ -662,7 +717,9 @@ def main():
     floor, _ = read_floor(shapes=[(16, 1), (32, 1), (32, 2)])
     configs = {"c2_int8_gemm": gemm_rate(4),
                "c3_attention": [attn_rate(L, i8) for L in (2048, 32768) for i8 in (False, True)],
-               "c4_moe": [moe_rate(T, 2) for T in (1, 5)]}
+               "c4_moe": [moe_rate(T, 2) for T in (1, 5)],
+               "k2_i8_gemv": gemv_i8_rate(),
+               "k1r_gemv_rows": [gemv_rows_rate(T) for T in (2, 8)]}
     cpu = None
     if not args.no_cpu:
         cpu = cpu_decode_baseline()
