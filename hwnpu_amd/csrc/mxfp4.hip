@@ -474,6 +474,63 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_rows(const uint4 *__restrict
   }
 }
 
+// K1r on the matrix cores, for several vectors (T <= 8) and rows of a multiple of 16 blocks: a
+// workgroup of 4 waves takes 16 rows; wave w takes blocks round*64 + w*16 .. +15. Per block one
+// v_mfma_f32_16x16x32_f16 of the 16 rows' codes (A: lane (row l%16, group l/16) holds the block's
+// codes group*8 .. +7 as exact fp16 e2m1 values) with the T vectors (B: lane (vector l%16, group)
+// holds x[vector][block*32 + group*8 .. +7], zero past T) sums the block's 32 products per (row,
+// vector); each lane's four (row, vector) sums are scaled by the rows' e8m0 block scales in fp32 and
+// added in block order. All of a round's loads are issued before its first MFMA. The four waves'
+// sums meet in LDS and wave 0 adds them in wave order and stores.
+template <int TT>
+__global__ __launch_bounds__(256) void k_mxfp4_gemv_rows_mfma(const uint32_t *__restrict__ w,
+                                                              const uint8_t *__restrict__ e,
+                                                              const f16 *__restrict__ x, void *__restrict__ y,
+                                                              uint32_t n, uint32_t nb, int mode) {
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  typedef float floatx4 __attribute__((ext_vector_type(4)));
+  __shared__ floatx4 part[3][64];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int c16 = lane & 15, g = lane >> 4;
+  const uint32_t row0 = blockIdx.x * 16;
+  const uint32_t arow = min(row0 + c16, n - 1);                    // the A row of this lane
+  const uint32_t vec = min((uint32_t)c16, (uint32_t)TT - 1);      // the B vector of this lane
+  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};  // rows g*4 + r, vector c16
+  for (uint32_t b0 = (uint32_t)wave * 16; b0 < nb; b0 += 64) {
+    uint32_t cw[16];
+    u32x4 xv[16], sv[4];
+#pragma unroll
+    for (int j = 0; j < 16; j++) cw[j] = w[((size_t)arow * nb + b0 + j) * 4 + g];
+    if (c16 < TT) {  // lanes past the T vectors load nothing
+#pragma unroll
+      for (int j = 0; j < 16; j++) xv[j] = *(const u32x4 *)(x + (size_t)vec * nb * 32 + (b0 + j) * 32 + g * 8);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; j++) xv[j] = (u32x4){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) sv[r] = *(const u32x4 *)(e + (size_t)min(row0 + g * 4 + r, n - 1) * nb + b0);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const u32x4 a = {__builtin_bit_cast(uint32_t, fp4x2_to_h2<0>(cw[j])), __builtin_bit_cast(uint32_t, fp4x2_to_h2<1>(cw[j])),
+                       __builtin_bit_cast(uint32_t, fp4x2_to_h2<2>(cw[j])), __builtin_bit_cast(uint32_t, fp4x2_to_h2<3>(cw[j]))};
+      const floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, xv[j]),
+                                                               (floatx4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[r] += d[r] * e8m0_scale((sv[r][j / 4] >> (8 * (j % 4))) & 255u);
+    }
+  }
+  if (wave > 0) part[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave > 0 || c16 >= TT) return;
+  acc = ((acc + part[0][lane]) + part[1][lane]) + part[2][lane];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t row = row0 + g * 4 + r;
+    if (row < n) store_out(y, (size_t)c16 * n + row, acc[r], mode);
+  }
+}
+
 // ---- the encoder (reference internal/mxfp4/encode.go:11-78), one thread a block, in float64
 // with every product and sum rounded on its own, as the reference computes it ----
 
@@ -727,6 +784,11 @@ HWK_API char *hwk_mxfp4_gemv(void *stream, const void *w, const void *e, const v
   return hwk::launched("hwk_mxfp4_gemv");
 }
 
+// The fewest vectors K1r takes to the matrix cores (fewer: T dot products a lane on the VALUs, which
+// is faster up to T = 5 on C1's shape: 4.5 / 5.8 / 8.3 µs at T = 1 / 2 / 4 against 8.3-8.6 µs for the
+// MFMA form, whose time barely grows with T: 9.2 µs at T = 8 against 12.6).
+constexpr uint32_t kRowsMfmaMinTokens = 6;
+
 HWK_API char *hwk_mxfp4_gemv_rows(void *stream, const void *w, const void *e, const void *x, void *y, uint32_t n,
                                   uint32_t k, uint32_t tokens, int out_mode) {
   HWK_CHECK(w && e && x && y, "hwk_mxfp4_gemv_rows: null pointer");
@@ -738,12 +800,24 @@ HWK_API char *hwk_mxfp4_gemv_rows(void *stream, const void *w, const void *e, co
   HWK_CHECK(hwk::aligned(y, out_mode == HWK_OUT_F16 ? 2 : 4), "hwk_mxfp4_gemv_rows: y misaligned");
   if (n == 0) return nullptr;
   const uint32_t nb = k / 32;
+  hipStream_t st = (hipStream_t)stream;
+  if (tokens >= kRowsMfmaMinTokens && nb % 16 == 0 && hwk::aligned(e, 16)) {
+#define HWK_ROWS_M(T)                                                                                          \
+  hipLaunchKernelGGL((k_mxfp4_gemv_rows_mfma<T>), dim3((n + 15) / 16), dim3(256), 0, st, (const uint32_t *)w, \
+                     (const uint8_t *)e, (const f16 *)x, y, n, nb, out_mode)
+    switch (tokens) {
+      case 6: HWK_ROWS_M(6); break;
+      case 7: HWK_ROWS_M(7); break;
+      default: HWK_ROWS_M(8); break;
+    }
+#undef HWK_ROWS_M
+    return hwk::launched("hwk_mxfp4_gemv_rows");
+  }
   constexpr int RPW = 2;
   const uint32_t sets = (n + RPW - 1) / RPW;
   const uint32_t waves = sets < stream_waves() ? sets : stream_waves();
   const dim3 grid((waves + 3) / 4), block(256);
   const size_t lds = (size_t)tokens * k * 2;
-  hipStream_t st = (hipStream_t)stream;
 #define HWK_ROWS(B, T)                                                                                        \
   hipLaunchKernelGGL((k_mxfp4_gemv_rows<B, RPW, T>), grid, block, lds, st, (const uint4 *)w, (const uint8_t *)e, \
                      (const uint4 *)x, y, n, nb, out_mode)

@@ -194,8 +194,9 @@ def test_f16_gemv_rows_parity(dev, orc, T, n, k):
 
 # ---------------- K1r: several vectors, weights read once ----------------
 
+# (T >= 6 with k a multiple of 512: the matrix-core form; the rest: the VALU form)
 @pytest.mark.parametrize("T,n,k", [(5, 8192, 2048), (1, 300, 6144), (2, 33, 96), (8, 2048, 2048), (3, 7, 4128),
-                                   (5, 6144, 2048), (4, 2048, 6144)])
+                                   (5, 6144, 2048), (4, 2048, 6144), (6, 1000, 4096), (7, 33, 512), (8, 5, 2048)])
 def test_mxfp4_gemv_rows_parity(dev, orc, T, n, k):
     print(f"mxfp4_gemv_rows T={T} n={n} k={k}", flush=True)
     w, e = synth.mxfp4_uniform(n, k, f"k1r.{n}.{k}")
