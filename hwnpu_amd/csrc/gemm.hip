@@ -34,7 +34,6 @@ constexpr int KS = 128;     // K a step
 constexpr int CH = KS / 8;  // 16-byte chunks of an X row a step
 constexpr int KK = KS / 32;  // MFMAs a step for one (16-row, 16-column) tile
 constexpr int NS = 2;       // register stages: loads run NS steps ahead
-constexpr int NT = 256;     // threads a workgroup (2 x 2 waves)
 constexpr int kOutSwiGLU = HWK_OUT_SWIGLU_F16;
 
 // 4 int8 codes (one dword) as 4 exact fp16 values (two dwords).
@@ -73,19 +72,20 @@ __device__ __forceinline__ int xchunk(int q, int kk) {
   return kk < 2 ? 2 * q + kk : 8 + 2 * q + (kk - 2);
 }
 
-template <int BM, int BN, bool MX>
+template <int BM, int BN, bool MX, int WM, int WN>
 struct Cfg {
-  static constexpr int TM = BM / 2 / 16, TN = BN / 2 / 16;  // 16 x 16 tiles a wave
+  static constexpr int NT = 64 * WM * WN;                   // threads: WM x WN waves over the tile
+  static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16 x 16 tiles a wave
   static constexpr int AL = BM * CH / NT;                   // X chunks a thread stages a step
   static constexpr int BL = MX ? 1 : 2;                     // 16-byte weight loads a lane a step a tile
-  static_assert(BM * CH % NT == 0, "X chunks a thread");
+  static_assert(BM * CH % NT == 0 && TM * WM * 16 == BM && TN * WN * 16 == BN, "tile shape");
 };
 
-template <int BM, int BN, bool MX>
+template <int BM, int BN, bool MX, int WM, int WN>
 struct Stage {
-  u32x4 a[Cfg<BM, BN, MX>::AL];
-  u32x4 b[Cfg<BM, BN, MX>::TN][Cfg<BM, BN, MX>::BL];
-  uint32_t e[Cfg<BM, BN, MX>::TN];  // MXFP4 block scale bytes
+  u32x4 a[Cfg<BM, BN, MX, WM, WN>::AL];
+  u32x4 b[Cfg<BM, BN, MX, WM, WN>::TN][Cfg<BM, BN, MX, WM, WN>::BL];
+  uint32_t e[Cfg<BM, BN, MX, WM, WN>::TN];  // MXFP4 block scale bytes
   uint32_t k0;                      // the step's K offset
 };
 
@@ -94,24 +94,24 @@ struct Stage {
 // end reads in-range data, which zero_tail clears when the stage is consumed (a select here would wait
 // for the load at once). Every load is issued unconditionally (a load under a branch would be waited
 // for at the join).
-template <int BM, int BN, bool MX>
-__device__ __forceinline__ void load_x(Stage<BM, BN, MX> &s, const u32x4 *__restrict__ X, uint32_t M, uint32_t K,
+template <int BM, int BN, bool MX, int WM, int WN>
+__device__ __forceinline__ void load_x(Stage<BM, BN, MX, WM, WN> &s, const u32x4 *__restrict__ X, uint32_t M, uint32_t K,
                                        uint32_t m0, uint32_t k0, int t) {
-  using C = Cfg<BM, BN, MX>;
+  using C = Cfg<BM, BN, MX, WM, WN>;
   s.k0 = k0;
 #pragma unroll
   for (int i = 0; i < C::AL; i++) {
-    const int c = t + NT * i, row = c / CH, ch = c % CH;
+    const int c = t + C::NT * i, row = c / CH, ch = c % CH;
     const uint32_t m = min(m0 + row, M - 1);
     s.a[i] = X[((size_t)m * K + min(k0 + ch * 8, K - 8)) / 8];
   }
 }
 
-template <int BM, int BN, bool MX>
-__device__ __forceinline__ void load_w(Stage<BM, BN, MX> &s, const uint8_t *__restrict__ W,
+template <int BM, int BN, bool MX, int WM, int WN>
+__device__ __forceinline__ void load_w(Stage<BM, BN, MX, WM, WN> &s, const uint8_t *__restrict__ W,
                                        const uint8_t *__restrict__ E, uint32_t K, uint32_t k0,
-                                       const uint32_t (&brow)[Cfg<BM, BN, MX>::TN], int q) {
-  using C = Cfg<BM, BN, MX>;
+                                       const uint32_t (&brow)[Cfg<BM, BN, MX, WM, WN>::TN], int q) {
+  using C = Cfg<BM, BN, MX, WM, WN>;
   if constexpr (MX) {
     const uint32_t blk = min(k0 + q * 32, K - 32) / 32;
 #pragma unroll
@@ -131,13 +131,13 @@ __device__ __forceinline__ void load_w(Stage<BM, BN, MX> &s, const uint8_t *__re
 }
 
 // A step reaching past K: its X chunks and weight loads past K become zeros (MXFP4: scale 0).
-template <int BM, int BN, bool MX>
-__device__ __forceinline__ void zero_tail(Stage<BM, BN, MX> &s, uint32_t K, int t, int q) {
-  using C = Cfg<BM, BN, MX>;
+template <int BM, int BN, bool MX, int WM, int WN>
+__device__ __forceinline__ void zero_tail(Stage<BM, BN, MX, WM, WN> &s, uint32_t K, int t, int q) {
+  using C = Cfg<BM, BN, MX, WM, WN>;
   const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int i = 0; i < C::AL; i++)
-    if (s.k0 + ((t + NT * i) % CH) * 8 >= K) s.a[i] = zero;
+    if (s.k0 + ((t + C::NT * i) % CH) * 8 >= K) s.a[i] = zero;
 #pragma unroll
   for (int j = 0; j < C::TN; j++) {
     if constexpr (MX) {
@@ -166,7 +166,7 @@ __device__ __forceinline__ float shifted_scale(uint32_t e, int s0) {
 // thread's loads issued before any is used; bytes otherwise) and combine per row in LDS (hs: the
 // largest exponent byte other than 255, ls: the smallest other than 0 and 255). hs and ls are set
 // to 0 and 255 by the caller before a barrier; another barrier follows before they are read.
-template <int BN>
+template <int BN, int NT>
 __device__ __forceinline__ void scan_shifts(const uint8_t *__restrict__ E, uint32_t n0, uint32_t N, uint32_t nb,
                                             bool quads, int t, int *hs, int *ls) {
   auto take = [&](uint32_t e, uint32_t &h, uint32_t &l) {
@@ -227,33 +227,33 @@ __device__ __forceinline__ void tile_of(uint32_t id, uint32_t mt, uint32_t nt, u
   tm = lin % mt;
 }
 
-template <int BM, int BN, bool MX>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))) void k_gemm(const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
+template <int BM, int BN, bool MX, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MX && WM * WN == 4 ? 2 : 1))) void k_gemm(const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
                                              const uint8_t *__restrict__ E, const uint16_t *__restrict__ S,
                                              void *__restrict__ Y, uint32_t M, uint32_t N, uint32_t K, int mode,
                                              bool equads) {
-  using C = Cfg<BM, BN, MX>;
-  constexpr int TM = C::TM, TN = C::TN;
+  using C = Cfg<BM, BN, MX, WM, WN>;
+  constexpr int TM = C::TM, TN = C::TN, NT = C::NT;
   __shared__ __attribute__((aligned(16))) u32x4 As[2][BM * CH];
   __shared__ int hs[MX ? BN : 1], ls[MX ? BN : 1];  // the row shift scan (MXFP4)
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int r16 = lane & 15, q = lane >> 4;
   uint32_t tm, tn;
   tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
-  const uint32_t nw = n0 + wn * (BN / 2);  // the wave's first column
+  const uint32_t nw = n0 + wn * (BN / WN);  // the wave's first column
   uint32_t brow[TN];
 #pragma unroll
   for (int j = 0; j < TN; j++) brow[j] = min(nw + j * 16 + r16, N - 1);
 
   const uint32_t steps = (K + KS - 1) / KS;
   auto kofs = [&](uint32_t j) -> uint32_t { return min(j, steps) * KS; };  // past the end: reads zeros
-  Stage<BM, BN, MX> st[NS];
+  Stage<BM, BN, MX, WM, WN> st[NS];
 #pragma unroll
   for (int s = 0; s < NS; s++) {
-    load_x<BM, BN, MX>(st[s], X, M, K, m0, kofs(s), t);
-    load_w<BM, BN, MX>(st[s], W, E, K, kofs(s), brow, q);
+    load_x<BM, BN, MX, WM, WN>(st[s], X, M, K, m0, kofs(s), t);
+    load_w<BM, BN, MX, WM, WN>(st[s], W, E, K, kofs(s), brow, q);
   }
   int s0[TN];
 #pragma unroll
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))
       ls[t] = 255;
     }
     __syncthreads();
-    scan_shifts<BN>(E, n0, N, K / 32, equads, t, hs, ls);
+    scan_shifts<BN, NT>(E, n0, N, K / 32, equads, t, hs, ls);
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < TN; j++) {
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))
     for (int s = 0; s < NS; s++) {
       const uint32_t j = j0 + s;
       u32x4 *buf = As[s & 1];  // NS is even: step j uses buffer j & 1
-      if (st[s].k0 + KS > K) zero_tail<BM, BN, MX>(st[s], K, t, q);  // uniform: only a ragged step
+      if (st[s].k0 + KS > K) zero_tail<BM, BN, MX, WM, WN>(st[s], K, t, q);  // uniform: only a ragged step
 #pragma unroll
       for (int i = 0; i < C::AL; i++) {
         const int c = t + NT * i, row = c / CH, ch = c % CH;
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))
       }
       __syncthreads();
       issue_order();
-      load_x<BM, BN, MX>(st[s], X, M, K, m0, kofs(j + NS), t);
+      load_x<BM, BN, MX, WM, WN>(st[s], X, M, K, m0, kofs(j + NS), t);
       issue_order();
       float sc[TN];
 #pragma unroll
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))
       auto operands = [&](half8 (&af)[TM], half8 (&bf)[TN], int kk) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-          const int row = wm * (BM / 2) + i * 16 + r16;
+          const int row = wm * (BM / WM) + i * 16 + r16;
           af[i] = __builtin_bit_cast(half8, buf[row * CH + (xchunk<MX>(q, kk) ^ (row & 15))]);
         }
 #pragma unroll
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))
             acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[kk & 1][i], bf[kk & 1][jn], acc[i][jn], 0, 0, 0);
       }
       issue_order();
-      load_w<BM, BN, MX>(st[s], W, E, K, kofs(j + NS), brow, q);
+      load_w<BM, BN, MX, WM, WN>(st[s], W, E, K, kofs(j + NS), brow, q);
       issue_order();
     }
   }
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))
 #pragma unroll
         for (int r = 0; r < 4; r++) v[r] = MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc;
         const float o0 = __shfl_xor(gate ? v[2] : v[0], 1, 64), o1 = __shfl_xor(gate ? v[3] : v[1], 1, 64);
-        const uint32_t mr = m0 + wm * (BM / 2) + i * 16 + q * 4 + (gate ? 0 : 2);  // the lane's first row
+        const uint32_t mr = m0 + wm * (BM / WM) + i * 16 + q * 4 + (gate ? 0 : 2);  // the lane's first row
         const float y0 = gate ? swiglu_value(v[0], o0) : swiglu_value(o0, v[2]);
         const float y1 = gate ? swiglu_value(v[1], o1) : swiglu_value(o1, v[3]);
         if (n < N && mr < M) ((f16 *)Y)[(size_t)mr * (N / 2) + c] = (f16)y0;
@@ -370,25 +370,30 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(MX ? 2 : 1))
     for (int i = 0; i < TM; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const uint32_t m = m0 + wm * (BM / 2) + i * 16 + q * 4 + r;
+        const uint32_t m = m0 + wm * (BM / WM) + i * 16 + q * 4 + r;
         if (m < M) store_out(Y, (size_t)m * N + n, MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc, mode);
       }
   }
 }
 
 // The tile shape for (m, n): the fewest rounds of workgroups over the CUs, a round weighted by the
-// tile's work and its per-tile overheads (larger tiles reuse their loads more).
+// tile's work and its per-tile overheads (larger tiles reuse their loads more). When every tile
+// gets a CU of its own, 8 waves (2 x 4, two a SIMD: one computes while the other waits) beat 4 by
+// 5-12 % on the prompt's shapes; with several tiles a CU, 4-wave workgroups fill the SIMDs as well.
 struct Shape {
-  int bm, bn;
+  int bm, bn, wm, wn;  // tile, waves over its rows and columns
 };
+constexpr Shape kShapes[] = {{128, 128, 2, 2}, {128, 96, 2, 2}, {128, 64, 2, 2}, {64, 128, 2, 2},
+                             {128, 128, 2, 4}, {128, 64, 2, 4}};
 Shape pick_shape(uint32_t m, uint32_t n, int cus) {
-  const Shape cand[] = {{128, 128}, {128, 96}, {128, 64}, {64, 128}};
-  Shape best = cand[0];
+  Shape best = kShapes[0];
   double best_cost = 1e300;
-  for (const Shape &s : cand) {
+  for (const Shape &s : kShapes) {
     const uint64_t tiles = (uint64_t)((m + s.bm - 1) / s.bm) * ((n + s.bn - 1) / s.bn);
     const uint64_t rounds = (tiles + cus - 1) / cus;
-    const double cost = (double)rounds * s.bm * s.bn * (1.0 + 32.0 / s.bm + 32.0 / s.bn);
+    const bool eight = s.wm * s.wn == 8;
+    if (eight && tiles > (uint64_t)cus) continue;
+    const double cost = (double)rounds * s.bm * s.bn * (1.0 + 32.0 / s.bm + 32.0 / s.bn) * (eight ? 0.75 : 1.0);
     if (cost < best_cost) {
       best_cost = cost;
       best = s;
@@ -412,18 +417,23 @@ char *launch(hipStream_t st, const void *x, const void *w, const void *e, const 
   const Shape sh = pick_shape(m, n, cus);
   const uint32_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn);
   const bool equads = MX && (k / 32) % 16 == 0 && hwk::aligned(e, 16);
-  const dim3 grid(tiles), block(NT);
+  const dim3 grid(tiles);
   const u32x4 *X = (const u32x4 *)x;
   const uint8_t *W = (const uint8_t *)w, *E = (const uint8_t *)e;
   const uint16_t *S = (const uint16_t *)s;
-  if (sh.bm == 128 && sh.bn == 128)
-    hipLaunchKernelGGL((k_gemm<128, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
-  else if (sh.bm == 128 && sh.bn == 96)
-    hipLaunchKernelGGL((k_gemm<128, 96, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
-  else if (sh.bm == 128)
-    hipLaunchKernelGGL((k_gemm<128, 64, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
+#define HWK_GEMM_IF(BMv, BNv, WMv, WNv)                                                                          \
+  if (sh.bm == BMv && sh.bn == BNv && sh.wm == WMv && sh.wn == WNv)                                               \
+    hipLaunchKernelGGL((k_gemm<BMv, BNv, MX, WMv, WNv>), grid, dim3(64 * WMv * WNv), 0, st, X, W, E, S, y, m, n, k, \
+                       mode, equads);                                                                             \
   else
-    hipLaunchKernelGGL((k_gemm<64, 128, MX>), grid, block, 0, st, X, W, E, S, y, m, n, k, mode, equads);
+  HWK_GEMM_IF(128, 128, 2, 2)
+  HWK_GEMM_IF(128, 96, 2, 2)
+  HWK_GEMM_IF(128, 64, 2, 2)
+  HWK_GEMM_IF(64, 128, 2, 2)
+  HWK_GEMM_IF(128, 128, 2, 4)
+  HWK_GEMM_IF(128, 64, 2, 4)
+  HWK_CHECK(false, "%s: no kernel for the %dx%d tile", what, sh.bm, sh.bn);
+#undef HWK_GEMM_IF
   return hwk::launched(what);
 }
 
