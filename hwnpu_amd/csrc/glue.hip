@@ -102,10 +102,9 @@ HWK_API char *hwk_rmsnorm(void *stream, const void *x, const void *w, void *out,
   if (rows == 0) return nullptr;
   hipStream_t st = (hipStream_t)stream;
   if (out_mode == HWK_OUT_F16)
-    hipLaunchKernelGGL(k_rmsnorm<true>, dim3(rows), dim3(256), 0, st, (const float *)x, (const float *)w, eps, out, n);
+    launch_rmsnorm<true>(st, (const float *)x, (const float *)w, eps, out, rows, n);
   else
-    hipLaunchKernelGGL(k_rmsnorm<false>, dim3(rows), dim3(256), 0, st, (const float *)x, (const float *)w, eps, out,
-                       n);
+    launch_rmsnorm<false>(st, (const float *)x, (const float *)w, eps, out, rows, n);
   return hwk::launched("hwk_rmsnorm");
 }
 
@@ -211,6 +210,6 @@ char *hwk::rmsnorm_f16(hipStream_t st, const float *h, const float *nw, double e
                        uint32_t k) {
   HWK_CHECK(h && nw && out, "rmsnorm_f16: null pointer");
   if (rows == 0 || k == 0) return nullptr;
-  hipLaunchKernelGGL(k_rmsnorm<true>, dim3(rows), dim3(256), 0, st, h, nw, eps, out, k);
+  launch_rmsnorm<true>(st, h, nw, eps, out, rows, k);
   return hwk::launched("rmsnorm_f16");
 }

@@ -23,8 +23,10 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   return v;
 }
 
-// One workgroup a row.
-template <bool F16OUT>
+// One workgroup a row. V > 0: the row (at most 256*V values) is loaded once into registers, all of a
+// thread's loads (x and w) issued before the sum; V = 0: two passes over the row. Either way thread t
+// sums x[t], x[t+256], ... in that order, then the wave and the workgroup sums are added alike.
+template <bool F16OUT, int V = 0>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, double eps,
                                                  void *__restrict__ out, uint32_t n) {
 #pragma clang fp contract(off)
@@ -32,22 +34,61 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
   const int t = threadIdx.x, lane = t & 63;
   const float *xr = x + (size_t)blockIdx.x * n;
   double ss = 0.0;
-  for (uint32_t i = t; i < n; i += 256) {
-    const double v = (double)xr[i];
-    ss += v * v;
+  float xv[V > 0 ? V : 1], wv[V > 0 ? V : 1];
+  if constexpr (V > 0) {
+#pragma unroll
+    for (int j = 0; j < V; j++) {
+      const uint32_t i = min((uint32_t)(t + 256 * j), n - 1);  // past n: the last value again, not summed
+      xv[j] = xr[i];
+      wv[j] = w[i];
+    }
+#pragma unroll
+    for (int j = 0; j < V; j++)
+      if ((uint32_t)(t + 256 * j) < n) {
+        const double v = (double)xv[j];
+        ss += v * v;
+      }
+  } else {
+    for (uint32_t i = t; i < n; i += 256) {
+      const double v = (double)xr[i];
+      ss += v * v;
+    }
   }
   ss = wave_sum_d(ss);
   if (lane == 0) red[t >> 6] = ss;
   __syncthreads();
   ss = ((red[0] + red[1]) + red[2]) + red[3];
   const float r = (float)(1.0 / sqrt(ss / (double)n + eps));
-  for (uint32_t i = t; i < n; i += 256) {
-    const float y = f32_value((xr[i] * r) * w[i]);
+  auto put = [&](uint32_t i, float y) {
     if (F16OUT)
       ((f16 *)out)[(size_t)blockIdx.x * n + i] = (f16)y;
     else
       ((float *)out)[(size_t)blockIdx.x * n + i] = y;
+  };
+  if constexpr (V > 0) {
+#pragma unroll
+    for (int j = 0; j < V; j++) {
+      const uint32_t i = t + 256 * j;
+      if (i < n) put(i, f32_value((xv[j] * r) * wv[j]));
+    }
+  } else {
+    for (uint32_t i = t; i < n; i += 256) put(i, f32_value((xr[i] * r) * w[i]));
   }
+}
+
+// Launches k_rmsnorm for rows of n values: the one-pass form up to 4096 values a row.
+template <bool F16OUT>
+inline void launch_rmsnorm(hipStream_t st, const float *x, const float *w, double eps, void *out, uint32_t rows,
+                           uint32_t n) {
+  const uint32_t per = (n + 255) / 256;
+  if (per <= 4)
+    hipLaunchKernelGGL((k_rmsnorm<F16OUT, 4>), dim3(rows), dim3(256), 0, st, x, w, eps, out, n);
+  else if (per <= 8)
+    hipLaunchKernelGGL((k_rmsnorm<F16OUT, 8>), dim3(rows), dim3(256), 0, st, x, w, eps, out, n);
+  else if (per <= 16)
+    hipLaunchKernelGGL((k_rmsnorm<F16OUT, 16>), dim3(rows), dim3(256), 0, st, x, w, eps, out, n);
+  else
+    hipLaunchKernelGGL((k_rmsnorm<F16OUT, 0>), dim3(rows), dim3(256), 0, st, x, w, eps, out, n);
 }
 
 // One wave a (token, head) of 128 dims: lane l holds dims l and l + 64, the pair rotate_half mixes.
