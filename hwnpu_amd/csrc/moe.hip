@@ -386,11 +386,10 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down(const float *__restrict__ 
 // LDS the staging copies may take (gfx950: 160 KB a workgroup, 64 KB without the attribute).
 constexpr size_t kMoeStageLds = 128 * 1024;
 
-template <int LPR, int BPL>
-void launch_down(hipStream_t st, const float *act, const int32_t *idx, const float *w, const void *dw, const void *de,
-                 const float *db, float *out, const MoeArgs &a) {
-  constexpr int RS = 64 / LPR, NW = 8;
-  constexpr int EPW = BPL <= 1 ? 8 : 12 / BPL;
+template <int LPR, int BPL, int EPW, int NW>
+void launch_down_cfg(hipStream_t st, const float *act, const int32_t *idx, const float *w, const void *dw,
+                     const void *de, const float *db, float *out, const MoeArgs &a) {
+  constexpr int RS = 64 / LPR;
   const size_t lds = (size_t)a.T * a.k * a.I * 4;
   const dim3 grid((a.H + RS - 1) / RS);
   if (lds <= kMoeStageLds) {
@@ -406,6 +405,22 @@ void launch_down(hipStream_t st, const float *act, const int32_t *idx, const flo
     hipLaunchKernelGGL((k_moe_down<LPR, BPL, EPW, false, NW>), grid, dim3(64 * NW), 0, st, act, idx, w,
                        (const uint4 *)dw, (const uint8_t *)de, db, out, a);
   }
+}
+
+// The waves of a down workgroup and the experts a wave loads at once, by the chosen (token, expert)
+// slots n = T*k (at most n distinct experts): every slot a wave of its own up to 4 (no load is a
+// padding copy), two a wave for 8 waves up to 32 (16 at once, a second round past 16 distinct
+// experts), else as many as the registers take.
+template <int LPR, int BPL>
+void launch_down(hipStream_t st, const float *act, const int32_t *idx, const float *w, const void *dw, const void *de,
+                 const float *db, float *out, const MoeArgs &a) {
+  const uint32_t n = a.T * a.k;
+  if (n <= 4)
+    launch_down_cfg<LPR, BPL, 1, 4>(st, act, idx, w, dw, de, db, out, a);
+  else if (n <= 32)
+    launch_down_cfg<LPR, BPL, 2, 8>(st, act, idx, w, dw, de, db, out, a);
+  else
+    launch_down_cfg<LPR, BPL, BPL <= 1 ? 8 : 12 / BPL, 8>(st, act, idx, w, dw, de, db, out, a);
 }
 
 char *check_params(const char *what, const hwk_moe_params *p) {
