@@ -190,9 +190,9 @@ __device__ __forceinline__ float gated(float g, float u, const MoeArgs &a) {
 // Workgroup (row-pair tile blockIdx.x, chosen expert number blockIdx.y in ascending id). 64 lanes
 // a row, BPL blocks a lane (nb = H/32 <= 64*BPL); a wave takes PPW row pairs (gate 2j, up 2j+1).
 // ROUTE: the workgroup routes every token from the logits first (waves over tokens), and workgroup
-// (0, 0) writes idx and w; else idx is given. XL: x (T, H) fp16 is copied into LDS (dynamic, T*H*2
-// bytes) before the route, so that no token's products wait on a global load.
-template <int BPL, int PPW, bool ROUTE, bool XL>
+// (0, 0) writes idx and w; else idx is given. x is read from global memory per token after the
+// weight loads are issued (an LDS copy of x first only delays the weight loads).
+template <int BPL, int PPW, bool ROUTE>
 __global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x, const float *__restrict__ logits,
                                                      const float *__restrict__ rbias, int32_t *__restrict__ idx,
                                                      float *__restrict__ wout, const uint4 *__restrict__ gw,
@@ -200,10 +200,8 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x
                                                      float *__restrict__ act, MoeArgs a) {
   __shared__ int32_t sidx[64];
   __shared__ float sw[64];
-  extern __shared__ uint4 xsh[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t n = a.T * a.k;
-  if constexpr (XL) stage_copy<8>(xsh, x, a.T * a.H / 8);
   if constexpr (ROUTE) {
     for (uint32_t t = wave; t < a.T; t += 4)
       choose_wave(logits + (size_t)t * a.E, rbias, a.E, a.k, a.score, a.norm, a.scale, sidx + t * a.k, sw + t * a.k);
@@ -254,7 +252,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const size_t xi = ((size_t)t * a.H + b * 32) / 8 + q;
-        xr[j][q] = XL ? xsh[xi] : x[xi];
+        xr[j][q] = x[xi];
       }
     }
 #pragma unroll
@@ -458,14 +456,9 @@ void launch_gate_up(hipStream_t st, const void *x, const float *logits, const fl
   const uint32_t unique_max = a.T * a.k < a.E ? a.T * a.k : a.E;
   const dim3 g1((a.I + 4 * PPW - 1) / (4 * PPW), unique_max);
   const int bpl1 = (int)((a.H / 32 + 63) / 64);
-  const size_t xl = (size_t)a.T * a.H * 2;  // x in LDS when it fits in 32 KB
-#define HWK_GU(B)                                                                                                \
-  if (xl <= 32 * 1024)                                                                                           \
-    hipLaunchKernelGGL((k_moe_gate_up<B, PPW, ROUTE, true>), g1, dim3(256), xl, st, (const uint4 *)x, logits,     \
-                       rbias, idx, w, (const uint4 *)gu_w, (const uint8_t *)gu_e, gu_b, act, a);                  \
-  else                                                                                                           \
-    hipLaunchKernelGGL((k_moe_gate_up<B, PPW, ROUTE, false>), g1, dim3(256), 0, st, (const uint4 *)x, logits,     \
-                       rbias, idx, w, (const uint4 *)gu_w, (const uint8_t *)gu_e, gu_b, act, a)
+#define HWK_GU(B)                                                                                         \
+  hipLaunchKernelGGL((k_moe_gate_up<B, PPW, ROUTE>), g1, dim3(256), 0, st, (const uint4 *)x, logits, rbias, idx, w, \
+                     (const uint4 *)gu_w, (const uint8_t *)gu_e, gu_b, act, a)
   switch (bpl1) {
     case 1: HWK_GU(1); break;
     case 2: HWK_GU(2); break;

@@ -244,21 +244,25 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   constexpr int NT = 64 * WPB;
   constexpr int PER = (64 * BPL * 32 + NT - 1) / NT;  // x values a thread makes (X_NORM)
   constexpr int XC = 64 * BPL * 4;                    // 16-byte chunks of x LDS holds
-  constexpr int XPER = (XC + NT - 1) / NT;            // chunks a thread copies (X_F16)
+  constexpr int XD = (64 * BPL * 16 + NT - 1) / NT;   // dwords of x a thread copies (X_F16)
   constexpr int M4 = (64 * BPL * 32 / 4 + NT - 1) / NT;  // groups of 4 x values a thread merges (X_MERGE)
   constexpr bool add = MODE == HWK_OUT_ADD_F32;
-  __shared__ uint4 xs[XC];
+  __shared__ uint4 xs[NT * XD / 4];  // x (at least XC chunks)
   __shared__ double red[WPB];
-  __shared__ float mm[XM == X_MERGE ? 64 * BPL / 4 * kMergeMaxChunks : 1];  // m, then the weight, of (head, chunk)
-  __shared__ float ml[XM == X_MERGE ? 64 * BPL / 4 * kMergeMaxChunks : 1];
+  constexpr int MS = XM == X_MERGE ? 64 * BPL / 4 * kMergeMaxChunks : 1;  // (head, chunk) slots (X_MERGE)
+  constexpr int MPER = (MS + NT - 1) / NT;                                 // slots a thread stages
+  __shared__ float mm[MS + 64];  // m of (head, chunk); past MS one spare slot a lane
+  __shared__ float ml[MS + 64];  // l of (head, chunk)
   const int t = threadIdx.x, lane = t & 63;
   const uint32_t k = nb * 32;
   const uint32_t r0 = (blockIdx.x * WPB + (t >> 6)) * RPW;
   // x's inputs first, then the old y of ADD mode, then the weights (loads complete in issue order
   // for the wait counter, so x is made while the weights are in flight)
   float hv[PER], wv[PER];
-  uint4 xv[XPER];
+  uint32_t xv[XD];
   float4 ov[XM == X_MERGE ? M4 : 1][XM == X_MERGE ? kMergeBatch : 1];
+  float mv[XM == X_MERGE ? MPER : 1], lv[XM == X_MERGE ? MPER : 1];
+  uint32_t md[XM == X_MERGE ? MPER : 1];
   uint32_t live = 1;
   if constexpr (XM == X_MERGE) {
     // the partials of the live chunks: o of this thread's x values (4 consecutive dims of one query
@@ -276,11 +280,16 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
         ov[j][c] = *(const float4 *)(in.ws + slot * 128 + d);
       }
     }
-    for (uint32_t i = t; i < heads * live; i += NT) {
-      const uint32_t hq = i / live, cc = i % live;
+    // m and l into registers here, into LDS (every thread writing, past heads * live into its spare
+    // slot) once the weight loads are issued: a load whose only use sits under a branch would be
+    // sunk into it, behind the weight loads, with a wait for those too
+#pragma unroll
+    for (int j = 0; j < MPER; j++) {
+      const uint32_t i = t + j * NT, ic = min(i, heads * live - 1), hq = ic / live, cc = ic % live;
       const size_t slot = ((size_t)(hq / in.G) * in.nchunk + cc) * in.G + hq % in.G;
-      mm[hq * kMergeMaxChunks + cc] = ws_m[slot];
-      ml[hq * kMergeMaxChunks + cc] = ws_l[slot];
+      mv[j] = ws_m[slot];
+      lv[j] = ws_l[slot];
+      md[j] = i < heads * live ? hq * kMergeMaxChunks + cc : MS + lane;
     }
   } else if constexpr (XM == X_NORM) {
 #pragma unroll
@@ -290,8 +299,10 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
       wv[j] = in.nw[i];
     }
   } else {
+    // dwords t, t + NT, ... of x (past x's end the last dword again, into slots no lane reads)
+    const uint32_t *xw = (const uint32_t *)in.x16;
 #pragma unroll
-    for (int j = 0; j < XPER; j++) xv[j] = in.x16[min((uint32_t)(t + j * NT), nb * 4 - 1)];
+    for (int j = 0; j < XD; j++) xv[j] = xw[min((uint32_t)(t + j * NT), nb * 16 - 1)];
   }
   float yo[RPW];
 #pragma unroll
@@ -299,6 +310,7 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   issue_order();
   RowSet<BPL, RPW> cur;
   load_rowset<64, BPL, RPW>(cur, w, e, r0, n, nb, lane);
+  issue_order();  // every weight load issued before the waits for x's inputs
   f16 *xh = (f16 *)xs;
   if constexpr (XM == X_NORM) {
     double ss = 0.0;
@@ -320,6 +332,11 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   } else if constexpr (XM == X_MERGE) {
     // the reference's Merge rule per query head: top = the largest m among chunks with l > 0, a chunk
     // weighs exp(m - top), x = fp16(sum(w * o) / sum(w * l))
+#pragma unroll
+    for (int j = 0; j < MPER; j++) {
+      mm[md[j]] = mv[j];
+      ml[md[j]] = lv[j];
+    }
     __syncthreads();
     const uint32_t heads = k / 128, slots = heads * in.nchunk;
 #pragma unroll
@@ -360,9 +377,10 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
     }
     (void)slots;
   } else {
+    // every thread writes (a write under a branch would let the compiler sink x's load into it,
+    // behind the weight loads, and wait for those too)
 #pragma unroll
-    for (int j = 0; j < XPER; j++)
-      if (t + j * NT < XC) xs[t + j * NT] = xv[j];
+    for (int j = 0; j < XD; j++) ((uint32_t *)xs)[t + j * NT] = xv[j];
   }
   __syncthreads();
   uint4 xr[BPL][4];
@@ -684,12 +702,12 @@ void launch_rpw(hipStream_t st, const void *w, const void *e, const void *x, voi
 }
 
 // K1 for rows of 33..256 blocks (64 lanes a row), one row a wave: the most waves in flight, which is
-// what a single launch's read of a few MB needs (16 waves a workgroup for matrices of 4096 rows or
-// more, measured fastest on C1; else 8 waves).
+// what a single launch's read of a few MB needs (4 waves a workgroup for matrices of 4096 rows or
+// more, measured fastest on C1: x's barrier then waits on 4 waves' loads, not 16; else 8 waves).
 template <int BPL, int MODE>
 void launch_lds_m(hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n, uint32_t nb) {
   if (n >= 4096) {
-    hipLaunchKernelGGL((k_mxfp4_gemv_lds<16, 1, BPL, MODE>), dim3((n + 15) / 16), dim3(64 * 16), 0, st,
+    hipLaunchKernelGGL((k_mxfp4_gemv_lds<4, 1, BPL, MODE>), dim3((n + 3) / 4), dim3(64 * 4), 0, st,
                        (const uint4 *)w, (const uint8_t *)e, (const uint4 *)x, y, n, nb);
   } else {
     hipLaunchKernelGGL((k_mxfp4_gemv_lds<8, 1, BPL, MODE>), dim3((n + 7) / 8), dim3(64 * 8), 0, st,

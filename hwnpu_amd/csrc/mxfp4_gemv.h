@@ -13,6 +13,8 @@
 // writes the row.
 #pragma once
 
+#include <type_traits>
+
 #include "hwk_common.h"
 
 // The fp32 sum of a 32-value block's codes times its x: 16 code bytes against x's 32 fp16 values.
@@ -40,16 +42,21 @@ __device__ __forceinline__ void mxfp4_gemv_lds(const uint4 *__restrict__ w, cons
                                                const uint4 *__restrict__ x, void *__restrict__ y, uint32_t n,
                                                uint32_t nb) {
   constexpr int NT = 64 * W;
-  constexpr int XC = 64 * BPL * 4;          // 16-byte chunks of x LDS holds
-  constexpr int XPER = (XC + NT - 1) / NT;  // chunks a thread stages
-  __shared__ uint4 xs[XC];
+  // x is staged in units of 16 bytes when the threads divide its 64*BPL*4 chunks, else of 4 bytes
+  constexpr int XU = (64 * BPL * 4) % NT == 0 ? 16 : 4;           // bytes a unit
+  constexpr int XN = (64 * BPL * 64 / XU + NT - 1) / NT;          // units a thread stages
+  using XT = std::conditional_t<XU == 16, uint4, uint32_t>;
+  __shared__ uint4 xs[NT * XN * XU / 16];
   const int lane = threadIdx.x & 63, t = threadIdx.x;
   const uint32_t r0 = (blockIdx.x * W + (t >> 6)) * RPW;
-  const uint32_t xc = nb * 4;  // x's chunks
   constexpr bool add = MODE == HWK_OUT_ADD_F32;
-  uint4 xv[XPER];
+  // every thread loads and writes units t, t + NT, ... of x (past x's end the last unit again, into
+  // slots no lane reads): no thread loads a unit that others load too, and no write sits under a
+  // branch (the compiler would sink x's load into it, behind the weight loads, and wait for those)
+  const XT *xu = (const XT *)x;
+  XT xv[XN];
 #pragma unroll
-  for (int j = 0; j < XPER; j++) xv[j] = x[min((uint32_t)(t + j * NT), xc - 1)];
+  for (int j = 0; j < XN; j++) xv[j] = xu[min((uint32_t)(t + j * NT), nb * 64 / XU - 1)];
   // the old y of an ADD-mode call, loaded before the weights so that the sum at the end waits on
   // no load
   float yo[RPW];
@@ -68,9 +75,9 @@ __device__ __forceinline__ void mxfp4_gemv_lds(const uint4 *__restrict__ w, cons
       s[i][j] = e[blk];
     }
   }
+  issue_order();  // every weight load issued before the wait for x
 #pragma unroll
-  for (int j = 0; j < XPER; j++)
-    if (t + j * NT < XC) xs[t + j * NT] = xv[j];
+  for (int j = 0; j < XN; j++) ((XT *)xs)[t + j * NT] = xv[j];
   __syncthreads();
   uint4 xr[BPL][4];
 #pragma unroll
