@@ -226,7 +226,8 @@ struct XIn {
   uint32_t G, chunk, nchunk;  // query heads a kv head; the partials' chunking
 };
 
-// Chunks of attention partials the X_MERGE prologue loads at once (more are loaded a chunk at a time).
+// Chunks of attention partials the X_MERGE prologue loads at once when a thread merges more than 4
+// values of x (more are loaded a chunk at a time); a thread of 4 values loads every chunk's at once.
 constexpr int kMergeBatch = 8;
 // The most chunks X_MERGE takes (LDS holds their m and l for every query head).
 constexpr uint32_t kMergeMaxChunks = 16;
@@ -246,13 +247,14 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   constexpr int XC = 64 * BPL * 4;                    // 16-byte chunks of x LDS holds
   constexpr int XD = (64 * BPL * 16 + NT - 1) / NT;   // dwords of x a thread copies (X_F16)
   constexpr int M4 = (64 * BPL * 32 / 4 + NT - 1) / NT;  // groups of 4 x values a thread merges (X_MERGE)
+  constexpr int MB = M4 <= 1 ? (int)kMergeMaxChunks : kMergeBatch;  // chunks' o a thread loads up front
   constexpr bool add = MODE == HWK_OUT_ADD_F32;
   __shared__ uint4 xs[NT * XD / 4];  // x (at least XC chunks)
   __shared__ double red[WPB];
   constexpr int MS = XM == X_MERGE ? 64 * BPL / 4 * kMergeMaxChunks : 1;  // (head, chunk) slots (X_MERGE)
   constexpr int MPER = (MS + NT - 1) / NT;                                 // slots a thread stages
-  __shared__ float mm[MS + 64];  // m of (head, chunk); past MS one spare slot a lane
-  __shared__ float ml[MS + 64];  // l of (head, chunk)
+  __shared__ __align__(16) float mm[MS + 64];  // m of (head, chunk); past MS one spare slot a lane
+  __shared__ __align__(16) float ml[MS + 64];  // l of (head, chunk)
   const int t = threadIdx.x, lane = t & 63;
   const uint32_t k = nb * 32;
   const uint32_t r0 = (blockIdx.x * WPB + (t >> 6)) * RPW;
@@ -260,7 +262,7 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   // for the wait counter, so x is made while the weights are in flight)
   float hv[PER], wv[PER];
   uint32_t xv[XD];
-  float4 ov[XM == X_MERGE ? M4 : 1][XM == X_MERGE ? kMergeBatch : 1];
+  float4 ov[XM == X_MERGE ? M4 : 1][XM == X_MERGE ? MB : 1];
   float mv[XM == X_MERGE ? MPER : 1], lv[XM == X_MERGE ? MPER : 1];
   uint32_t md[XM == X_MERGE ? MPER : 1];
   uint32_t live = 1;
@@ -274,7 +276,7 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
     for (int j = 0; j < M4; j++) {
       const uint32_t e = min((uint32_t)(t + j * NT), k / 4 - 1) * 4, hq = e / 128, d = e % 128;
 #pragma unroll
-      for (int c = 0; c < kMergeBatch; c++) {
+      for (int c = 0; c < MB; c++) {
         const uint32_t cc = min((uint32_t)c, live - 1);
         const size_t slot = ((size_t)(hq / in.G) * in.nchunk + cc) * in.G + hq % in.G;
         ov[j][c] = *(const float4 *)(in.ws + slot * 128 + d);
@@ -345,22 +347,52 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
       if (e >= k) continue;
       const uint32_t hq = e / 128, d = e % 128;
       const float *hm = mm + hq * kMergeMaxChunks, *hl = ml + hq * kMergeMaxChunks;
+      // chunks in ascending order, the first MB unrolled: their m and l read from LDS at once (slots
+      // past live hold stale values, read but not used), held in registers by an empty asm so that
+      // the compiler does not move each read into the branch of its chunk, a wait apiece
+      typedef float f32x4 __attribute__((ext_vector_type(4)));
+      f32x4 m4[MB / 4], l4[MB / 4];
+#pragma unroll
+      for (int q = 0; q < MB / 4; q++) {
+        m4[q] = ((const f32x4 *)hm)[q];
+        l4[q] = ((const f32x4 *)hl)[q];
+      }
+#pragma unroll
+      for (int q = 0; q < MB / 4; q++) asm volatile("" : "+v"(m4[q]), "+v"(l4[q]));
+      float cm[MB], cl[MB];
+      bool ok[MB];
+#pragma unroll
+      for (int c = 0; c < MB; c++) {
+        cm[c] = m4[c / 4][c % 4];
+        cl[c] = l4[c / 4][c % 4];
+      }
       float top = -__builtin_inff();
-      for (uint32_t c = 0; c < live; c++)
+#pragma unroll
+      for (int c = 0; c < MB; c++) {
+        ok[c] = ((uint32_t)c < live) & (cl[c] > 0.0f);
+        if (ok[c]) top = fmaxf(top, cm[c]);
+      }
+      for (uint32_t c = MB; c < live; c++)
         if (hl[c] > 0.0f) top = fmaxf(top, hm[c]);
       float den = 0.0f, n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
-      for (uint32_t c = 0; c < live; c++) {
-        const float wc = (hl[c] > 0.0f && top != -__builtin_inff()) ? expf(hm[c] - top) : 0.0f;
-        if (wc > 0.0f) {
-          float4 o;
-          if (c < (uint32_t)kMergeBatch) {
+      const bool any = top != -__builtin_inff();
 #pragma unroll
-            for (int cb = 0; cb < kMergeBatch; cb++)
-              if ((uint32_t)cb == c) o = ov[j][cb];
-          } else {
-            const size_t slot = ((size_t)(hq / in.G) * in.nchunk + c) * in.G + hq % in.G;
-            o = *(const float4 *)(in.ws + slot * 128 + d);
-          }
+      for (int c = 0; c < MB; c++) {
+        const float wc = (ok[c] & any) ? expf(cm[c] - top) : 0.0f;
+        if (wc > 0.0f) {
+          const float4 o = ov[j][c];
+          den += wc * cl[c];
+          n0 += wc * o.x;
+          n1 += wc * o.y;
+          n2 += wc * o.z;
+          n3 += wc * o.w;
+        }
+      }
+      for (uint32_t c = MB; c < live; c++) {
+        const float wc = (hl[c] > 0.0f && any) ? expf(hm[c] - top) : 0.0f;
+        if (wc > 0.0f) {
+          const size_t slot = ((size_t)(hq / in.G) * in.nchunk + c) * in.G + hq % in.G;
+          const float4 o = *(const float4 *)(in.ws + slot * 128 + d);
           den += wc * hl[c];
           n0 += wc * o.x;
           n1 += wc * o.y;
