@@ -207,9 +207,24 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_stream(const uint4 *__restri
 }
 
 // Sum of a float64 over the wave.
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// A double's DPP move (both halves moved alike; lanes the row mask leaves out get 0.0).
+template <int CTRL, int ROW_MASK, bool BOUND>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROW_MASK, 0xf, BOUND);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xf, BOUND);
+  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// Sum of a double over the 64 lanes by DPP row shifts and row broadcasts, as wave_sum_to_63 (no LDS
+// round trip): lane 63 ends with the total.
+__device__ __forceinline__ double wave_sum_f64_to_63(double v) {
+  v += dpp_f64<0x111, 0xf, true>(v);   // row_shr:1
+  v += dpp_f64<0x112, 0xf, true>(v);   // row_shr:2
+  v += dpp_f64<0x114, 0xf, true>(v);   // row_shr:4
+  v += dpp_f64<0x118, 0xf, true>(v);   // row_shr:8
+  v += dpp_f64<0x142, 0xa, false>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_f64<0x143, 0xc, false>(v);  // row_bcast:31 into rows 2 and 3
   return v;
 }
 
@@ -255,6 +270,7 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   constexpr int MPER = (MS + NT - 1) / NT;                                 // slots a thread stages
   __shared__ __align__(16) float mm[MS + 64];  // m of (head, chunk); past MS one spare slot a lane
   __shared__ __align__(16) float ml[MS + 64];  // l of (head, chunk)
+  __shared__ __align__(16) float mw[MS];       // weight of (head, chunk)
   const int t = threadIdx.x, lane = t & 63;
   const uint32_t k = nb * 32;
   const uint32_t r0 = (blockIdx.x * WPB + (t >> 6)) * RPW;
@@ -321,8 +337,8 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
       if (t + j * NT >= k) hv[j] = 0.0f;
 #pragma unroll
     for (int j = 0; j < PER; j++) ss += (double)hv[j] * (double)hv[j];
-    ss = wave_sum_f64(ss);
-    if (lane == 0) red[t >> 6] = ss;
+    ss = wave_sum_f64_to_63(ss);
+    if (lane == 63) red[t >> 6] = ss;
     __syncthreads();
     ss = 0.0;
 #pragma unroll
@@ -340,48 +356,55 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
       ml[md[j]] = lv[j];
     }
     __syncthreads();
-    const uint32_t heads = k / 128, slots = heads * in.nchunk;
+    const uint32_t heads = k / 128;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    // every (head, chunk)'s weight, once for the workgroup: top over the head's chunks (its m and l
+    // read from LDS at once and held in registers by an empty asm, so that the compiler does not
+    // move each read into the branch of its chunk, a wait apiece; slots past live hold stale values,
+    // read but not used), then exp(m - top), or 0 for a chunk past live, of l <= 0 or of a head
+    // with none
+    for (uint32_t i = t; i < heads * kMergeMaxChunks; i += NT) {
+      const uint32_t hq = i / kMergeMaxChunks, c = i % kMergeMaxChunks;
+      const float *hm = mm + hq * kMergeMaxChunks, *hl = ml + hq * kMergeMaxChunks;
+      f32x4 m4[kMergeMaxChunks / 4], l4[kMergeMaxChunks / 4];
+#pragma unroll
+      for (int q = 0; q < (int)kMergeMaxChunks / 4; q++) {
+        m4[q] = ((const f32x4 *)hm)[q];
+        l4[q] = ((const f32x4 *)hl)[q];
+      }
+      const float mc = hm[c], lc = hl[c];
+#pragma unroll
+      for (int q = 0; q < (int)kMergeMaxChunks / 4; q++) asm volatile("" : "+v"(m4[q]), "+v"(l4[q]));
+      float top = -__builtin_inff();
+#pragma unroll
+      for (int cc = 0; cc < (int)kMergeMaxChunks; cc++)
+        if (((uint32_t)cc < live) & (l4[cc / 4][cc % 4] > 0.0f)) top = fmaxf(top, m4[cc / 4][cc % 4]);
+      const bool use = (c < live) & (lc > 0.0f) & (top != -__builtin_inff());
+      mw[i] = use ? expf(mc - top) : 0.0f;
+    }
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < M4; j++) {
       const uint32_t e = (uint32_t)(t + j * NT) * 4;
       if (e >= k) continue;
       const uint32_t hq = e / 128, d = e % 128;
-      const float *hm = mm + hq * kMergeMaxChunks, *hl = ml + hq * kMergeMaxChunks;
-      // chunks in ascending order, the first MB unrolled: their m and l read from LDS at once (slots
-      // past live hold stale values, read but not used), held in registers by an empty asm so that
-      // the compiler does not move each read into the branch of its chunk, a wait apiece
-      typedef float f32x4 __attribute__((ext_vector_type(4)));
-      f32x4 m4[MB / 4], l4[MB / 4];
+      const float *hw = mw + hq * kMergeMaxChunks, *hl = ml + hq * kMergeMaxChunks;
+      // chunks in ascending order, the first MB unrolled with their weights and l read at once
+      f32x4 w4[MB / 4], l4[MB / 4];
 #pragma unroll
       for (int q = 0; q < MB / 4; q++) {
-        m4[q] = ((const f32x4 *)hm)[q];
+        w4[q] = ((const f32x4 *)hw)[q];
         l4[q] = ((const f32x4 *)hl)[q];
       }
 #pragma unroll
-      for (int q = 0; q < MB / 4; q++) asm volatile("" : "+v"(m4[q]), "+v"(l4[q]));
-      float cm[MB], cl[MB];
-      bool ok[MB];
-#pragma unroll
-      for (int c = 0; c < MB; c++) {
-        cm[c] = m4[c / 4][c % 4];
-        cl[c] = l4[c / 4][c % 4];
-      }
-      float top = -__builtin_inff();
-#pragma unroll
-      for (int c = 0; c < MB; c++) {
-        ok[c] = ((uint32_t)c < live) & (cl[c] > 0.0f);
-        if (ok[c]) top = fmaxf(top, cm[c]);
-      }
-      for (uint32_t c = MB; c < live; c++)
-        if (hl[c] > 0.0f) top = fmaxf(top, hm[c]);
+      for (int q = 0; q < MB / 4; q++) asm volatile("" : "+v"(w4[q]), "+v"(l4[q]));
       float den = 0.0f, n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
-      const bool any = top != -__builtin_inff();
 #pragma unroll
       for (int c = 0; c < MB; c++) {
-        const float wc = (ok[c] & any) ? expf(cm[c] - top) : 0.0f;
+        const float wc = w4[c / 4][c % 4];
         if (wc > 0.0f) {
           const float4 o = ov[j][c];
-          den += wc * cl[c];
+          den += wc * l4[c / 4][c % 4];
           n0 += wc * o.x;
           n1 += wc * o.y;
           n2 += wc * o.z;
@@ -389,7 +412,7 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
         }
       }
       for (uint32_t c = MB; c < live; c++) {
-        const float wc = (hl[c] > 0.0f && any) ? expf(hm[c] - top) : 0.0f;
+        const float wc = hw[c];
         if (wc > 0.0f) {
           const size_t slot = ((size_t)(hq / in.G) * in.nchunk + c) * in.G + hq % in.G;
           const float4 o = *(const float4 *)(in.ws + slot * 128 + d);
@@ -407,7 +430,6 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
       xh[e + 2] = (f16)f32_value(r2);
       xh[e + 3] = (f16)f32_value(r3);
     }
-    (void)slots;
   } else {
     // every thread writes (a write under a branch would let the compiler sink x's load into it,
     // behind the weight loads, and wait for those too)
