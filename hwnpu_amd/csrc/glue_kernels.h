@@ -17,15 +17,10 @@
 namespace hwk_glue {
 namespace {  // each translation unit that launches them holds its own copy
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
 // One workgroup a row. V > 0: the row (at most 256*V values) is loaded once into registers, all of a
 // thread's loads (x and w) issued before the sum; V = 0: two passes over the row. Either way thread t
-// sums x[t], x[t+256], ... in that order, then the wave and the workgroup sums are added alike.
+// sums x[t], x[t+256], ... in that order, then the wave (DPP row shifts into lane 63) and the
+// workgroup sums are added alike.
 template <bool F16OUT, int V = 0>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, double eps,
                                                  void *__restrict__ out, uint32_t n) {
@@ -54,8 +49,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
       ss += v * v;
     }
   }
-  ss = wave_sum_d(ss);
-  if (lane == 0) red[t >> 6] = ss;
+  ss = wave_sum_f64_to_63(ss);
+  if (lane == 63) red[t >> 6] = ss;
   __syncthreads();
   ss = ((red[0] + red[1]) + red[2]) + red[3];
   const float r = (float)(1.0 / sqrt(ss / (double)n + eps));

@@ -50,6 +50,35 @@ char *attn_step(hipStream_t st, const float *qkv, const float *qn, const float *
 
 }  // namespace hwk
 
+// A double's DPP move (both halves moved alike; lanes the row mask leaves out get 0.0).
+template <int CTRL, int ROW_MASK, bool BOUND>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROW_MASK, 0xf, BOUND);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xf, BOUND);
+  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// Sum of a double over the 64 lanes by DPP row shifts and row broadcasts, as wave_sum_to_63 (no LDS
+// round trip): lane 63 ends with the total.
+__device__ __forceinline__ double wave_sum_f64_to_63(double v) {
+  v += dpp_f64<0x111, 0xf, true>(v);   // row_shr:1
+  v += dpp_f64<0x112, 0xf, true>(v);   // row_shr:2
+  v += dpp_f64<0x114, 0xf, true>(v);   // row_shr:4
+  v += dpp_f64<0x118, 0xf, true>(v);   // row_shr:8
+  v += dpp_f64<0x142, 0xa, false>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_f64<0x143, 0xc, false>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+// The sum of a double over the 64 lanes, in every lane (lane 63's total read back as a scalar).
+__device__ __forceinline__ double wave_sum_f64_all(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, wave_sum_f64_to_63(v));
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
 // Per-head RMSNorm then RoPE of one 128-wide head held as dims (l, l+64) by lane l: (x * r) * w
 // with r = float(1 / sqrt(mean(x^2) + eps)) (mean in float64), then x*cos + rotate_half(x)*sin
 // with the position's float32 tables (rotate_half = cat(-x2, x1); reference internal/llm/blocks/
@@ -57,9 +86,7 @@ char *attn_step(hipStream_t st, const float *qkv, const float *qn, const float *
 __device__ __forceinline__ void head_norm_rope(float x0, float x1, float nw0, float nw1, float c, float s,
                                                double eps, float &o0, float &o1) {
 #pragma clang fp contract(off)
-  double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  const double ss = wave_sum_f64_all((double)x0 * (double)x0 + (double)x1 * (double)x1);
   const float r = (float)(1.0 / sqrt(ss / 128.0 + eps));
   const float y0 = (x0 * r) * nw0, y1 = (x1 * r) * nw1;
   o0 = f32_value(y0 * c + (-y1) * s);  // j < half: x*cos + (-x[j+half])*sin

@@ -207,27 +207,6 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_stream(const uint4 *__restri
 }
 
 // Sum of a float64 over the wave.
-// A double's DPP move (both halves moved alike; lanes the row mask leaves out get 0.0).
-template <int CTRL, int ROW_MASK, bool BOUND>
-__device__ __forceinline__ double dpp_f64(double v) {
-  const uint64_t u = __builtin_bit_cast(uint64_t, v);
-  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROW_MASK, 0xf, BOUND);
-  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xf, BOUND);
-  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-}
-
-// Sum of a double over the 64 lanes by DPP row shifts and row broadcasts, as wave_sum_to_63 (no LDS
-// round trip): lane 63 ends with the total.
-__device__ __forceinline__ double wave_sum_f64_to_63(double v) {
-  v += dpp_f64<0x111, 0xf, true>(v);   // row_shr:1
-  v += dpp_f64<0x112, 0xf, true>(v);   // row_shr:2
-  v += dpp_f64<0x114, 0xf, true>(v);   // row_shr:4
-  v += dpp_f64<0x118, 0xf, true>(v);   // row_shr:8
-  v += dpp_f64<0x142, 0xa, false>(v);  // row_bcast:15 into rows 1 and 3
-  v += dpp_f64<0x143, 0xc, false>(v);  // row_bcast:31 into rows 2 and 3
-  return v;
-}
-
 // Where the decode-step GEMV's x comes from.
 enum XMode { X_F16 = 0, X_NORM = 1, X_MERGE = 2 };
 
