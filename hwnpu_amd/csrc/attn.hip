@@ -283,14 +283,15 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const f16 *__restrict__ 
 //
 // Workgroup (kv head h, chunk c) of W waves over the keys [c*chunk, min((c+1)*chunk, p+1)) for the token
 // at position p = *pos; the grid covers the cache's capacity and a workgroup whose chunk starts past p
-// leaves at once (the consumer reads only chunks 0 .. p/chunk). Prologue: q for the kv head's G query
+// attends no key (the consumer reads only chunks 0 .. p/chunk). Prologue: q for the kv head's G query
 // heads comes from the fp32 projection qkv (heads + 2*kvh rows of 128) through the per-head RMSNorm and
 // RoPE; the workgroup whose chunk holds p (the owner) also makes the new k (normed, rotated) and v,
 // writes them to the caches at p for later steps and keeps them in LDS: the tile holding p takes them
-// from there in place of its load of row p, so the owner waits on no store. The prologue's loads go
-// out first, then the waves' first tiles (loads complete in issue order for the wait counter). Each
-// workgroup leaves its partial (o unnormalized, m in natural-log units, l) per query head with plain
-// stores at slot (h*nchunk + c)*G + g; the o_proj GEMV merges them (mxfp4_gemv_x's X_MERGE).
+// from there in place of its load of row p, so the owner waits on no store. The prologue's rows and
+// the waves' first tiles are loaded before the position is read, then the RoPE tables' row p and the
+// second tiles. Each workgroup leaves its partial (o unnormalized, m in natural-log units, l) per
+// query head with plain stores at slot (h*nchunk + c)*G + g; the o_proj GEMV merges them
+// (mxfp4_gemv_x's X_MERGE).
 template <int G, int W>
 __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ qkv, const float *__restrict__ qn,
                                                       const float *__restrict__ kn, const float *__restrict__ cos_t,
@@ -306,27 +307,36 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
   __shared__ __attribute__((aligned(16))) f16 knew[128], vnew[128];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t h = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
-  const uint32_t p = (uint32_t)*pos, len = p + 1;
   const uint32_t begin = c * chunk;
-  if (begin >= len) return;
-  const bool owner = p - begin < chunk;  // the chunk holds p (begin <= p)
-  const uint32_t end = owner ? len : begin + chunk;
   const size_t head_base = (size_t)h * cap;
-  // prologue jobs: wave j makes job j (query head j < G, then k, then v); a wave past the jobs repeats
-  // the last one and keeps nothing, so that every wave's loads are issued before its tile loads
-  const uint32_t jobs = owner ? G + 2 : G;
-  const uint32_t j0 = (uint32_t)wave < jobs ? (uint32_t)wave : jobs - 1;
+  // the position first (written by the previous step's argmax), then the loads that do not depend on
+  // it, none waiting for it: wave j loads prologue job j (query head j < G, then k, then v; a wave
+  // past the jobs repeats the last one, every workgroup loads the k and v jobs and only the owner
+  // keeps them) and its first tile (rows clamped to the capacity); then, the position read, the
+  // RoPE tables' row p and the second tile (loads complete in issue order for the wait counter: the
+  // RoPE waits on the first tile at most)
+  const int32_t pv = load_first(pos);
+  const uint32_t j0 = (uint32_t)wave < (uint32_t)G + 2 ? (uint32_t)wave : (uint32_t)G + 1;
   auto job_row = [&](uint32_t j) { return j < G ? h * G + j : j == G ? heads + h : heads + kvh + h; };
   const float *nwp = j0 < G ? qn : kn;
   const float x0 = qkv[(size_t)job_row(j0) * 128 + lane], x1 = qkv[(size_t)job_row(j0) * 128 + lane + 64];
   const float nw0 = nwp[lane], nw1 = nwp[lane + 64];
-  const float cp = cos_t[(size_t)p * 64 + lane], sp = sin_t[(size_t)p * 64 + lane];
-  issue_order();
-  const uint32_t kb = begin + wave * kpw, ke = min(kb + kpw, end);
-  const uint32_t nt = kb < ke ? (ke - kb + 15) / 16 : 0;
+  const uint32_t kb = begin + wave * kpw;
   KTile<false> ta, tb;
   load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, kb, cap, lane);
+  issue_order();
+  const uint32_t p = (uint32_t)__builtin_amdgcn_readfirstlane(pv), len = p + 1;
+  const float cp = cos_t[(size_t)p * 64 + lane], sp = sin_t[(size_t)p * 64 + lane];
+  issue_order();
   load_ktile<false>(tb, kc, vc, nullptr, nullptr, head_base, kb + 16, cap, lane);
+  // a workgroup whose chunk starts past p attends no key (no early exit: the compiler would move the
+  // loads above behind the branch, and so behind the read of the position) and leaves a partial of
+  // weight 0, which the merge does not read
+  const bool owner = p - begin < chunk;  // the chunk holds p (begin <= p)
+  const uint32_t end = begin >= len ? begin : owner ? len : begin + chunk;
+  const uint32_t jobs = owner ? G + 2 : G;
+  const uint32_t ke = min(kb + kpw, end);
+  const uint32_t nt = kb < ke ? (ke - kb + 15) / 16 : 0;
   auto make_job = [&](uint32_t j, float a0, float a1, float w0, float w1, bool keep) {
     float o0, o1;
     head_norm_rope(a0, a1, w0, w1, cp, sp, eps, o0, o1);

@@ -113,6 +113,17 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// *p by a vector load (its index an opaque zero), for a value that later loads must not wait on: a
+// scalar load shares its wait counter with LDS traffic and the kernel arguments' loads, so waits for
+// those would wait for it too, while vector loads complete in issue order (a load issued first is
+// waited for without waiting on the loads after it). readfirstlane of the result gives it as a scalar
+// where it is used.
+__device__ __forceinline__ int32_t load_first(const int32_t *p) {
+  uint32_t z = 0;
+  asm volatile("" : "+v"(z));
+  return p[z];
+}
+
 // v as a float32 value of its own: instruction selection cannot see through the empty asm, so a
 // conversion to fp16 that follows rounds this float32 (twice rounded, as the reference's fp16
 // storage of a float32 result). Without it the backend folds a product and the conversion into
