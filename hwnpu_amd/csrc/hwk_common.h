@@ -85,12 +85,92 @@ __device__ __forceinline__ h2 fp4x2_to_h2(uint32_t w) {
   return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, SEL);
 }
 
-// Sum of a value over groups of G lanes (G a power of two up to 64), every lane gets its group's.
+// The two permlane swaps: v_permlane16_swap exchanges the odd rows (16 lanes) of its first operand
+// with the even rows of its second, v_permlane32_swap the upper half of the first with the lower
+// half of the second. On two copies of v, the two results hold v and its row (half) partner in every
+// lane. Issued as inline asm after two wait states (the hazard the compiler inserts before them):
+// the compiler builtin's second result is not usable (it is folded into the first).
+__device__ __forceinline__ void swap_rows16(float &a, float &b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_rows32(float &a, float &b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+// Sum / max over the 4 row groups (l, l^16, l^32, l^48); every lane gets the result.
+__device__ __forceinline__ float row_groups_sum(float v) {
+  float a = v, b = v;
+  swap_rows16(a, b);
+  v = a + b;
+  a = v;
+  b = v;
+  swap_rows32(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float row_groups_max(float v) {
+  float a = v, b = v;
+  swap_rows16(a, b);
+  v = fmaxf(a, b);
+  a = v;
+  b = v;
+  swap_rows32(a, b);
+  return fmaxf(a, b);
+}
+
+// Sum / max of v over aligned groups of G lanes (G = 8, 16, 32 or 64) with no LDS round trip: quad
+// swaps, the half-row and row mirrors (DPP), then the row-group swaps. Each step adds a lane and its
+// partner, so every lane of a group ends with the same bits.
+#define HWK_DPP_ALL(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), ctrl, 0xf, 0xf, false))
+template <int G>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+  static_assert(G == 8 || G == 16 || G == 32 || G == 64, "groups of 8, 16, 32 or 64 lanes");
+  v += HWK_DPP_ALL(v, 0xb1);   // quad_perm [1, 0, 3, 2]
+  v += HWK_DPP_ALL(v, 0x4e);   // quad_perm [2, 3, 0, 1]
+  v += HWK_DPP_ALL(v, 0x141);  // row_half_mirror
+  if constexpr (G >= 16) v += HWK_DPP_ALL(v, 0x140);  // row_mirror
+  if constexpr (G >= 32) {
+    float a = v, b = v;
+    swap_rows16(a, b);
+    v = a + b;
+  }
+  if constexpr (G == 64) {
+    float a = v, b = v;
+    swap_rows32(a, b);
+    v = a + b;
+  }
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_max_dpp(float v) {
+  static_assert(G == 8 || G == 16 || G == 32 || G == 64, "groups of 8, 16, 32 or 64 lanes");
+  v = fmaxf(v, HWK_DPP_ALL(v, 0xb1));
+  v = fmaxf(v, HWK_DPP_ALL(v, 0x4e));
+  v = fmaxf(v, HWK_DPP_ALL(v, 0x141));
+  if constexpr (G >= 16) v = fmaxf(v, HWK_DPP_ALL(v, 0x140));
+  if constexpr (G >= 32) {
+    float a = v, b = v;
+    swap_rows16(a, b);
+    v = fmaxf(a, b);
+  }
+  if constexpr (G == 64) {
+    float a = v, b = v;
+    swap_rows32(a, b);
+    v = fmaxf(a, b);
+  }
+  return v;
+}
+
+// Sum of a value over groups of G lanes (G a power of two up to 64), every lane gets its group's: by
+// DPP and permlane swaps from 8 lanes up, else by LDS shuffles.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G >= 8) {
+    return group_sum_dpp<G>(v);
+  } else {
 #pragma unroll
-  for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+    for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+  }
 }
 
 // Sum of a value over the 64 lanes by DPP row shifts and row broadcasts (no LDS traffic): lane 63

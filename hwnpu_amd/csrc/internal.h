@@ -93,33 +93,3 @@ __device__ __forceinline__ void head_norm_rope(float x0, float x1, float nw0, fl
   o1 = f32_value(y1 * c + y0 * s);     // j >= half: x*cos + x[j-half]*sin
 }
 
-// The two permlane swaps: v_permlane16_swap exchanges the odd rows (16 lanes) of its first operand
-// with the even rows of its second, v_permlane32_swap the upper half of the first with the lower
-// half of the second. On two copies of v, the two results hold v and its row (half) partner in every
-// lane. Issued as inline asm after two wait states (the hazard the compiler inserts before them):
-// the compiler builtin's second result is not usable (it is folded into the first).
-__device__ __forceinline__ void swap_rows16(float &a, float &b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap_rows32(float &a, float &b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-// Sum / max over the 4 row groups (l, l^16, l^32, l^48); every lane gets the result.
-__device__ __forceinline__ float row_groups_sum(float v) {
-  float a = v, b = v;
-  swap_rows16(a, b);
-  v = a + b;
-  a = v;
-  b = v;
-  swap_rows32(a, b);
-  return a + b;
-}
-__device__ __forceinline__ float row_groups_max(float v) {
-  float a = v, b = v;
-  swap_rows16(a, b);
-  v = fmaxf(a, b);
-  a = v;
-  b = v;
-  swap_rows32(a, b);
-  return fmaxf(a, b);
-}

@@ -44,9 +44,7 @@ __device__ void choose_wave(const float *__restrict__ logits, const float *__res
   const float bl = bias && live ? bias[lane] : 0.0f;
   float s;
   if (score == HWK_SCORE_SOFTMAX) {
-    float m = v;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    const float m = group_max_dpp<64>(v);
     const float ex = live ? (float)exp((double)(v - m)) : 0.0f;
     float total = 0.0f;
     for (uint32_t j = 0; j < E; j++) total += lane_f(ex, j);
