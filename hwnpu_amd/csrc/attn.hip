@@ -213,12 +213,16 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const f16 *__restrict__ 
   const size_t head_base = (size_t)h * cap;
   const uint32_t kb = begin + wave * kpw, ke = min(kb + kpw, end);
   const uint32_t nt = kb < ke ? (ke - kb + 15) / 16 : 0;
-  KTile<I8> ta, tb;
-  load_ktile<I8>(ta, k, v, ks, vs, head_base, kb, cap, lane);
-  load_ktile<I8>(tb, k, v, ks, vs, head_base, kb + 16, cap, lane);
+  // q first, then the two tiles (loads complete in issue order for the wait counter: the first
+  // tile's scores wait on q and that tile only)
   half8 qb[4];
 #pragma unroll
   for (int s = 0; s < 4; s++) qb[s] = half8_of(*(const uint4 *)(q + ((size_t)h * G + (lane % G)) * 128 + kstep_dim<I8>(s, lane)));
+  issue_order();
+  KTile<I8> ta, tb;
+  load_ktile<I8>(ta, k, v, ks, vs, head_base, kb, cap, lane);
+  issue_order();
+  load_ktile<I8>(tb, k, v, ks, vs, head_base, kb + 16, cap, lane);
   float m = -__builtin_inff(), ls = 0.0f, acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; g++)
