@@ -434,17 +434,28 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
     }
     v[i] = wave_sum_to_63(acc);
   }
-  if (lane == 63) {
-    if constexpr (SWIGLU) {
+  if constexpr (SWIGLU) {
+    // the workgroup's (gate, up) sums gathered in LDS, then wave 0 computes them a pair a lane: the
+    // float64 exp is issued once for all the pairs, not by each wave with one lane active
+    constexpr int NP = WPB * RPW / 2;
+    static_assert(NP <= 64, "a pair a lane of wave 0");
+    __shared__ float gus[2 * NP];
+    if (lane == 63) {
 #pragma unroll
       for (int i = 0; i < RPW; i += 2) {
-        if (r0 + i + 1 < n) {
-#pragma clang fp contract(off)
-          const float g = v[i], u = v[i + 1];
-          ((f16 *)y)[(r0 + i) / 2] = (f16)f32_value(g / (1.0f + (float)exp(-(double)g)) * u);
-        }
+        gus[2 * ((t >> 6) * (RPW / 2) + i / 2)] = v[i];
+        gus[2 * ((t >> 6) * (RPW / 2) + i / 2) + 1] = v[i + 1];
       }
-    } else {
+    }
+    __syncthreads();
+    const uint32_t pair = blockIdx.x * NP + t;
+    if (t < NP && 2 * pair + 1 < n) {
+#pragma clang fp contract(off)
+      const float g = gus[2 * t], u = gus[2 * t + 1];
+      ((f16 *)y)[pair] = (f16)f32_value(g / (1.0f + (float)exp(-(double)g)) * u);
+    }
+  } else if (lane == 63) {
+    {
 #pragma unroll
       for (int i = 0; i < RPW; i++) {
         if (r0 + i >= n) continue;
