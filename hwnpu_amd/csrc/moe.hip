@@ -198,6 +198,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x
                                                      float *__restrict__ act, MoeArgs a) {
   __shared__ int32_t sidx[64];
   __shared__ float sw[64];
+  __shared__ float gsum[PPW == 2 ? 1 : 2 * 64 * 4 * PPW];  // (token, wave, pair) -> (gate, up) sums
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t n = a.T * a.k;
   if constexpr (ROUTE) {
@@ -267,8 +268,24 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x
         gu[r] = group_sum<64>(v) + bias[p][r];
       }
       const uint32_t pair = pair0 + p;
-      if (lane == 0 && pair < I) act[((size_t)t * a.k + slot) * I + pair] = gated(gu[0], gu[1], a);
+      if constexpr (PPW == 2) {
+        if (lane == 0 && pair < I) act[((size_t)t * a.k + slot) * I + pair] = gated(gu[0], gu[1], a);
+      } else if (lane == 0) {
+        gsum[2 * ((t * 4 + wave) * PPW + p)] = gu[0];
+        gsum[2 * ((t * 4 + wave) * PPW + p) + 1] = gu[1];
+      }
     }
+  }
+  if constexpr (PPW == 2) return;
+  // with 4 pairs a wave (past 2 tokens): the gated unit (a float64 exp) a (token, pair) a thread over
+  // the workgroup, not by each wave with its lanes computing the same value (at 2 pairs a wave the
+  // barrier costs more than it saves)
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < a.T * 4 * PPW; i += 256) {
+    const uint32_t t = i / (4 * PPW), w = (i / PPW) % 4, p = i % PPW;
+    const int slot = slot_of(sidx, t, a.k, e);
+    const uint32_t pair = (blockIdx.x * 4 + w) * PPW + p;
+    if (slot >= 0 && pair < I) act[((size_t)t * a.k + slot) * I + pair] = gated(gsum[2 * i], gsum[2 * i + 1], a);
   }
 }
 
