@@ -319,10 +319,22 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
     ss = wave_sum_f64_to_63(ss);
     if (lane == 63) red[t >> 6] = ss;
     __syncthreads();
-    ss = 0.0;
+    // r by wave 0 alone (a float64 chain issued by one wave, not by every wave of the workgroup),
+    // handed over in LDS; ss / k by an exponent shift when k is a power of two (the same value)
+    __shared__ float rs;
+    if (t < 64) {
+      ss = 0.0;
 #pragma unroll
-    for (int i = 0; i < WPB; i++) ss += red[i];
-    const float r = (float)(1.0 / sqrt(ss / (double)k + in.eps));
+      for (int i = 0; i < WPB; i++) ss += red[i];
+      double mean;
+      if ((k & (k - 1)) == 0)
+        mean = __builtin_ldexp(ss, -__builtin_ctz(k));
+      else
+        mean = ss / (double)k;
+      if (t == 0) rs = (float)(1.0 / sqrt(mean + in.eps));
+    }
+    __syncthreads();
+    const float r = rs;
 #pragma unroll
     for (int j = 0; j < PER; j++)
       if (t + j * NT < k) xh[t + j * NT] = (f16)f32_value((hv[j] * r) * wv[j]);
