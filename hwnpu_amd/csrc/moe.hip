@@ -254,6 +254,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x
         xr[j][q] = x[xi];
       }
     }
+    float gl = 0.0f, ul = 0.0f;  // PPW == 2: lane p's pair
 #pragma unroll
     for (int p = 0; p < PPW; p++) {
       float gu[2];
@@ -267,13 +268,20 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint4 *__restrict__ x
         }
         gu[r] = group_sum<64>(v) + bias[p][r];
       }
-      const uint32_t pair = pair0 + p;
       if constexpr (PPW == 2) {
-        if (lane == 0 && pair < I) act[((size_t)t * a.k + slot) * I + pair] = gated(gu[0], gu[1], a);
+        if (lane == p) {
+          gl = gu[0];
+          ul = gu[1];
+        }
       } else if (lane == 0) {
         gsum[2 * ((t * 4 + wave) * PPW + p)] = gu[0];
         gsum[2 * ((t * 4 + wave) * PPW + p) + 1] = gu[1];
       }
+    }
+    // PPW == 2: both pairs' gated units (a float64 exp) in one instruction stream, a pair a lane
+    if constexpr (PPW == 2) {
+      const uint32_t pair = pair0 + lane;
+      if (lane < PPW && pair < I) act[((size_t)t * a.k + slot) * I + pair] = gated(gl, ul, a);
     }
   }
   if constexpr (PPW == 2) return;
