@@ -644,12 +644,14 @@ __global__ void k_kv_quantize_i8(const f16 *__restrict__ x, int8_t *__restrict__
   }
 }
 
-// The split of hwk_attn_decode: workgroups of W waves (8 for int8 caches of 8,192 keys or more, else
-// 4: measured fastest for each), each wave kpw keys (a multiple of 16), chunk = W*kpw keys a
+// The split of hwk_attn_decode: workgroups of W waves (8 from 8,192 keys, fp16 caches below 32,768;
+// else 4: measured fastest for each), each wave kpw keys (a multiple of 16), chunk = W*kpw keys a
 // workgroup. kpw is sized so that the launch runs about 2048 waves (8 a CU, each with two tiles of
 // loads in flight), between 32 and 256 keys, more when a head would exceed kMaxChunks chunks. A
 // caller's split (a multiple of 64) is the chunk.
-uint32_t decode_waves(const hwk_attn_params *p) { return p->kv_int8 && p->len >= 8192 ? 8u : 4u; }
+uint32_t decode_waves(const hwk_attn_params *p) {
+  return p->len >= 8192 && (p->kv_int8 || p->len < 32768) ? 8u : 4u;
+}
 
 uint32_t pick_kpw(const hwk_attn_params *p) {
   const uint32_t W = decode_waves(p);
@@ -729,6 +731,9 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
                        ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, kpw, scale_log2);                      \
   else if (p->kv_int8)                                                                                               \
     hipLaunchKernelGGL((k_attn_decode<GG, true, 4>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,   \
+                       ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, kpw, scale_log2);                      \
+  else if (W == 8)                                                                                                   \
+    hipLaunchKernelGGL((k_attn_decode<GG, false, 8>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,  \
                        ws_l, out, mode, pos, len, p->capacity, chunk, nchunk, kpw, scale_log2);                      \
   else                                                                                                               \
     hipLaunchKernelGGL((k_attn_decode<GG, false, 4>), grid, block, 0, st, (const f16 *)q, k, v, ks, vs, ws_o, ws_m,  \
