@@ -497,9 +497,22 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_rows(const uint4 *__restrict
   uint32_t set = blockIdx.x * 4 + (t >> 6);
   const uint32_t sets = (n + RPW - 1) / RPW;
   const bool live = set < sets;
+  // x's chunks (up to 8 a thread) loaded before the weights, the first row set's weight loads
+  // issued unconditionally (a clamped set; a load under a branch is waited for where the branches
+  // join), then x written to LDS (past x's end the last chunk again: the same value, into its own
+  // slot) waiting on x only
+  constexpr int XPT = (TT * 64 * BPL * 4 + 255) / 256, XF = XPT < 8 ? XPT : 8;
+  const uint32_t xn = TT * nb * 4;
+  uint4 xv[XF];
+#pragma unroll
+  for (int j = 0; j < XF; j++) xv[j] = x[min((uint32_t)(t + j * 256), xn - 1)];
+  issue_order();
   RowSet<BPL, RPW> cur, nxt;
-  if (live) load_rowset<64, BPL, RPW>(cur, w, e, set * RPW, n, nb, lane);
-  for (uint32_t i = t; i < TT * nb * 4; i += 256) xs[i] = x[i];
+  load_rowset<64, BPL, RPW>(cur, w, e, min(set, sets - 1) * RPW, n, nb, lane);
+  issue_order();
+#pragma unroll
+  for (int j = 0; j < XF; j++) xs[min((uint32_t)(t + j * 256), xn - 1)] = xv[j];
+  for (uint32_t i = t + XF * 256; i < xn; i += 256) xs[i] = x[i];
   __syncthreads();
   if (!live) return;
   for (;;) {
