@@ -717,7 +717,7 @@ def main():
     floor, _ = read_floor(shapes=[(16, 1), (32, 1), (32, 2)])
     configs = {"c2_int8_gemm": gemm_rate(4),
                "c3_attention": [attn_rate(L, i8) for L in (2048, 32768) for i8 in (False, True)],
-               "c4_moe": [moe_rate(T, 2) for T in (1, 5)],
+               "c4_moe": [moe_rate(T) for T in (1, 5)],
                "k2_i8_gemv": gemv_i8_rate(),
                "k1r_gemv_rows": [gemv_rows_rate(T) for T in (2, 8)]}
     cpu = None
