@@ -117,18 +117,33 @@ template <int TT, bool ONEPASS>
 __global__ __launch_bounds__(256) void k_f16_gemv_rows(const uint4 *__restrict__ w, const uint4 *__restrict__ x,
                                                        void *__restrict__ y, uint32_t n, uint32_t nc, int mode) {
   extern __shared__ uint4 xsr[];  // (TT, nc)
-  for (uint32_t i = threadIdx.x; i < TT * nc; i += 256) xsr[i] = x[i];
-  __syncthreads();
   const int lane = threadIdx.x & 63;
   const uint32_t waves = gridDim.x * 4;
   uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // every load issued unconditionally (a chunk past nc reads the last one; dot4 skips it): a load
+  // under a branch is waited for where the branches join
   auto load4 = [&](uint32_t row, uint32_t base, uint4 (&c)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const uint32_t ch = base + j * 64 + lane;
-      c[j] = ch < nc ? load_stream(&w[(size_t)row * nc + ch]) : make_uint4(0, 0, 0, 0);
+      const uint32_t ch = min(base + j * 64 + lane, nc - 1);
+      c[j] = load_stream(&w[(size_t)row * nc + ch]);
     }
   };
+  // x's chunks (up to 8 a thread) loaded first, then the first row's weights (single pass), then x
+  // written to LDS waiting on x only (past x's end the last chunk again, into its own slot)
+  constexpr int XF = TT < 8 ? TT : 8;
+  const uint32_t xn = TT * nc;
+  uint4 xv[XF];
+#pragma unroll
+  for (int j = 0; j < XF; j++) xv[j] = x[min((uint32_t)(threadIdx.x + j * 256), xn - 1)];
+  issue_order();
+  uint4 cur[4];
+  if constexpr (ONEPASS) load4(min(r, n - 1), 0, cur);
+  issue_order();
+#pragma unroll
+  for (int j = 0; j < XF; j++) xsr[min((uint32_t)(threadIdx.x + j * 256), xn - 1)] = xv[j];
+  for (uint32_t i = threadIdx.x + XF * 256; i < xn; i += 256) xsr[i] = x[i];
+  __syncthreads();
   auto dot4 = [&](const uint4 (&c)[4], uint32_t base, float (&acc)[TT]) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -149,8 +164,6 @@ __global__ __launch_bounds__(256) void k_f16_gemv_rows(const uint4 *__restrict__
     }
   };
   if (r >= n) return;
-  uint4 cur[4];
-  if constexpr (ONEPASS) load4(r, 0, cur);
   for (; r < n; r += waves) {
     float acc[TT];
 #pragma unroll
