@@ -31,22 +31,32 @@ __global__ __launch_bounds__(256) void k_gemv(const uint4 *__restrict__ w, const
 #pragma unroll
   for (int i = 0; i < RPW; i++) acc[i] = 0.0f;
   for (uint32_t base = 0; base < nc; base += LPR * CPL) {
+    // x first, then the weights, every load issued unconditionally from a clamped row / chunk (a
+    // load under a branch is waited for where the branches join); a chunk past nc is zeroed where it
+    // is used, rows past n are not stored
+    uint4 xr[CPL][XQ];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+      const uint32_t ch = min(base + j * LPR + l, nc - 1);
+#pragma unroll
+      for (int q = 0; q < XQ; q++) xr[j][q] = x[(size_t)ch * XQ + q];
+    }
+    issue_order();
     uint4 c[RPW][CPL];
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
-        const uint32_t r = row0 + i * RS, ch = base + j * LPR + l;
-        c[i][j] = (r < n && ch < nc) ? load_stream(&w[(size_t)r * nc + ch]) : make_uint4(0, 0, 0, 0);
+        const uint32_t r = min(row0 + i * RS, n - 1), ch = min(base + j * LPR + l, nc - 1);
+        c[i][j] = load_stream(&w[(size_t)r * nc + ch]);
       }
     }
-    uint4 xr[CPL][XQ];
 #pragma unroll
-    for (int j = 0; j < CPL; j++) {
-      const uint32_t ch = base + j * LPR + l;
+    for (int j = 0; j < CPL; j++)
+      if (base + j * LPR + l >= nc) {
 #pragma unroll
-      for (int q = 0; q < XQ; q++) xr[j][q] = ch < nc ? x[(size_t)ch * XQ + q] : make_uint4(0, 0, 0, 0);
-    }
+        for (int q = 0; q < XQ; q++) xr[j][q] = make_uint4(0, 0, 0, 0);
+      }
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
       float d0 = 0.0f, d1 = 0.0f;
