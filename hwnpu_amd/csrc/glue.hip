@@ -35,8 +35,7 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float *__restrict__ x
   float bv = -__builtin_inff();
   uint32_t bi = 0xffffffffu;
   for (uint64_t i = lo + t; i < hi; i += 256) arg_better(bv, bi, xr[i], (uint32_t)i);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) arg_better(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+  wave_best(bv, bi);
   if (lane == 0) {
     sv[t >> 6] = bv;
     si[t >> 6] = bi;
@@ -56,8 +55,7 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float *__restrict__ x
   const uint32_t lane = threadIdx.x, row = blockIdx.x;
   float bv = part_v[(size_t)row * kArgParts + lane];
   uint32_t bi = part_i[(size_t)row * kArgParts + lane];
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) arg_better(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+  wave_best(bv, bi);
   if (lane == 0) {
     const float x0 = x[(size_t)row * n];
     out[row] = (x0 != x0 || bi == 0xffffffffu) ? 0 : (int32_t)bi;

@@ -160,6 +160,41 @@ __device__ __forceinline__ float group_max_dpp(float v) {
   return v;
 }
 
+// The best (value, index) of the 64 lanes, in every lane: the larger value, on a tie the lower index
+// (a NaN never replaces a pair and the pairs a thread's scan leaves hold none, so each step's choice
+// between a lane's pair and its partner's is the same in both lanes), by DPP and permlane swaps.
+__device__ __forceinline__ void best_of(float &bv, uint32_t &bi, float v, uint32_t i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+__device__ __forceinline__ void wave_best(float &bv, uint32_t &bi) {
+#define HWK_BEST_STEP(ctrl) \
+  best_of(bv, bi, HWK_DPP_ALL(bv, ctrl), __builtin_bit_cast(uint32_t, HWK_DPP_ALL(__builtin_bit_cast(float, bi), ctrl)))
+  HWK_BEST_STEP(0xb1);   // quad_perm [1, 0, 3, 2]
+  HWK_BEST_STEP(0x4e);   // quad_perm [2, 3, 0, 1]
+  HWK_BEST_STEP(0x141);  // row_half_mirror
+  HWK_BEST_STEP(0x140);  // row_mirror
+#undef HWK_BEST_STEP
+  {
+    float va = bv, vb = bv, ia = __builtin_bit_cast(float, bi), ib = ia;
+    swap_rows16(va, vb);  // (even row's, odd row's) of each row pair, in both rows
+    swap_rows16(ia, ib);
+    bv = va;
+    bi = __builtin_bit_cast(uint32_t, ia);
+    best_of(bv, bi, vb, __builtin_bit_cast(uint32_t, ib));
+  }
+  {
+    float va = bv, vb = bv, ia = __builtin_bit_cast(float, bi), ib = ia;
+    swap_rows32(va, vb);  // (lower half's, upper half's), in both halves
+    swap_rows32(ia, ib);
+    bv = va;
+    bi = __builtin_bit_cast(uint32_t, ia);
+    best_of(bv, bi, vb, __builtin_bit_cast(uint32_t, ib));
+  }
+}
+
 // Sum of a value over groups of G lanes (G a power of two up to 64), every lane gets its group's: by
 // DPP and permlane swaps from 8 lanes up, else by LDS shuffles.
 template <int G>

@@ -108,12 +108,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uin
     for (int j = 0; j < kArgPer; j++)
       if (base + t + j * 256 < hi) better(bv, bi, v[j], base + t + j * 256);
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ov = __shfl_xor(bv, off, 64);
-    const uint32_t oi = __shfl_xor(bi, off, 64);
-    better(bv, bi, ov, oi);
-  }
+  wave_best(bv, bi);
   if ((t & 63) == 0) {
     sv[t >> 6] = bv;
     si[t >> 6] = bi;
@@ -140,12 +135,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uin
       v = -__builtin_inff();
       i = 0xffffffffu;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(v, off, 64);
-      const uint32_t oi = __shfl_xor(i, off, 64);
-      better(v, i, ov, oi);
-    }
+    wave_best(v, i);
     if (t == 0) {
       hist[p + 1] = (int32_t)((i == 0xffffffffu || x0 != x0) ? 0 : i);
       *pos = p + 1;
@@ -203,12 +193,7 @@ __global__ __launch_bounds__(1024) void k_argmax_rows(const float *__restrict__ 
   float bv = -__builtin_inff();
   uint32_t bi = 0xffffffffu;
   for (uint32_t i = t; i < n; i += 1024) better(bv, bi, row[i], i);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ov = __shfl_xor(bv, off, 64);
-    const uint32_t oi = __shfl_xor(bi, off, 64);
-    better(bv, bi, ov, oi);
-  }
+  wave_best(bv, bi);
   if ((t & 63) == 0) {
     sv[t >> 6] = bv;
     si[t >> 6] = bi;
