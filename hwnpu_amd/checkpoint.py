@@ -59,7 +59,8 @@ class SafeTensors:
                 raise CheckpointError(f"safetensors: {path}: no header length")
             (n,) = struct.unpack("<Q", raw)
             if n > HEADER_MAX:
-                raise CheckpointError(f"safetensors: {path}: header of {n} bytes is not plausible")
+                raise CheckpointError(f"safetensors: {path}: the header length field says {n} bytes, "
+                                      f"past the {HEADER_MAX >> 20} MiB this reader accepts")
             hdr = self._f.read(n)
             if len(hdr) != n:
                 raise CheckpointError(f"safetensors: {path}: header cut off")
@@ -124,7 +125,7 @@ class SafeTensors:
         if dt == "BF16":
             return (a.astype(np.uint32) << 16).view(np.float32)
         if dt in ("F16", "F32", "F64"):
-            return a.astype(np.float32)
+            return a.astype(np.float32, copy=False)  # F32: the mapped view itself (read-only)
         raise CheckpointError(f"safetensors: {self.path}: {name}: cannot convert {dt} to float32")
 
 
@@ -210,8 +211,21 @@ def write_safetensors(path: str, tensors: dict, metadata: dict | None = None) ->
 
 # ---------------- device copies ----------------
 
+_TORCH = {np.dtype(np.uint8): torch.uint8, np.dtype(np.int8): torch.int8, np.dtype(np.uint16): torch.int16,
+          np.dtype(np.float16): torch.float16, np.dtype(np.float32): torch.float32, np.dtype(np.int32): torch.int32,
+          np.dtype(np.int64): torch.int64, np.dtype(np.float64): torch.float64}
+
+
 def _to_device(a: np.ndarray) -> torch.Tensor:
-    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    """A new device tensor holding a's values, copied straight from a (a read-only view of the mapped
+    file is read in place: no host staging copy; uint16 bit patterns arrive as int16)."""
+    a = np.ascontiguousarray(a)
+    t = torch.empty(a.shape, dtype=_TORCH[a.dtype], device="cuda")
+    if a.nbytes:
+        from .qwen3 import h2d
+
+        h2d(t.data_ptr(), a)
+    return t
 
 
 def _copy_into(ptr: int, nbytes: int, src: torch.Tensor) -> None:
@@ -222,6 +236,16 @@ def _copy_into(ptr: int, nbytes: int, src: torch.Tensor) -> None:
 
     src = src.contiguous()
     d2d(ptr, src.data_ptr(), nbytes)
+
+
+def _host_into(ptr: int, nbytes: int, a: np.ndarray, what: str) -> None:
+    """A host array (a mapped view) straight into the device memory at ptr (exactly nbytes)."""
+    a = np.ascontiguousarray(a)
+    if a.nbytes != nbytes:
+        raise CheckpointError(f"checkpoint: {what}: {a.nbytes} bytes for a slot of {nbytes}")
+    from .qwen3 import h2d
+
+    h2d(ptr, a)
 
 
 # ---------------- MoE experts ----------------
@@ -267,65 +291,98 @@ def load_experts(ck: Checkpoint, names: dict) -> dict:
 
 # ---------------- the Qwen3 decoder ----------------
 
-def _linear(ck: Checkpoint, name: str, rows: int, cols: int):
-    """(codes (rows, cols/32, 16), scales (rows, cols/32)) uint8 on the GPU of the linear `name`
-    (``....q_proj.weight``): its MXFP4 blocks and scales if the checkpoint holds them, else its float
-    matrix encoded on the device."""
+def _linear_into(ck: Checkpoint, name: str, rows: int, cols: int, w_ptr: int, e_ptr: int, stride: int = 1) -> None:
+    """Writes the linear `name` (``....q_proj.weight``) as MXFP4 into device memory: codes (rows,
+    cols/32, 16) at w_ptr, scales (rows, cols/32) at e_ptr, row r at row r*stride of the destination
+    (stride 2: gate/up interleaved row by row). Its MXFP4 blocks and scales go straight from the
+    mapped file if the checkpoint holds them; else its float matrix is copied to the device and
+    encoded there."""
+    from .qwen3 import copy_rows
+
+    nb = cols // 32
     base = name[:-len(".weight")] if name.endswith(".weight") else name
     if ck.has(base + "_blocks"):
+        for part in ("_blocks", "_scales"):
+            dt, _ = ck.info(base + part)
+            if dt != "U8":
+                raise CheckpointError(f"qwen3: {base}{part} is {dt}, want U8")
         w, e = ck.raw(base + "_blocks"), ck.raw(base + "_scales")
-        if tuple(w.shape) != (rows, cols // 32, 16) or tuple(e.shape) != (rows, cols // 32):
+        if tuple(w.shape) != (rows, nb, 16) or tuple(e.shape) != (rows, nb):
             raise CheckpointError(f"qwen3: {base}_blocks/_scales have shapes {tuple(w.shape)} {tuple(e.shape)}, "
-                                  f"want ({rows}, {cols // 32}, 16)")
-        return _to_device(w), _to_device(e)
+                                  f"want ({rows}, {nb}, 16)")
+        w, e = np.ascontiguousarray(w), np.ascontiguousarray(e)
+        copy_rows(w_ptr, stride * nb * 16, w.ctypes.data, nb * 16, nb * 16, rows, 1)
+        copy_rows(e_ptr, stride * nb, e.ctypes.data, nb, nb, rows, 1)
+        return
     dt, shape = ck.info(name)
     if tuple(shape) != (rows, cols):
         raise CheckpointError(f"qwen3: {name} has shape {shape}, want {[rows, cols]}")
     x = _to_device(ck.float32(name))
-    w = torch.empty((rows, cols // 32, 16), dtype=torch.uint8, device="cuda")
-    e = torch.empty((rows, cols // 32), dtype=torch.uint8, device="cuda")
-    hwk.load().hwk_mxfp4_encode(_stream(), x.data_ptr(), w.data_ptr(), e.data_ptr(), rows, cols)
-    return w, e
+    if stride == 1:
+        hwk.load().hwk_mxfp4_encode(_stream(), x.data_ptr(), w_ptr, e_ptr, rows, cols)
+    else:
+        w = torch.empty((rows, nb, 16), dtype=torch.uint8, device="cuda")
+        e = torch.empty((rows, nb), dtype=torch.uint8, device="cuda")
+        hwk.load().hwk_mxfp4_encode(_stream(), x.data_ptr(), w.data_ptr(), e.data_ptr(), rows, cols)
+        copy_rows(w_ptr, stride * nb * 16, w.data_ptr(), nb * 16, nb * 16, rows, 3)
+        copy_rows(e_ptr, stride * nb, e.data_ptr(), nb, nb, rows, 3)
+    torch.cuda.current_stream().synchronize()  # x (and w, e) stay alive until the encode has read them
 
 
-def load_qwen3(model, ck: Checkpoint, prefix: str = "model.") -> None:
-    """Fills a hwnpu_amd.qwen3.Qwen3's weights from a checkpoint of the Hugging Face Qwen3 names."""
+def _tied(ck: Checkpoint, prefix: str, config: dict | None) -> None:
+    """hwk_qwen3 has only a tied head (the embedding rows). The reference reads lm_head.weight instead
+    when the config unties them (internal/llm/qwen3/config.go:142-147); such a checkpoint is refused
+    rather than run with the wrong head."""
+    if config is None:
+        p = os.path.join(os.path.dirname(os.path.abspath(ck.path)), "config.json")
+        if os.path.exists(p):
+            with open(p) as f:
+                config = json.load(f)
+    if config is not None and config.get("tie_word_embeddings", True) is False:
+        raise CheckpointError("qwen3: the config unties the output head (tie_word_embeddings false); "
+                              "hwk_qwen3 has only the tied head")
+    for name in ("lm_head.weight", prefix + "lm_head.weight"):
+        if ck.has(name):
+            raise CheckpointError(f"qwen3: the checkpoint holds {name}, an untied head; hwk_qwen3 has only the tied head")
+
+
+def load_qwen3(model, ck: Checkpoint, prefix: str = "model.", config: dict | None = None) -> None:
+    """Fills a hwnpu_amd.qwen3.Qwen3's weights from a checkpoint of the Hugging Face Qwen3 names.
+    config: the model's config.json as a dict (read from beside the checkpoint when None and present),
+    consulted for tie_word_embeddings."""
+    _tied(ck, prefix, config)
     c = model.cfg
     hd = c.head_dim
-    qn, kn = c.heads * hd, c.kv_heads * hd
+    qn, kn, H, I = c.heads * hd, c.kv_heads * hd, c.hidden, c.inter
     for i in range(c.layers):
         p = f"{prefix}layers.{i}."
-        q = _linear(ck, p + "self_attn.q_proj.weight", qn, c.hidden)
-        k = _linear(ck, p + "self_attn.k_proj.weight", kn, c.hidden)
-        v = _linear(ck, p + "self_attn.v_proj.weight", kn, c.hidden)
-        for part, j in (("blocks", 0), ("scales", 1)):
-            ptr, n = model.tensor(f"layers.{i}.qkv.{part}")
-            _copy_into(ptr, n, torch.cat([q[j], k[j], v[j]], 0))
-        o = _linear(ck, p + "self_attn.o_proj.weight", c.hidden, qn)
-        g = _linear(ck, p + "mlp.gate_proj.weight", c.inter, c.hidden)
-        u = _linear(ck, p + "mlp.up_proj.weight", c.inter, c.hidden)
-        d = _linear(ck, p + "mlp.down_proj.weight", c.hidden, c.inter)
-        for part, j in (("blocks", 0), ("scales", 1)):
-            ptr, n = model.tensor(f"layers.{i}.o.{part}")
-            _copy_into(ptr, n, o[j])
-            gu = torch.stack([g[j], u[j]], 1)  # gate row r at 2r, up row r at 2r+1
-            ptr, n = model.tensor(f"layers.{i}.gate_up.{part}")
-            _copy_into(ptr, n, gu)
-            ptr, n = model.tensor(f"layers.{i}.down.{part}")
-            _copy_into(ptr, n, d[j])
+        qkv_w, _ = model.tensor(f"layers.{i}.qkv.blocks")
+        qkv_e, _ = model.tensor(f"layers.{i}.qkv.scales")
+        for name, row0, rows in (("q", 0, qn), ("k", qn, kn), ("v", qn + kn, kn)):
+            _linear_into(ck, p + f"self_attn.{name}_proj.weight", rows, H, qkv_w + row0 * (H // 2),
+                         qkv_e + row0 * (H // 32))
+        _linear_into(ck, p + "self_attn.o_proj.weight", H, qn, model.tensor(f"layers.{i}.o.blocks")[0],
+                     model.tensor(f"layers.{i}.o.scales")[0])
+        gu_w, _ = model.tensor(f"layers.{i}.gate_up.blocks")
+        gu_e, _ = model.tensor(f"layers.{i}.gate_up.scales")
+        # gate row r at 2r, up row r at 2r+1
+        _linear_into(ck, p + "mlp.gate_proj.weight", I, H, gu_w, gu_e, stride=2)
+        _linear_into(ck, p + "mlp.up_proj.weight", I, H, gu_w + H // 2, gu_e + H // 32, stride=2)
+        _linear_into(ck, p + "mlp.down_proj.weight", H, I, model.tensor(f"layers.{i}.down.blocks")[0],
+                     model.tensor(f"layers.{i}.down.scales")[0])
         for name, t in (("input_layernorm.weight", "input_norm"), ("post_attention_layernorm.weight", "post_norm"),
                         ("self_attn.q_norm.weight", "q_norm"), ("self_attn.k_norm.weight", "k_norm")):
             ptr, n = model.tensor(f"layers.{i}.{t}")
-            _copy_into(ptr, n, _to_device(ck.float32(p + name)))
+            _host_into(ptr, n, ck.float32(p + name), p + name)
     ptr, n = model.tensor("norm")
-    _copy_into(ptr, n, _to_device(ck.float32(prefix + "norm.weight")))
+    _host_into(ptr, n, ck.float32(prefix + "norm.weight"), prefix + "norm.weight")
     ptr, n = model.tensor("embed")
     emb = prefix + "embed_tokens.weight"
     dt, shape = ck.info(emb)
     if tuple(shape) != (c.vocab, c.hidden):
         raise CheckpointError(f"qwen3: {emb} has shape {shape}, want {[c.vocab, c.hidden]}")
     if dt == "F16":
-        _copy_into(ptr, n, _to_device(ck.raw(emb)))
+        _host_into(ptr, n, ck.raw(emb), emb)
     else:  # the fp16 of the float32 value, round to nearest even
         _copy_into(ptr, n, _to_device(ck.float32(emb)).to(torch.float16))
     torch.cuda.synchronize()

@@ -21,6 +21,7 @@ __attribute__((used)) __constant__ uint32_t hwk_co_manifest_count = 2;
 __global__ __launch_bounds__(512) void hwk_co_mxfp4_gemv(const uint4 *__restrict__ w, const uint8_t *__restrict__ e,
                                                          const uint4 *__restrict__ x, f16 *__restrict__ y, uint32_t n,
                                                          uint32_t nb) {
+  if (n == 0) return;        // nothing to read (the runtime launches no grid for n = 0)
   if (nb == 0 || nb > 64) {  // uniform: the whole grid takes this branch
     const uint32_t r = blockIdx.x * 16 + threadIdx.x;
     if (threadIdx.x < 16 && r < n) y[r] = (f16)__builtin_nanf("");

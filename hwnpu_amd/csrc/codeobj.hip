@@ -254,6 +254,9 @@ bool unbundle(const uint8_t *img, size_t n, const uint8_t **elf, size_t *elfn) {
   return false;
 }
 
+// A HIP kernel's explicit arguments fit in 4 KiB.
+constexpr uint32_t kMaxKernargBytes = 4096;
+
 struct KArg {
   uint32_t index, offset, size;
   bool buffer;
@@ -312,6 +315,12 @@ char *parse(const void *image, size_t n, std::vector<Kernel> &out) {
         HWK_CHECK(kind && kind->k == Mp::STR && off && size, "hwk_module_load: kernel %s: malformed argument",
                   kk.name.c_str());
         if (kind->s.rfind("hidden_", 0) == 0) continue;  // filled by the runtime
+        // offsets and sizes are checked in 64 bits against the explicit-argument limit before
+        // they size the host's argument buffer
+        HWK_CHECK(off->k == Mp::INT && size->k == Mp::INT && off->i >= 0 && size->i >= 1 &&
+                      (uint64_t)off->i + (uint64_t)size->i <= kMaxKernargBytes,
+                  "hwk_module_load: kernel %s: argument at offset %lld of %lld bytes (at most %u in all)",
+                  kk.name.c_str(), (long long)off->i, (long long)size->i, kMaxKernargBytes);
         KArg ka;
         ka.index = idx++;
         ka.offset = (uint32_t)off->i;
@@ -365,7 +374,8 @@ struct hwk_module {
 struct hwk_run {
   hwk_module *m;
   const Kernel *k;
-  std::vector<uint8_t> args;  // the explicit argument buffer; unset arguments stay zero
+  std::vector<uint8_t> args;  // the explicit argument buffer; unset value arguments stay zero
+  std::vector<uint8_t> set;   // per argument: set since the run was made (buffers must be)
   char *first_err = nullptr;
   hipEvent_t done = nullptr;
   bool submitted = false;
@@ -475,6 +485,7 @@ HWK_API char *hwk_run_new(hwk_module *m, const char *kernel, hwk_run **out) {
   r->m = m;
   r->k = k;
   r->args.assign((k->kernarg_bytes + 7) & ~7u, 0);
+  r->set.assign(k->args.size(), 0);
   r->done = ev;
   *out = r;
   return nullptr;
@@ -490,6 +501,7 @@ HWK_API char *hwk_run_set_arg(hwk_run *r, uint32_t index, const void *value, siz
     return record(r, hwk::errf("hwk_run_set_arg: argument %u (%s) takes %u bytes, got %zu", index, a->name.c_str(),
                                a->size, value ? n : (size_t)0));
   memcpy(r->args.data() + a->offset, value, n);
+  r->set[index] = 1;
   return nullptr;
 }
 
@@ -509,6 +521,7 @@ HWK_API char *hwk_run_set_buffer_at(hwk_run *r, uint32_t index, hwk_buf *b, size
     return record(r, hwk::errf("hwk_run_set_buffer: buffer argument %s has size %u", a->name.c_str(), a->size));
   const uint64_t addr = (uint64_t)(uintptr_t)b->ptr + off;
   memcpy(r->args.data() + a->offset, &addr, 8);
+  r->set[index] = 1;
   return nullptr;
 }
 
@@ -533,6 +546,11 @@ HWK_API char *hwk_run_submit(hwk_run *r, void *stream) {
     if (q != hipSuccess) return hwk::hip_err("hipEventQuery", q);
   }
   const Kernel &k = *r->k;
+  // A buffer argument left unset would reach the kernel as a null address (on the reference's NPU
+  // an unused buffer is harmless; here every kernel dereferences its buffers).
+  for (size_t i = 0; i < k.args.size(); i++)
+    HWK_CHECK(!k.args[i].buffer || r->set[i], "hwk_run_submit: buffer argument %zu (%s) of %s was never set", i,
+              k.args[i].name.c_str(), k.name.c_str());
   const hwk_co_geometry &g = k.geom;
   uint64_t gx = g.grid_div;
   if (g.grid_arg != HWK_CO_FIXED_GRID) {
@@ -544,14 +562,15 @@ HWK_API char *hwk_run_submit(hwk_run *r, void *stream) {
     const uint64_t cap = (uint64_t)g.grid_per_cu * (uint64_t)r->m->dev->prop.multiProcessorCount;
     if (gx > cap) gx = cap;
   }
-  if (gx == 0) gx = 1;  // an empty problem still runs one workgroup, which sees nothing to do
   HWK_CHECK(gx <= 0x7fffffffu, "hwk_run_submit: grid of %llu workgroups", (unsigned long long)gx);
   std::vector<void *> params(k.args.size());
   for (size_t i = 0; i < k.args.size(); i++) params[i] = r->args.data() + k.args[i].offset;
   HWK_TRY("hipSetDevice", hipSetDevice(r->m->dev->index));
-  HWK_TRY("hipModuleLaunchKernel",
-          hipModuleLaunchKernel(k.fn, (uint32_t)gx, 1, 1, g.block, 1, 1, g.lds_bytes, (hipStream_t)stream,
-                                params.empty() ? nullptr : params.data(), nullptr));
+  // an empty problem (a grid argument of 0) launches nothing; its fence still completes in stream order
+  if (gx > 0)
+    HWK_TRY("hipModuleLaunchKernel",
+            hipModuleLaunchKernel(k.fn, (uint32_t)gx, 1, 1, g.block, 1, 1, g.lds_bytes, (hipStream_t)stream,
+                                  params.empty() ? nullptr : params.data(), nullptr));
   HWK_TRY("hipEventRecord", hipEventRecord(r->done, (hipStream_t)stream));
   r->submitted = true;
   return nullptr;

@@ -713,33 +713,13 @@ __global__ void k_synth_mxfp4(uint8_t *__restrict__ w, uint8_t *__restrict__ e, 
   encode_block(v, w + d * 16, e + d);
 }
 
-// Tuning knobs read once per process: HWK_MXFP4_RPW (row sets of 1, 2, 4 or 8 rows a lane group;
-// default 0: 1 for matrices of fewer rows than half the streaming grid's waves, else 2) and
-// HWK_GEMV_WPC (resident waves a CU the streaming grid is sized for; default 16). The defaults are
-// the fastest decode step of the 28-layer model (2048-row o_proj/down take 1 row a wave) with the
-// 8192-row GEMV of the roofline unchanged (2 rows a wave).
-int env_int(const char *name, int dflt) {
-  const char *s = getenv(name);
-  return s ? atoi(s) : dflt;
-}
-
-int gemv_rpw_env() {
-  static int v = [] {
-    int r = env_int("HWK_MXFP4_RPW", 0);
-    return (r == 1 || r == 2 || r == 4 || r == 8) ? r : 0;
-  }();
-  return v;
-}
-
-// Waves the streaming grid runs: resident waves per CU times the current device's CUs.
+// Waves the streaming grid runs: 16 resident waves a CU times the current device's CUs (the
+// fastest of 8-32 measured on C1's shape and the decode step's).
 uint32_t stream_waves() {
-  static int wpc = [] {
-    int v = env_int("HWK_GEMV_WPC", 16);
-    return v < 1 ? 1 : v > 32 ? 32 : v;
-  }();
+  constexpr int kWavesPerCu = 16;
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  return (uint32_t)(wpc * (cus > 0 ? cus : 256));
+  return (uint32_t)(kWavesPerCu * (cus > 0 ? cus : 256));
 }
 
 template <int LPR, int BPL, int RPW>
@@ -760,14 +740,9 @@ void launch_gemv(hipStream_t st, const void *w, const void *e, const void *x, vo
 template <int LPR, int BPL>
 void launch_rpw(hipStream_t st, const void *w, const void *e, const void *x, void *y, uint32_t n, uint32_t nb,
                 int mode) {
-  int rpw = gemv_rpw_env();
-  if (!rpw) rpw = (n + 1) / 2 < stream_waves() / 2 ? 1 : 2;
-  switch (rpw) {
-    case 1: launch_gemv<LPR, BPL, 1>(st, w, e, x, y, n, nb, mode); break;
-    case 4: launch_gemv<LPR, BPL, 4>(st, w, e, x, y, n, nb, mode); break;
-    case 8: launch_gemv<LPR, BPL, 8>(st, w, e, x, y, n, nb, mode); break;
-    default: launch_gemv<LPR, BPL, 2>(st, w, e, x, y, n, nb, mode); break;
-  }
+  // one row set a lane group for matrices of fewer rows than half the streaming grid's waves, else 2
+  if ((n + 1) / 2 < stream_waves() / 2) launch_gemv<LPR, BPL, 1>(st, w, e, x, y, n, nb, mode);
+  else launch_gemv<LPR, BPL, 2>(st, w, e, x, y, n, nb, mode);
 }
 
 // K1 for rows of 33..256 blocks (64 lanes a row), one row a wave: the most waves in flight, which is
@@ -959,50 +934,15 @@ namespace hwk {
 
 namespace {
 
-// Tuning knob read once a process: HWK_GEMVX_WPB, waves a workgroup of the decode-step GEMV (4, 8 or
-// 16; default 8: x is made once for 8 waves' rows, and the model's shapes still give every CU whole
-// workgroups: qkv 2048 row sets, 256 workgroups; gate_up 6144, 768).
-int gemvx_wpb() {
-  static int v = [] {
-    const int w = env_int("HWK_GEMVX_WPB", 8);
-    return w == 4 || w == 16 ? w : 8;
-  }();
-  return v;
-}
-
-// HWK_GEMVX_RPW: rows a wave takes a pass (2 or 4; default 2).
-int gemvx_rpw() {
-  static int v = [] {
-    const int r = env_int("HWK_GEMVX_RPW", 2);
-    return r == 4 ? 4 : 2;
-  }();
-  return v;
-}
-
-template <int BPL, int XM, bool SWIGLU, int WPB, int RPW, int MODE>
-void launch_x_w(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb) {
+// The decode-step GEMV's workgroups: 8 waves of 2 rows a pass (x is made once for 8 waves' rows, and
+// the model's shapes still give every CU whole workgroups: qkv 2048 row sets, 256 workgroups;
+// gate_up 6144, 768; measured against 4 and 16 waves, and 4 rows a pass).
+template <int BPL, int XM, bool SWIGLU, int MODE>
+void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb) {
+  constexpr int WPB = 8, RPW = 2;
   const uint32_t sets = (n + RPW - 1) / RPW;
   hipLaunchKernelGGL((k_mxfp4_gemv_x<BPL, RPW, XM, SWIGLU, WPB, MODE>), dim3((sets + WPB - 1) / WPB), dim3(64 * WPB), 0,
                      st, (const uint4 *)w, (const uint8_t *)e, in, y, n, nb);
-}
-
-template <int BPL, int XM, bool SWIGLU, int MODE>
-void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb) {
-  const bool r4 = gemvx_rpw() == 4;
-  switch (gemvx_wpb()) {
-    case 4:
-      r4 ? launch_x_w<BPL, XM, SWIGLU, 4, 4, MODE>(st, w, e, in, y, n, nb)
-         : launch_x_w<BPL, XM, SWIGLU, 4, 2, MODE>(st, w, e, in, y, n, nb);
-      break;
-    case 16:
-      r4 ? launch_x_w<BPL, XM, SWIGLU, 16, 4, MODE>(st, w, e, in, y, n, nb)
-         : launch_x_w<BPL, XM, SWIGLU, 16, 2, MODE>(st, w, e, in, y, n, nb);
-      break;
-    default:
-      r4 ? launch_x_w<BPL, XM, SWIGLU, 8, 4, MODE>(st, w, e, in, y, n, nb)
-         : launch_x_w<BPL, XM, SWIGLU, 8, 2, MODE>(st, w, e, in, y, n, nb);
-      break;
-  }
 }
 
 template <int XM, bool SWIGLU, int MODE>

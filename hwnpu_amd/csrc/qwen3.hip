@@ -114,14 +114,15 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uin
     si[t >> 6] = bi;
   }
   __syncthreads();
-  // the partial is stored device-coherent and acknowledged before the block counts itself in; the
-  // last block reads the partials with device-coherent loads (no L2 write-back or invalidate)
+  // The handoff by the memory model: thread 0 stores the block's partial, then counts the block in
+  // with an agent-scope acquire-release add, so every partial store happens before the adds that
+  // follow it in the counter's modification order. The block that draws the last count acquires
+  // all of them; its barrier carries that to the threads that read the partials.
   if (t == 0) {
     for (int w = 1; w < 4; w++) better(bv, bi, sv[w], si[w]);
     __hip_atomic_store(&part_v[blockIdx.x], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&part_i[blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
-    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
   }
   __syncthreads();
   if (!last) return;
@@ -659,7 +660,8 @@ HWK_API char *hwk_qwen3_prefill(hwk_qwen3 *m, void *stream, const int32_t *token
 HWK_API char *hwk_qwen3_step(hwk_qwen3 *m, void *stream) {
   HWK_CHECK(m, "hwk_qwen3_step: null model");
   HWK_CHECK(m->started, "hwk_qwen3_step: no prompt yet");
-  HWK_CHECK(m->host_pos + 1 < m->c.max_ctx, "hwk_qwen3_step: position %u is the last of %u", m->host_pos, m->c.max_ctx);
+  HWK_CHECK((uint64_t)m->host_pos + 1 < m->c.max_ctx, "hwk_qwen3_step: position %u is the last of %u", m->host_pos,
+            m->c.max_ctx);
   HWK_Q(step(m, (hipStream_t)stream));
   m->host_pos++;
   m->verify_n = 0;
@@ -729,7 +731,8 @@ HWK_API char *hwk_qwen3_position(hwk_qwen3 *m, uint32_t *pos) {
 
 HWK_API char *hwk_qwen3_rewind(hwk_qwen3 *m, void *stream, uint32_t pos, int32_t next_token) {
   HWK_CHECK(m, "hwk_qwen3_rewind: null model");
-  HWK_CHECK(pos + 1 < m->c.max_ctx, "hwk_qwen3_rewind: position %u leaves no step in %u", pos, m->c.max_ctx);
+  HWK_CHECK((uint64_t)pos + 1 < m->c.max_ctx, "hwk_qwen3_rewind: position %u leaves no step in %u", pos,
+            m->c.max_ctx);
   HWK_CHECK(next_token < 0 || (uint32_t)next_token < m->c.vocab, "hwk_qwen3_rewind: token %d out of vocab %u",
             next_token, m->c.vocab);
   hipLaunchKernelGGL(k_rewind, dim3(1), dim3(1), 0, (hipStream_t)stream, m->hist, m->pos, pos, next_token);

@@ -26,6 +26,8 @@ def _hiprt():
         lib = C.CDLL("libamdhip64.so")
         lib.hipMemcpy.restype = C.c_int
         lib.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        lib.hipMemcpy2D.restype = C.c_int
+        lib.hipMemcpy2D.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_int]
         _hip = lib
     return _hip
 
@@ -45,6 +47,26 @@ def d2d(dst: int, src: int, nbytes: int) -> None:
     rc = _hiprt().hipMemcpy(C.c_void_p(dst), C.c_void_p(src), nbytes, 3)  # device to device
     if rc != 0:
         raise hwk.HwkError(f"hipMemcpy device to device: error {rc}")
+
+
+def h2d(dst: int, a: np.ndarray) -> None:
+    """A synchronous copy of a C-contiguous host array (a read-only view of a mapped file is fine) into
+    device memory at dst."""
+    if not a.flags.c_contiguous:
+        raise ValueError("h2d: a C-contiguous array")
+    torch.cuda.current_stream().synchronize()
+    rc = _hiprt().hipMemcpy(C.c_void_p(dst), C.c_void_p(a.ctypes.data), a.nbytes, 1)  # host to device
+    if rc != 0:
+        raise hwk.HwkError(f"hipMemcpy host to device: error {rc}")
+
+
+def copy_rows(dst: int, dst_pitch: int, src: int, src_pitch: int, width: int, rows: int, kind: int) -> None:
+    """rows rows of width bytes, src_pitch apart at src, into rows dst_pitch apart at dst
+    (hipMemcpy2D; kind 1 host to device, 3 device to device), synchronously."""
+    torch.cuda.current_stream().synchronize()
+    rc = _hiprt().hipMemcpy2D(C.c_void_p(dst), dst_pitch, C.c_void_p(src), src_pitch, width, rows, kind)
+    if rc != 0:
+        raise hwk.HwkError(f"hipMemcpy2D: error {rc}")
 
 
 def _f64_bits(v: float) -> int:
@@ -138,6 +160,8 @@ class Qwen3:
     def rewind(self, pos: int, next_token: int = -1) -> None:
         """Back to a mark (Rewind, decode.go:1190-1203); next_token >= 0 is written as the token the
         next step takes."""
+        if not 0 <= pos < 2 ** 32:
+            raise ValueError(f"rewind: position {pos} is not a cache position")
         hwk.load().hwk_qwen3_rewind(self._h, _stream(), pos, next_token)
 
     def save(self):

@@ -150,8 +150,15 @@ typedef struct or_qwen3 or_qwen3;
 /* element i of the normal stream keyed by key (splitmix64 + Box-Muller in float64) */
 double or_normal_at(uint64_t key, uint64_t i);
 uint64_t or_fnv64a(const char *s);
-/* the synthetic checkpoint of seed with weight std sd */
+/* the synthetic checkpoint of seed with weight std sd (norm weights 1); sd 0 draws nothing (zero
+ * linears and embedding, for or_qwen3_set to fill) */
 or_qwen3 *or_qwen3_new(const or_qwen3_cfg *cfg, uint64_t seed, float sd, int threads);
+/* replaces the tensor of a Hugging Face Qwen3 name (model.layers.N.{input_layernorm,
+ * post_attention_layernorm,self_attn.{q,k}_norm,self_attn.{q,k,v,o}_proj,mlp.{gate,up,down}_proj}
+ * .weight, model.norm.weight, model.embed_tokens.weight) by n float32 values (row-major (out, in)
+ * for a linear: the values it computes with, e.g. a dequantized MXFP4 matrix; the embedding is
+ * rounded to fp16); 0 on success, -1 for an unknown name, -2 for a wrong count */
+int or_qwen3_set(or_qwen3 *m, const char *name, const float *v, size_t n);
 void or_qwen3_free(or_qwen3 *m);
 /* sums of every linear's code bytes, of their scale bytes, and of the embedding's fp16 bits */
 void or_qwen3_checksums(const or_qwen3 *m, uint64_t out[3]);

@@ -73,6 +73,7 @@ def lib():
             "or_qwen3_free": (None, [P]),
             "or_qwen3_checksums": (None, [P, P]),
             "or_qwen3_run": (C.c_int32, [P, P, C.c_int, C.c_int, P]),
+            "or_qwen3_set": (C.c_int, [P, C.c_char_p, P, C.c_size_t]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -350,6 +351,15 @@ class Qwen3:
         lib().or_qwen3_checksums(self._h, _p(out))
         return [int(v) for v in out]
 
+    def set(self, name: str, values) -> None:
+        """Replaces a tensor by its Hugging Face name (norm weights, linears as the float values they
+        compute with, the embedding); std=0 at construction starts from zero weights."""
+        v = _c(values, np.float32)
+        rc = lib().or_qwen3_set(self._h, name.encode(), _p(v), v.size)
+        if rc:
+            raise ValueError(f"or_qwen3_set({name!r}, {v.size} values): " +
+                             ("unknown name" if rc == -1 else "wrong number of values"))
+
     def run(self, tokens, start):
         toks = _c(tokens, np.int32)
         logits = np.empty(self.vocab, np.float32)
@@ -359,10 +369,6 @@ class Qwen3:
 
 def normal_at(key: int, i: int) -> float:
     return lib().or_normal_at(key, i)
-
-
-def fnv64a(name: str) -> int:
-    return lib().or_fnv64a(name.encode())
 
 
 # ---- the reference's synthetic checkpoint (internal/llm/synth.go:17-35) ----

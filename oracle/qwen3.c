@@ -12,7 +12,11 @@
  * The synthetic checkpoint: each linear's values float32(N(0,1) * std) from the counter stream
  * of its Hugging Face name (splitmix64 at key + (i+1)*gamma, Box-Muller in float64; key = seed ^
  * fnv64a(name)), encoded to MXFP4 (or_mxfp4_encode) and dequantized; the embedding
- * f16(float32(N(0,1) * std)); norm weights 1.
+ * f16(float32(N(0,1) * std)); norm weights 1. With std 0 nothing is drawn: linears and embedding
+ * start at zero. or_qwen3_set then replaces any tensor by its Hugging Face name with a
+ * checkpoint's values, the norm weights included (Qwen3RMSNorm's weight, applied as
+ * (x * r) * w in float32: input_layernorm, post_attention_layernorm, q_norm/k_norm per head before
+ * RoPE, model.norm before the head; qwen3_test.go:155-163,196,205, build.go:108,150,188,283).
  *
  * Test infrastructure only (see oracle.h). */
 #include <math.h>
@@ -56,6 +60,9 @@ struct or_qwen3 {
   float *emb;                           /* f16 values widened (vocab, hidden) */
   float *kc, *vc;                       /* (layers, kv_heads, max_ctx, head_dim), fp16 values */
   float *cos_t, *sin_t;                 /* (max_ctx, head_dim) */
+  float *in_nw, *post_nw;               /* (layers, hidden) */
+  float *q_nw, *k_nw;                   /* (layers, head_dim) */
+  float *final_nw;                      /* (hidden) */
   uint64_t sum_blocks, sum_scales, sum_embed;
 };
 
@@ -99,6 +106,14 @@ or_qwen3 *or_qwen3_new(const or_qwen3_cfg *cfg, uint64_t seed, float sd, int thr
     m->wg[i] = malloc(sizeof(float) * (size_t)c->inter * c->hidden);
     m->wu[i] = malloc(sizeof(float) * (size_t)c->inter * c->hidden);
     m->wd[i] = malloc(sizeof(float) * (size_t)c->hidden * c->inter);
+    if (!(sd > 0)) {
+      memset(m->wqkv[i], 0, sizeof(float) * (size_t)(qn + 2 * kn) * c->hidden);
+      memset(m->wo[i], 0, sizeof(float) * (size_t)c->hidden * qn);
+      memset(m->wg[i], 0, sizeof(float) * (size_t)c->inter * c->hidden);
+      memset(m->wu[i], 0, sizeof(float) * (size_t)c->inter * c->hidden);
+      memset(m->wd[i], 0, sizeof(float) * (size_t)c->hidden * c->inter);
+      continue;
+    }
 #define KEY(n)                                                      \
   (snprintf(name, sizeof name, "model.layers.%d.%s", i, n), seed ^ or_fnv64a(name))
     synth_linear(m, m->wqkv[i], qn, c->hidden, KEY("self_attn.q_proj.weight"), sd);
@@ -115,11 +130,19 @@ or_qwen3 *or_qwen3_new(const or_qwen3_cfg *cfg, uint64_t seed, float sd, int thr
   uint64_t ekey = seed ^ or_fnv64a("model.embed_tokens.weight"), se = 0;
 #pragma omp parallel for schedule(static) num_threads(m->threads) reduction(+ : se)
   for (size_t i = 0; i < ne; i++) {
-    uint16_t b = or_f16_bits((float)(or_normal_at(ekey, i) * (double)sd));
+    uint16_t b = sd > 0 ? or_f16_bits((float)(or_normal_at(ekey, i) * (double)sd)) : 0;
     se += b;
     m->emb[i] = or_f16_value(b);
   }
   m->sum_embed = se;
+  m->in_nw = malloc(sizeof(float) * (size_t)c->layers * c->hidden);
+  m->post_nw = malloc(sizeof(float) * (size_t)c->layers * c->hidden);
+  m->q_nw = malloc(sizeof(float) * (size_t)c->layers * hd);
+  m->k_nw = malloc(sizeof(float) * (size_t)c->layers * hd);
+  m->final_nw = malloc(sizeof(float) * (size_t)c->hidden);
+  for (size_t i = 0; i < (size_t)c->layers * c->hidden; i++) m->in_nw[i] = m->post_nw[i] = 1.0f;
+  for (size_t i = 0; i < (size_t)c->layers * hd; i++) m->q_nw[i] = m->k_nw[i] = 1.0f;
+  for (int i = 0; i < c->hidden; i++) m->final_nw[i] = 1.0f;
   size_t kv = (size_t)c->layers * c->kv_heads * c->max_ctx * hd;
   m->kc = calloc(kv, sizeof(float));
   m->vc = calloc(kv, sizeof(float));
@@ -148,7 +171,51 @@ void or_qwen3_free(or_qwen3 *m) {
   free(m->vc);
   free(m->cos_t);
   free(m->sin_t);
+  free(m->in_nw);
+  free(m->post_nw);
+  free(m->q_nw);
+  free(m->k_nw);
+  free(m->final_nw);
   free(m);
+}
+
+/* The destination of a Hugging Face tensor name: its float32 storage, the row stride and row
+ * count it occupies there (a stacked q/k/v matrix takes its rows at an offset). */
+static float *tensor_of(or_qwen3 *m, const char *name, size_t *count) {
+  const or_qwen3_cfg *c = &m->c;
+  size_t H = (size_t)c->hidden, hd = (size_t)c->head_dim, qn = (size_t)c->heads * hd, kn = (size_t)c->kv_heads * hd,
+         I = (size_t)c->inter;
+  if (!strcmp(name, "model.norm.weight")) return *count = H, m->final_nw;
+  if (!strcmp(name, "model.embed_tokens.weight")) return *count = (size_t)c->vocab * H, m->emb;
+  int li, used = 0;
+  char rest[96];
+  if (sscanf(name, "model.layers.%d.%95s%n", &li, rest, &used) != 2 || name[used] != 0 || li < 0 || li >= c->layers)
+    return NULL;
+  if (!strcmp(rest, "input_layernorm.weight")) return *count = H, m->in_nw + (size_t)li * H;
+  if (!strcmp(rest, "post_attention_layernorm.weight")) return *count = H, m->post_nw + (size_t)li * H;
+  if (!strcmp(rest, "self_attn.q_norm.weight")) return *count = hd, m->q_nw + (size_t)li * hd;
+  if (!strcmp(rest, "self_attn.k_norm.weight")) return *count = hd, m->k_nw + (size_t)li * hd;
+  if (!strcmp(rest, "self_attn.q_proj.weight")) return *count = qn * H, m->wqkv[li];
+  if (!strcmp(rest, "self_attn.k_proj.weight")) return *count = kn * H, m->wqkv[li] + qn * H;
+  if (!strcmp(rest, "self_attn.v_proj.weight")) return *count = kn * H, m->wqkv[li] + (qn + kn) * H;
+  if (!strcmp(rest, "self_attn.o_proj.weight")) return *count = H * qn, m->wo[li];
+  if (!strcmp(rest, "mlp.gate_proj.weight")) return *count = I * H, m->wg[li];
+  if (!strcmp(rest, "mlp.up_proj.weight")) return *count = I * H, m->wu[li];
+  if (!strcmp(rest, "mlp.down_proj.weight")) return *count = H * I, m->wd[li];
+  return NULL;
+}
+
+int or_qwen3_set(or_qwen3 *m, const char *name, const float *v, size_t n) {
+  size_t want = 0;
+  float *dst = tensor_of(m, name, &want);
+  if (!dst) return -1;
+  if (n != want) return -2;
+  if (dst == m->emb) {
+    for (size_t i = 0; i < n; i++) dst[i] = or_f16_value(or_f16_bits(v[i]));
+  } else {
+    memcpy(dst, v, sizeof(float) * n);
+  }
+  return 0;
 }
 
 void or_qwen3_checksums(const or_qwen3 *m, uint64_t out[3]) {
@@ -159,15 +226,15 @@ void or_qwen3_checksums(const or_qwen3 *m, uint64_t out[3]) {
 
 static float f16r(float x) { return or_f16_value(or_f16_bits(x)); }
 
-/* Qwen3RMSNorm rounded to fp16: (x * r) * w, r = float32(1 / sqrt(mean(x^2) + eps)); the
- * synthetic checkpoint's norm weights are 1 (w NULL) */
+/* Qwen3RMSNorm rounded to fp16: (x * r) * w, r = float32(1 / sqrt(mean(x^2) + eps)), with w the
+ * norm's weight (qwen3_test.go:155-163) */
 static void rms_f16(float *out, const float *x, const float *w, int rows, int n, double eps) {
   for (int r = 0; r < rows; r++) {
     const float *xr = x + (size_t)r * n;
     double ss = 0;
     for (int j = 0; j < n; j++) ss += (double)xr[j] * (double)xr[j];
     float inv = (float)(1.0 / sqrt(ss / (double)n + eps));
-    for (int j = 0; j < n; j++) out[(size_t)r * n + j] = f16r((xr[j] * inv) * (w ? w[j] : 1.0f));
+    for (int j = 0; j < n; j++) out[(size_t)r * n + j] = f16r((xr[j] * inv) * w[j]);
   }
 }
 
@@ -194,18 +261,20 @@ static void forward(or_qwen3 *m, const int32_t *tokens, int T, int start, float 
   for (int t = 0; t < T; t++) memcpy(h + (size_t)t * H, m->emb + (size_t)tokens[t] * H, sizeof(float) * H);
   for (int li = 0; li < c->layers; li++) {
     float *kc = m->kc + (size_t)li * nkv * c->max_ctx * hd, *vc = m->vc + (size_t)li * nkv * c->max_ctx * hd;
-    rms_f16(x, h, NULL, T, H, c->eps);
+    rms_f16(x, h, m->in_nw + (size_t)li * H, T, H, c->eps);
     linear(m, qkv, x, m->wqkv[li], T, H, qkv_n);
     for (int t = 0; t < T; t++) {
       int p = start + t;
       float *row = qkv + (size_t)t * qkv_n, tmp[128];
       for (int j = 0; j < nh + nkv; j++) {
         float *v = row + (size_t)j * hd;
-        /* per-head RMSNorm (weights 1) in float32, rounded to fp16 only after RoPE */
+        /* per-head RMSNorm (q_norm for query heads, k_norm for key heads; qwen3_test.go:196) in
+         * float32, rounded to fp16 only after RoPE */
+        const float *nw = (j < nh ? m->q_nw : m->k_nw) + (size_t)li * hd;
         double ss = 0;
         for (int d = 0; d < hd; d++) ss += (double)v[d] * (double)v[d];
         float r = (float)(1.0 / sqrt(ss / (double)hd + c->eps));
-        for (int d = 0; d < hd; d++) tmp[d] = v[d] * r;
+        for (int d = 0; d < hd; d++) tmp[d] = (v[d] * r) * nw[d];
         or_apply_rope(tmp, 1, hd, m->cos_t + (size_t)p * hd, m->sin_t + (size_t)p * hd);
         if (j < nh) {
           for (int d = 0; d < hd; d++) q[((size_t)j * T + t) * hd + d] = f16r(tmp[d]);
@@ -251,7 +320,7 @@ static void forward(or_qwen3 *m, const int32_t *tokens, int T, int start, float 
     free(ll);
     linear(m, y, att, m->wo[li], T, qn, H);
     for (size_t i = 0; i < (size_t)T * H; i++) h[i] += y[i];
-    rms_f16(x, h, NULL, T, H, c->eps);
+    rms_f16(x, h, m->post_nw + (size_t)li * H, T, H, c->eps);
     linear(m, g, x, m->wg[li], T, H, I);
     linear(m, u, x, m->wu[li], T, H, I);
     or_silu_mul(g, g, u, (size_t)T * I);
@@ -274,7 +343,7 @@ int32_t or_qwen3_run(or_qwen3 *m, const int32_t *tokens, int T, int start, float
   const or_qwen3_cfg *c = &m->c;
   float *hl = malloc(sizeof(float) * c->hidden), *x = malloc(sizeof(float) * c->hidden);
   forward(m, tokens, T, start, hl);
-  rms_f16(x, hl, NULL, 1, c->hidden, c->eps);
+  rms_f16(x, hl, m->final_nw, 1, c->hidden, c->eps);
   linear(m, logits, x, m->emb, 1, c->hidden, c->vocab);
   free(hl);
   free(x);

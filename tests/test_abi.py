@@ -100,6 +100,20 @@ def test_bad_arguments_rejected(call, match):
         call(hwk.load())
 
 
+def test_attn_noalloc_refuses_past_scratch():
+    """hwk_attn_decode_noalloc checks its parameters against the library's scratch before any HIP
+    call: split 64 over 1M keys needs 16,384 chunks of 130 floats per query head, past 4 MiB."""
+    import math
+
+    from hwnpu_amd import ops
+
+    p = ops.attn_params(32, 8, 1 << 20, 1 << 20, False, 1 / math.sqrt(128), "f32", 64)
+    need = hwk.load().hwk_attn_workspace_bytes(p)
+    assert need > hwk.ATTN_SCRATCH_BYTES
+    with pytest.raises(hwk.HwkError, match="scratch"):
+        hwk.load().hwk_attn_decode_noalloc(None, FAKE, FAKE, FAKE, None, None, FAKE, p)
+
+
 def test_attn_prefill_rejects_bad_params():
     L = hwk.load()
     p = hwk.AttnParams()

@@ -58,7 +58,7 @@ def test_reader_rejects_bad_files(tmp_path):
     p = tmp_path / "bad.safetensors"
     with open(p, "wb") as f:
         f.write(struct.pack("<Q", 200 << 20))
-    with pytest.raises(CheckpointError, match="not plausible"):
+    with pytest.raises(CheckpointError, match="MiB this reader accepts"):
         SafeTensors(str(p))
     raw_file(p, {"a": {"dtype": "F32", "shape": [4], "data_offsets": [0, 16]}}, b"\0" * 8)
     with pytest.raises(CheckpointError, match="past the end"):
@@ -96,3 +96,40 @@ def test_writer_round_trip_alignment_and_index(tmp_path):
         assert np.array_equal(ck.float32("x"), t["x"][1])
         with pytest.raises(CheckpointError, match="has no"):
             ck.raw("nope")
+
+
+def test_qwen3_loader_refuses_untied_head_and_non_u8_blocks(tmp_path):
+    """hwk_qwen3 has only the tied head: a checkpoint holding lm_head.weight, or one whose config.json
+    says tie_word_embeddings false (the reference then reads lm_head.weight,
+    internal/llm/qwen3/config.go:142-147), is refused before anything touches a device; so are MXFP4
+    blocks or scales stored as anything but U8."""
+    from hwnpu_amd import checkpoint
+
+    class NoModel:  # the checks come before the model is read
+        cfg = None
+
+    p = str(tmp_path / "m.safetensors")
+    write_safetensors(p, {"lm_head.weight": ("F16", np.zeros((4, 32), np.float16))})
+    with Checkpoint(p) as ck, pytest.raises(CheckpointError, match="untied head"):
+        checkpoint.load_qwen3(NoModel(), ck)
+    q = str(tmp_path / "n.safetensors")
+    write_safetensors(q, {"model.norm.weight": ("F32", np.ones(32, np.float32))})
+    with open(tmp_path / "config.json", "w") as f:
+        json.dump({"tie_word_embeddings": False}, f)
+    with Checkpoint(q) as ck, pytest.raises(CheckpointError, match="tie_word_embeddings"):
+        checkpoint.load_qwen3(NoModel(), ck)
+    with Checkpoint(q) as ck, pytest.raises(CheckpointError, match="tie_word_embeddings"):
+        checkpoint.load_qwen3(NoModel(), ck, config={"tie_word_embeddings": False})
+    r = str(tmp_path / "b.safetensors")
+    write_safetensors(r, {"x.q_proj_blocks": ("I8", np.zeros((4, 1, 16), np.int8)),
+                          "x.q_proj_scales": ("U8", np.zeros((4, 1), np.uint8))})
+    with Checkpoint(r) as ck, pytest.raises(CheckpointError, match="want U8"):
+        checkpoint._linear_into(ck, "x.q_proj.weight", 4, 32, 0, 0)
+
+
+def test_reader_refuses_oversized_header_length(tmp_path):
+    p = str(tmp_path / "big.safetensors")
+    with open(p, "wb") as f:
+        f.write(struct.pack("<Q", (100 << 20) + 1) + b"{}")
+    with pytest.raises(CheckpointError, match="MiB"):
+        SafeTensors(p)

@@ -5,7 +5,8 @@ into libhwk's device layouts, checked against the CPU oracle or against the mode
   loads into a fresh model with the same weight checksums and the same greedy tokens.
 - A float checkpoint (F32 and BF16 linears, Hugging Face names) is encoded on the device to MXFP4
   bit-exactly as the oracle's Encode (internal/mxfp4/encode.go:11-78) encodes it, into the stacked
-  q/k/v and interleaved gate/up layout; norms and the fp16 embedding land as they are.
+  q/k/v and interleaved gate/up layout; norms and the fp16 embedding land as they are. The loaded
+  model, whose RMSNorm weights are N(1, 0.1), then runs against the oracle given the same tensors.
 - gpt-oss-named experts with BF16 biases (internal/llm/gptoss/config.go:193-194) run through
   hwk_moe_layer with the gpt-oss unit and match the oracle on the same arrays.
 """
@@ -74,40 +75,52 @@ def test_qwen3_mxfp4_checkpoint_round_trip(dev, tmp_path):
         b.close()
 
 
-def test_qwen3_float_checkpoint_encodes_like_oracle(dev, orc, tmp_path):
-    cfg = dict(SMALL, layers=1, vocab=512)
+LINEARS = ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight", "self_attn.o_proj.weight",
+           "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")
+
+
+def float_checkpoint(cfg, path, seed=9, norm_sd=0.1):
+    """A float Qwen3 checkpoint under Hugging Face names: linears N(0, 0.02) (F32, or BF16 for every
+    other one), every RMSNorm weight N(1, norm_sd) (input, post-attention, q/k per head, final), an
+    F32 embedding. Returns the values the loader sees: {name: float32 array}."""
     hd = cfg["head_dim"]
     qn, kn, H, I = cfg["heads"] * hd, cfg["kv_heads"] * hd, cfg["hidden"], cfg["inter"]
-    rng = np.random.default_rng(9)
-    p = "model.layers.0."
-    W = {"self_attn.q_proj.weight": (qn, H), "self_attn.k_proj.weight": (kn, H), "self_attn.v_proj.weight": (kn, H),
-         "self_attn.o_proj.weight": (H, qn), "mlp.gate_proj.weight": (I, H), "mlp.up_proj.weight": (I, H),
-         "mlp.down_proj.weight": (H, I)}
+    shapes = dict(zip(LINEARS, ((qn, H), (kn, H), (kn, H), (H, qn), (I, H), (I, H), (H, I))))
+    rng = np.random.default_rng(seed)
     t, vals = {}, {}
-    for j, (name, shape) in enumerate(W.items()):
-        x = (rng.standard_normal(shape) * 0.02).astype(np.float32)
-        if j % 2:  # BF16 for half of them: the values the loader sees are the bf16 ones
-            bits = (x.view(np.uint32) >> 16).astype(np.uint16)
-            t[p + name] = ("BF16", bits)
-            x = (bits.astype(np.uint32) << 16).view(np.float32)
-        else:
-            t[p + name] = ("F32", x)
-        vals[name] = x
-    norms = {n: (rng.standard_normal(s) * 0.1 + 1).astype(np.float32) for n, s in
-             (("input_layernorm.weight", H), ("post_attention_layernorm.weight", H), ("self_attn.q_norm.weight", hd),
-              ("self_attn.k_norm.weight", hd))}
-    for n, v in norms.items():
-        t[p + n] = ("F32", v)
-    t["model.norm.weight"] = ("F32", np.ones(H, np.float32))
+    for i in range(cfg["layers"]):
+        p = f"model.layers.{i}."
+        for j, name in enumerate(LINEARS):
+            x = (rng.standard_normal(shapes[name]) * 0.02).astype(np.float32)
+            if j % 2:  # BF16 for half of them: the values the loader sees are the bf16 ones
+                bits = (x.view(np.uint32) >> 16).astype(np.uint16)
+                t[p + name] = ("BF16", bits)
+                x = (bits.astype(np.uint32) << 16).view(np.float32)
+            else:
+                t[p + name] = ("F32", x)
+            vals[p + name] = x
+        for n, size in (("input_layernorm.weight", H), ("post_attention_layernorm.weight", H),
+                        ("self_attn.q_norm.weight", hd), ("self_attn.k_norm.weight", hd)):
+            v = (rng.standard_normal(size) * norm_sd + 1).astype(np.float32)
+            t[p + n], vals[p + n] = ("F32", v), v
+    v = (rng.standard_normal(H) * norm_sd + 1).astype(np.float32)
+    t["model.norm.weight"], vals["model.norm.weight"] = ("F32", v), v
     emb = (rng.standard_normal((cfg["vocab"], H)) * 0.02).astype(np.float32)
-    t["model.embed_tokens.weight"] = ("F32", emb)
-    path = str(tmp_path / "float.safetensors")
+    t["model.embed_tokens.weight"], vals["model.embed_tokens.weight"] = ("F32", emb), emb
     checkpoint.write_safetensors(path, t)
+    return vals
+
+
+def test_qwen3_float_checkpoint_encodes_like_oracle(dev, orc, tmp_path):
+    cfg = dict(SMALL, layers=1, vocab=512)
+    path = str(tmp_path / "float.safetensors")
+    vals = float_checkpoint(cfg, path)
     m = Qwen3(**cfg, max_ctx=64, max_prompt=32)
     try:
         with checkpoint.Checkpoint(path) as ck:
             checkpoint.load_qwen3(m, ck)
-        enc = {n: orc.mxfp4_encode(v) for n, v in vals.items()}
+        p = "model.layers.0."
+        enc = {n: orc.mxfp4_encode(vals[p + n]) for n in LINEARS}
         qkv_w = np.concatenate([enc[f"self_attn.{x}_proj.weight"][0] for x in "qkv"])
         qkv_e = np.concatenate([enc[f"self_attn.{x}_proj.weight"][1] for x in "qkv"])
         assert np.array_equal(dev_bytes(m, "layers.0.qkv.blocks"), qkv_w.reshape(-1))
@@ -119,8 +132,65 @@ def test_qwen3_float_checkpoint_encodes_like_oracle(dev, orc, tmp_path):
         for name, mine in (("self_attn.o_proj.weight", "o"), ("mlp.down_proj.weight", "down")):
             assert np.array_equal(dev_bytes(m, f"layers.0.{mine}.blocks"), enc[name][0].reshape(-1))
             assert np.array_equal(dev_bytes(m, f"layers.0.{mine}.scales"), enc[name][1].reshape(-1))
-        assert np.array_equal(dev_bytes(m, "layers.0.q_norm", np.float32), norms["self_attn.q_norm.weight"])
-        assert np.array_equal(dev_bytes(m, "embed", np.uint16), orc.f32_to_f16(emb).reshape(-1))
+        for hf, mine in (("input_layernorm.weight", "input_norm"), ("post_attention_layernorm.weight", "post_norm"),
+                         ("self_attn.q_norm.weight", "q_norm"), ("self_attn.k_norm.weight", "k_norm")):
+            assert np.array_equal(dev_bytes(m, f"layers.0.{mine}", np.float32), vals[p + hf])
+        assert np.array_equal(dev_bytes(m, "norm", np.float32), vals["model.norm.weight"])
+        assert np.array_equal(dev_bytes(m, "embed", np.uint16), orc.f32_to_f16(vals["model.embed_tokens.weight"]).reshape(-1))
+    finally:
+        m.close()
+
+
+# max_ctx past 16384 takes the decode step's split attention with a separate merge
+@pytest.mark.parametrize("max_ctx", [160, 16500])
+def test_qwen3_float_checkpoint_runs_like_oracle(dev, orc, tmp_path, max_ctx):
+    """A checkpoint-loaded model with real (non-unit) RMSNorm weights, run end to end against the
+    oracle given the same tensors (the linears as the oracle's Encode then Dequantize of the file's
+    values, which the device encoding matches bit for bit above): the prompt (RMSNorm kernel, the
+    prompt's per-head q/k norm + RoPE), eager steps and graph replays (the norm folded into the qkv
+    and gate_up GEMVs, q/k norms in the decode attention's prologue, the final norm), and a verify
+    of three rows. Greedy tokens identical, logits within the model bar (test_qwen3_gpu)."""
+    from test_qwen3_gpu import check_close
+
+    cfg = dict(SMALL)
+    path = str(tmp_path / "float.safetensors")
+    vals = float_checkpoint(cfg, path, seed=21)
+    print(f"float checkpoint {cfg} max_ctx={max_ctx}", flush=True)
+    m = Qwen3(**cfg, max_ctx=max_ctx, max_prompt=64)
+    try:
+        with checkpoint.Checkpoint(path) as ck:
+            checkpoint.load_qwen3(m, ck)
+        ref = orc.Qwen3(**cfg, max_ctx=max_ctx, std=0.0)
+        for name, v in vals.items():
+            if name.endswith("_proj.weight"):
+                v = orc.mxfp4_dequantize(*orc.mxfp4_encode(v)).astype(np.float32)
+            ref.set(name, v)
+        prompt = synth_np.uniform_int(60, 0, cfg["vocab"], "t.ckpt.float.prompt").astype(np.int32)
+        m.prefill(prompt, 0)
+        tok, want = ref.run(prompt, 0)
+        check_close(m.logits(), want, "prefill logits")
+        assert m.history(60, 1)[0] == tok
+        pos = 60
+        for i in range(3):
+            m.step()
+            tok, want = ref.run([tok], pos)
+            check_close(m.logits(), want, f"step {i} logits")
+            pos += 1
+            assert m.history(pos, 1)[0] == tok, f"step {i}"
+        m.decode(8)
+        want_toks = []
+        for i in range(8):
+            tok, want = ref.run([tok], pos + i)
+            want_toks.append(tok)
+        check_close(m.logits(), want, "graph step logits")
+        assert [int(t) for t in m.history(pos + 1, 8)] == want_toks
+        pos += 8
+        rows = [tok, 5, 77]
+        lg, am = m.verify(rows)
+        for j, t in enumerate(rows):
+            wt, want = ref.run([t], pos + j)
+            check_close(lg[j], want, f"verify row {j}")
+            assert int(am[j]) == wt, f"verify row {j}"
     finally:
         m.close()
 

@@ -155,6 +155,31 @@ def test_argument_checks_and_first_error(device, program):
         b.close()
 
 
+def test_unset_buffer_refused_and_empty_grid_launches_nothing(device, program):
+    """A submit with a buffer argument never set is refused before any launch (the kernel would
+    read a null address); a grid argument of 0 launches nothing and its fence still completes."""
+    (w, e, x), (bw, be, bx, by) = _gemv_inputs(device, 16, 2048, 5)
+    np.frombuffer(by.bytes(), np.uint16)[:] = 0x7bff
+    by.sync_to_device()
+    run = program.new_run("hwk_co_mxfp4_gemv")
+    try:
+        run.set_buffer(0, bw).set_buffer(1, be).set_buffer(2, bx).set_uint32(4, 16).set_uint32(5, 64)
+        with pytest.raises(hwk.HwkError, match="never set"):
+            run.submit()
+        run.set_buffer(3, by).set_uint32(4, 0)
+        assert run.submit().wait(60000)
+        by.sync_from_device()
+        assert np.all(np.frombuffer(by.bytes(), np.uint16) == 0x7bff)
+        run.set_uint32(4, 16)
+        assert run.submit().wait(60000)
+        by.sync_from_device()
+        assert not np.any(np.frombuffer(by.bytes(), np.uint16) == 0x7bff)
+    finally:
+        run.close()
+        for b in (bw, be, bx, by):
+            b.close()
+
+
 def test_submit_while_running_refused(device, program):
     """A GEMV run queued behind 2 GB of streaming reads on one stream is still running when it is
     submitted again: the second submit is refused; after its fence it runs again."""

@@ -165,3 +165,31 @@ def test_verify_matches_steps_and_oracle(dev, orc, n_draft):
             m.verify(list(range(9)))  # more than 8 rows
     finally:
         m.close()
+
+
+def test_rewind_and_step_refuse_positions_past_the_cache(dev):
+    """A rewind to 2**32 - 1 (what ctypes makes of -1 for the uint32 argument) is refused by the
+    library before any launch, as is every position without room for a step; the session stays
+    usable afterwards."""
+    from hwnpu_amd import HwkError, hwk
+    from hwnpu_amd.ops import _stream
+
+    m = Qwen3(**dict(SMALL, layers=1, vocab=512), max_ctx=32, max_prompt=16)
+    try:
+        m.synth(seed=0, std=0.02)
+        m.prefill(np.arange(8, dtype=np.int32), 0)
+        for bad in (0xFFFFFFFF, 0xFFFFFFFE, 31, 32):
+            with pytest.raises(HwkError):
+                hwk.load().hwk_qwen3_rewind(m._h, _stream(), bad, -1)
+        with pytest.raises(ValueError):
+            m.rewind(-1)
+        assert m.position() == 8
+        m.rewind(30)
+        m.step()  # position 30 -> 31, the last
+        with pytest.raises(HwkError):
+            m.step()
+        m.rewind(4)
+        m.step()
+        assert m.position() == 5
+    finally:
+        m.close()
