@@ -287,55 +287,55 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const f16 *__restrict__ 
 //
 // Workgroup (kv head h, chunk c) of W waves over the keys [c*chunk, min((c+1)*chunk, p+1)) for the token
 // at position p = *pos; the grid covers the cache's capacity and a workgroup whose chunk starts past p
-// attends no key (the consumer reads only chunks 0 .. p/chunk). Prologue: q for the kv head's G query
-// heads comes from the fp32 projection qkv (heads + 2*kvh rows of 128) through the per-head RMSNorm and
-// RoPE; the workgroup whose chunk holds p (the owner) also makes the new k (normed, rotated) and v,
-// writes them to the caches at p for later steps and keeps them in LDS: the tile holding p takes them
-// from there in place of its load of row p, so the owner waits on no store. The prologue's rows and
-// the waves' first tiles are loaded before the position is read, then the RoPE tables' row p and the
-// second tiles. Each workgroup leaves its partial (o unnormalized, m in natural-log units, l) per
-// query head with plain stores at slot (h*nchunk + c)*G + g; the o_proj GEMV merges them
-// (mxfp4_gemv_x's X_MERGE).
-template <int G, int W>
+// attends no key and leaves a partial of weight 0 (l = 0). Prologue: q for the kv head's G query heads
+// comes from the fp32 projection qkv (heads + 2*kvh rows of 128) through the per-head RMSNorm and RoPE
+// (the step's cos/sin row, cos | sin of 64 values each, made by the step's first kernel); the workgroup
+// whose chunk holds p (the owner) also makes the new k (normed, rotated) and v, writes them to the
+// caches at p for later steps and keeps them in LDS: the tile holding p takes them from there in place
+// of its load of row p, so the owner waits on no store. Every load of the prologue and both tiles is
+// issued before the first wait (the tiles' rows do not depend on p). Each workgroup leaves its partial
+// (o unnormalized, m in natural-log units, l) per query head with plain stores at slot
+// (h*nchunk + c)*G + g; the o_proj GEMV merges them (mxfp4_gemv_x's X_MERGE).
+template <int G, int W, bool ONE>
 __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ qkv, const float *__restrict__ qn,
-                                                      const float *__restrict__ kn, const float *__restrict__ cos_t,
-                                                      const float *__restrict__ sin_t, double eps, f16 *__restrict__ kc,
-                                                      f16 *__restrict__ vc, float *__restrict__ ws_o,
-                                                      float *__restrict__ ws_m, float *__restrict__ ws_l,
-                                                      const int32_t *__restrict__ pos, uint32_t heads, uint32_t kvh,
-                                                      uint32_t cap, uint32_t chunk, uint32_t nchunk, uint32_t kpw,
-                                                      float scale_log2) {
+                                                      const float *__restrict__ kn, const float *__restrict__ rope,
+                                                      double eps, f16 *__restrict__ kc, f16 *__restrict__ vc,
+                                                      float *__restrict__ ws_o, float *__restrict__ ws_m,
+                                                      float *__restrict__ ws_l, const int32_t *__restrict__ pos,
+                                                      uint32_t heads, uint32_t kvh, uint32_t cap, uint32_t chunk,
+                                                      uint32_t nchunk, uint32_t kpw, float scale_log2) {
   __shared__ float sm[W][G], sl[W][G];
   __shared__ float sacc[W][G][128];
   __shared__ __attribute__((aligned(16))) f16 qs[G][128];
   __shared__ __attribute__((aligned(16))) f16 knew[128], vnew[128];
+  kernarg_now(qkv, qn, kn, rope, eps, kc, vc, ws_o, ws_m, ws_l, pos, heads, kvh, cap, chunk, nchunk, kpw, scale_log2);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t h = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
   const uint32_t begin = c * chunk;
   const size_t head_base = (size_t)h * cap;
-  // the position first (written by the previous step's argmax), then the loads that do not depend on
-  // it, none waiting for it: wave j loads prologue job j (query head j < G, then k, then v; a wave
-  // past the jobs repeats the last one, every workgroup loads the k and v jobs and only the owner
-  // keeps them) and its first tile (rows clamped to the capacity); then, the position read, the
-  // RoPE tables' row p and the second tile (loads complete in issue order for the wait counter: the
-  // RoPE waits on the first tile at most)
+  // the position first (written by the previous step's argmax), then every load that does not depend
+  // on it: wave j's prologue job j (query head j < G, then k, then v; a wave past the jobs repeats the
+  // last one, every workgroup loads the k and v jobs and only the owner keeps them), the RoPE row,
+  // and the wave's two tiles (rows clamped to the capacity). Loads complete in issue order for the
+  // wait counter: the position's wait holds nothing else, the RoPE's none of the tiles.
   const int32_t pv = load_first(pos);
   const uint32_t j0 = (uint32_t)wave < (uint32_t)G + 2 ? (uint32_t)wave : (uint32_t)G + 1;
   auto job_row = [&](uint32_t j) { return j < G ? h * G + j : j == G ? heads + h : heads + kvh + h; };
   const float *nwp = j0 < G ? qn : kn;
   const float x0 = qkv[(size_t)job_row(j0) * 128 + lane], x1 = qkv[(size_t)job_row(j0) * 128 + lane + 64];
   const float nw0 = nwp[lane], nw1 = nwp[lane + 64];
+  const float cp = rope[lane], sp = rope[64 + lane];
+  issue_order();
   const uint32_t kb = begin + wave * kpw;
   KTile<false> ta, tb;
   load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, kb, cap, lane);
   issue_order();
-  const uint32_t p = (uint32_t)__builtin_amdgcn_readfirstlane(pv), len = p + 1;
-  const float cp = cos_t[(size_t)p * 64 + lane], sp = sin_t[(size_t)p * 64 + lane];
+  if constexpr (!ONE) load_ktile<false>(tb, kc, vc, nullptr, nullptr, head_base, kb + 16, cap, lane);
   issue_order();
-  load_ktile<false>(tb, kc, vc, nullptr, nullptr, head_base, kb + 16, cap, lane);
+  const uint32_t p = (uint32_t)__builtin_amdgcn_readfirstlane(pv), len = p + 1;
   // a workgroup whose chunk starts past p attends no key (no early exit: the compiler would move the
   // loads above behind the branch, and so behind the read of the position) and leaves a partial of
-  // weight 0, which the merge does not read
+  // weight 0 (l = 0), which the merge skips
   const bool owner = p - begin < chunk;  // the chunk holds p (begin <= p)
   const uint32_t end = begin >= len ? begin : owner ? len : begin + chunk;
   const uint32_t jobs = owner ? G + 2 : G;
@@ -387,28 +387,35 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
   for (int g = 0; g < G; g++)
 #pragma unroll
     for (int d = 0; d < 8; d++) acc[g][d] = 0.0f;
-  uint32_t i = 0, key = kb;
-  for (; i + 3 < nt; i += 2, key += 32) {
-    patch(ta, key);
-    attend_ktile<G, false>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
-    load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
-    patch(tb, key + 16);
-    attend_ktile<G, false>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
-    load_ktile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + 48, cap, lane);
-  }
-  const uint32_t rem = nt - i;  // 0 .. 3
-  if (rem >= 1) {
-    patch(ta, key);
-    attend_ktile<G, false>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
-  }
-  if (rem == 3) load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
-  if (rem >= 2) {
-    patch(tb, key + 16);
-    attend_ktile<G, false>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
-  }
-  if (rem == 3) {
-    patch(ta, key + 32);
-    attend_ktile<G, false>(ta, qb, key + 32, ke, scale_log2, lane, m, ls, acc);
+  if constexpr (ONE) {  // one tile a wave (kpw 16)
+    if (nt) {
+      patch(ta, kb);
+      attend_ktile<G, false>(ta, qb, kb, ke, scale_log2, lane, m, ls, acc);
+    }
+  } else {
+    uint32_t i = 0, key = kb;
+    for (; i + 3 < nt; i += 2, key += 32) {
+      patch(ta, key);
+      attend_ktile<G, false>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
+      load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
+      patch(tb, key + 16);
+      attend_ktile<G, false>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
+      load_ktile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + 48, cap, lane);
+    }
+    const uint32_t rem = nt - i;  // 0 .. 3
+    if (rem >= 1) {
+      patch(ta, key);
+      attend_ktile<G, false>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
+    }
+    if (rem == 3) load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
+    if (rem >= 2) {
+      patch(tb, key + 16);
+      attend_ktile<G, false>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
+    }
+    if (rem == 3) {
+      patch(ta, key + 32);
+      attend_ktile<G, false>(ta, qb, key + 32, ke, scale_log2, lane, m, ls, acc);
+    }
   }
 #pragma unroll
   for (int g = 0; g < G; g++)
@@ -763,7 +770,7 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
 
 // The model step's split: 4 waves a workgroup, kpw keys a wave (32: two tiles, both in flight), chunk =
 // 4*kpw keys; kpw grows past 32 so that a kv head has at most kStepMaxChunks chunks (the o_proj GEMV
-// merges every chunk's partial in its prologue).
+// merges every chunk's partial in its prologue). (Eight waves of one tile each were measured no faster.)
 constexpr int kStepWaves = 4;
 constexpr uint32_t kStepMaxChunks = 16;
 
@@ -781,10 +788,10 @@ size_t hwk::attn_step_workspace_bytes(const hwk_attn_params *p) {
   return (size_t)p->heads * nchunk * (128 + 2) * sizeof(float);
 }
 
-char *hwk::attn_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *cos_t,
-                     const float *sin_t, double eps, void *kc, void *vc, void *workspace, size_t workspace_bytes,
-                     const hwk_attn_params *p, const int32_t *pos) {
-  HWK_CHECK(p && qkv && qn && kn && cos_t && sin_t && kc && vc && workspace && pos, "attn_step: null argument");
+char *hwk::attn_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *rope, double eps,
+                     void *kc, void *vc, void *workspace, size_t workspace_bytes, const hwk_attn_params *p,
+                     const int32_t *pos) {
+  HWK_CHECK(p && qkv && qn && kn && rope && kc && vc && workspace && pos, "attn_step: null argument");
   HWK_CHECK(p->head_dim == 128 && !p->kv_int8, "attn_step: fp16 caches of head_dim 128 only");
   HWK_CHECK(p->kv_heads > 0 && p->heads % p->kv_heads == 0, "attn_step: %u heads over %u", p->heads, p->kv_heads);
   const uint32_t G = p->heads / p->kv_heads;
@@ -797,13 +804,13 @@ char *hwk::attn_step(hipStream_t st, const float *qkv, const float *qn, const fl
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
   constexpr int W = kStepWaves;
   const uint32_t kpw = chunk / W;
-#define HWK_STEP2(GG)                                                                                             \
-  hipLaunchKernelGGL((k_attn_step<GG, W>), dim3(p->kv_heads * nchunk), dim3(64 * W), 0, st, qkv, qn, kn, cos_t,    \
-                     sin_t, eps, (f16 *)kc, (f16 *)vc, ws_o, ws_m, ws_l, pos, p->heads, p->kv_heads, p->capacity,    \
-                     chunk, nchunk, kpw, scale_log2)
-  if (G == 1) HWK_STEP2(1);
-  else if (G == 2) HWK_STEP2(2);
-  else HWK_STEP2(4);
+#define HWK_STEP2(GG, ONE)                                                                                        \
+  hipLaunchKernelGGL((k_attn_step<GG, W, ONE>), dim3(p->kv_heads * nchunk), dim3(64 * W), 0, st, qkv, qn, kn, rope,   \
+                     eps, (f16 *)kc, (f16 *)vc, ws_o, ws_m, ws_l, pos, p->heads, p->kv_heads, p->capacity, chunk,      \
+                     nchunk, kpw, scale_log2)
+  if (G == 1) HWK_STEP2(1, false);
+  else if (G == 2) HWK_STEP2(2, false);
+  else HWK_STEP2(4, false);
 #undef HWK_STEP2
   return hwk::launched("attn_step");
 }

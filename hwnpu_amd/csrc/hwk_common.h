@@ -260,6 +260,20 @@ __device__ __forceinline__ float swiglu_value(float g, float u) {
 // only where a value is used).
 __device__ __forceinline__ void issue_order() { __builtin_amdgcn_sched_barrier(0); }
 
+// Loads the named kernel arguments into SGPRs here, all in one batch with one wait: otherwise the
+// compiler loads each argument where it is first used, and a load issued after an issue_order()
+// fence waits for its argument with a round trip of its own before the global loads behind it issue.
+template <typename T>
+__device__ __forceinline__ int kernarg_one(const T &v) {
+  asm volatile("" ::"s"(v));
+  return 0;
+}
+template <typename... T>
+__device__ __forceinline__ void kernarg_now(const T &...v) {
+  const int d[] = {kernarg_one(v)...};
+  (void)d;
+}
+
 // Store one GEMV/GEMM output per out_mode.
 __device__ __forceinline__ void store_out(void *y, size_t i, float v, int mode) {
   if (mode == HWK_OUT_F16)

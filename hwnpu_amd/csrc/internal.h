@@ -18,10 +18,11 @@ char *mxfp4_gemv_x(hipStream_t st, const void *w, const void *e, const void *x16
 
 // y = W x for MXFP4 W (n, heads*128) with x the fp16 attention output merged from attn_step's partials
 // in the workgroup's prologue (the reference's Merge rule, internal/llm/paged/paged.go:252-310): for
-// query head hq, x = fp16(sum_c w_c o_c / sum_c w_c l_c) over the chunks c <= *pos / chunk with l_c > 0,
-// w_c = exp(m_c - top), top their largest m. nchunk <= 16. y per out_mode.
+// query head hq, x = fp16(sum_c w_c o_c / sum_c w_c l_c) over the chunks c < nchunk with l_c > 0 (a
+// chunk past the position has l = 0), w_c = exp(m_c - top), top their largest m. nchunk <= 16. y per
+// out_mode.
 char *mxfp4_gemv_merge(hipStream_t st, const void *w, const void *e, const void *workspace, uint32_t heads, uint32_t G,
-                       uint32_t chunk, uint32_t nchunk, const int32_t *pos, void *y, uint32_t n, int out_mode);
+                       uint32_t nchunk, void *y, uint32_t n, int out_mode);
 
 // Synthetic MXFP4 rows (hwk_synth_mxfp4's draws) with source row r written at row row0 + r*stride.
 char *synth_mxfp4_rows(hipStream_t st, void *w, void *e, uint32_t rows, uint32_t k, uint64_t key, float stdv,
@@ -36,17 +37,18 @@ char *attn_decode_dev(hipStream_t st, const void *q, const void *k, const void *
                       const void *v_scale, void *out, void *workspace, size_t workspace_bytes,
                       const hwk_attn_params *p, const int32_t *pos, uint32_t len_add);
 
-// The model's decode attention for the token at *pos (k_attn_step): the per-head q/k RMSNorm, RoPE and
-// the KV append in its prologue (q, k, v from the stacked fp32 projection qkv), workgroups of a kv head
-// over chunks of the keys [0, *pos], each leaving its partial (o unnormalized, m in natural-log units,
-// l) per query head at slot (kv head * nchunk + chunk) * G + g of the workspace: o (slots, 128) | m
-// (slots) | l (slots). The chunks past *pos / chunk are not written. attn_step_layout gives the
-// chunking (fixed by the capacity), which the merging consumer needs.
+// The model's decode attention for the token at *pos (k_attn_step): the per-head q/k RMSNorm, RoPE
+// (rope: the position's cos | sin rows, 64 values each) and the KV append in its prologue (q, k, v
+// from the stacked fp32 projection qkv), workgroups of a kv head over chunks of the keys [0, *pos],
+// each leaving its partial (o unnormalized, m in natural-log units, l) per query head at slot
+// (kv head * nchunk + chunk) * G + g of the workspace: o (slots, 128) | m (slots) | l (slots). Every
+// chunk of the capacity is written; a chunk past *pos has l = 0 and weighs nothing in the merge.
+// attn_step_layout gives the chunking (fixed by the capacity), which the merging consumer needs.
 void attn_step_layout(const hwk_attn_params *p, uint32_t *chunk, uint32_t *nchunk);
 size_t attn_step_workspace_bytes(const hwk_attn_params *p);
-char *attn_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *cos_t,
-                const float *sin_t, double eps, void *kc, void *vc, void *workspace, size_t workspace_bytes,
-                const hwk_attn_params *p, const int32_t *pos);
+char *attn_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *rope, double eps,
+                void *kc, void *vc, void *workspace, size_t workspace_bytes, const hwk_attn_params *p,
+                const int32_t *pos);
 
 }  // namespace hwk
 

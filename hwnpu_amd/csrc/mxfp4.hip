@@ -216,8 +216,7 @@ struct XIn {
   const float *nw;
   double eps;
   const float *ws;   // X_MERGE: attn_step's partials, o (slots, 128) | m (slots) | l (slots)
-  const int32_t *pos;
-  uint32_t G, chunk, nchunk;  // query heads a kv head; the partials' chunking
+  uint32_t G, nchunk;  // query heads a kv head; chunks a kv head
 };
 
 // Chunks of attention partials the X_MERGE prologue loads at once when a thread merges more than 4
@@ -250,6 +249,7 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   __shared__ __align__(16) float mm[MS + 64];  // m of (head, chunk); past MS one spare slot a lane
   __shared__ __align__(16) float ml[MS + 64];  // l of (head, chunk)
   __shared__ __align__(16) float mw[MS];       // weight of (head, chunk)
+  kernarg_now(w, e, y, n, nb, in.x16, in.h, in.nw, in.eps, in.ws, in.G, in.nchunk);
   const int t = threadIdx.x, lane = t & 63;
   const uint32_t k = nb * 32;
   const uint32_t r0 = (blockIdx.x * WPB + (t >> 6)) * RPW;
@@ -260,12 +260,12 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   float4 ov[XM == X_MERGE ? M4 : 1][XM == X_MERGE ? MB : 1];
   float mv[XM == X_MERGE ? MPER : 1], lv[XM == X_MERGE ? MPER : 1];
   uint32_t md[XM == X_MERGE ? MPER : 1];
-  uint32_t live = 1;
+  // every chunk of the partials is read: one past the step's position has l = 0 and weighs nothing
+  const uint32_t live = XM == X_MERGE ? in.nchunk : 1;
   if constexpr (XM == X_MERGE) {
-    // the partials of the live chunks: o of this thread's x values (4 consecutive dims of one query
-    // head a group), and every (head, chunk)'s m and l into LDS
+    // the partials: o of this thread's x values (4 consecutive dims of one query head a group), and
+    // every (head, chunk)'s m and l into LDS
     const uint32_t heads = k / 128, slots = heads * in.nchunk;
-    live = min((uint32_t)*in.pos / in.chunk + 1, in.nchunk);
     const float *ws_m = in.ws + (size_t)slots * 128, *ws_l = ws_m + slots;
 #pragma unroll
     for (int j = 0; j < M4; j++) {
@@ -974,7 +974,7 @@ char *mxfp4_gemv_x(hipStream_t st, const void *w, const void *e, const void *x16
   HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "mxfp4_gemv_x: out_mode %d", out_mode);
   HWK_CHECK(aligned(w, 16) && (h || aligned(x16, 16)), "mxfp4_gemv_x: w and x must be 16-byte aligned");
   if (n == 0) return nullptr;
-  XIn in{(const uint4 *)x16, h, nw, eps, nullptr, nullptr, 1, 1, 1};
+  XIn in{(const uint4 *)x16, h, nw, eps, nullptr, 1, 1};
   const uint32_t nb = k / 32;
   if (h) launch_x_mode<X_NORM>(st, w, e, in, y, n, nb, out_mode, swiglu);
   else launch_x_mode<X_F16>(st, w, e, in, y, n, nb, out_mode, swiglu);
@@ -982,17 +982,17 @@ char *mxfp4_gemv_x(hipStream_t st, const void *w, const void *e, const void *x16
 }
 
 char *mxfp4_gemv_merge(hipStream_t st, const void *w, const void *e, const void *workspace, uint32_t heads, uint32_t G,
-                       uint32_t chunk, uint32_t nchunk, const int32_t *pos, void *y, uint32_t n, int out_mode) {
-  HWK_CHECK(w && e && workspace && pos && y, "mxfp4_gemv_merge: null pointer");
+                       uint32_t nchunk, void *y, uint32_t n, int out_mode) {
+  HWK_CHECK(w && e && workspace && y, "mxfp4_gemv_merge: null pointer");
   const uint32_t k = heads * 128;
   HWK_CHECK(heads >= 1 && k <= 64 * 4 * 32, "mxfp4_gemv_merge: %u heads of 128 (at most 8192 values)", heads);
-  HWK_CHECK(G >= 1 && heads % G == 0 && chunk > 0, "mxfp4_gemv_merge: G %u, chunk %u", G, chunk);
+  HWK_CHECK(G >= 1 && heads % G == 0, "mxfp4_gemv_merge: G %u", G);
   HWK_CHECK(nchunk >= 1 && nchunk <= kMergeMaxChunks, "mxfp4_gemv_merge: %u chunks (at most %u)", nchunk,
             kMergeMaxChunks);
   HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "mxfp4_gemv_merge: out_mode %d", out_mode);
   HWK_CHECK(aligned(w, 16) && aligned(workspace, 16), "mxfp4_gemv_merge: w and the workspace 16-byte aligned");
   if (n == 0) return nullptr;
-  XIn in{nullptr, nullptr, nullptr, 0.0, (const float *)workspace, pos, G, chunk, nchunk};
+  XIn in{nullptr, nullptr, nullptr, 0.0, (const float *)workspace, G, nchunk};
   launch_x_mode<X_MERGE>(st, w, e, in, y, n, k / 32, out_mode, false);
   return launched("mxfp4_gemv_merge");
 }

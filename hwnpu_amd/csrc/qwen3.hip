@@ -93,6 +93,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uin
   __shared__ float sv[4];
   __shared__ uint32_t si[4];
   __shared__ bool last;
+  kernarg_now(x, n, part_v, part_i, counter, hist, pos);
   const uint32_t t = threadIdx.x;
   const uint32_t per = (n + kArgBlocks - 1) / kArgBlocks;
   const uint32_t lo = blockIdx.x * per, hi = lo + per < n ? lo + per : n;
@@ -143,6 +144,24 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uin
       __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+}
+
+// The decode step's first kernel: the embedding row of the token hist[*pos] into h (fp32), and the
+// RoPE tables' row *pos into rope_now (cos | sin, 64 values each), so that the step's attention
+// kernels read their cos/sin without first waiting for the position.
+__global__ __launch_bounds__(256) void k_step_embed(const int32_t *__restrict__ hist, const int32_t *__restrict__ pos,
+                                                    const f16 *__restrict__ table, float *__restrict__ h,
+                                                    uint32_t hidden, uint32_t vocab, const float *__restrict__ cos_t,
+                                                    const float *__restrict__ sin_t, float *__restrict__ rope_now) {
+  kernarg_now(hist, pos, table, h, hidden, vocab, cos_t, sin_t, rope_now);
+  const uint32_t p = (uint32_t)*pos;
+  const int32_t id = hist[p];
+  const bool ok = id >= 0 && (uint32_t)id < vocab;
+  const f16 *row = table + (size_t)(ok ? id : 0) * hidden;
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < hidden; i += gridDim.x * 256)
+    h[i] = ok ? (float)row[i] : __builtin_nanf("");
+  if (blockIdx.x == 0 && threadIdx.x < 128)
+    rope_now[threadIdx.x] = threadIdx.x < 64 ? cos_t[(size_t)p * 64 + threadIdx.x] : sin_t[(size_t)p * 64 + threadIdx.x - 64];
 }
 
 uint64_t fnv64a(const std::string &s) {
@@ -241,6 +260,7 @@ struct hwk_qwen3 {
   float *norm;
   f16 *embed;
   float *cos_t, *sin_t;
+  float *rope_now;  // the decode step's cos | sin rows at its position (head_dim/2 values each)
   int32_t *hist, *pos;
   uint32_t *counter, *part_i;
   uint32_t step_chunk = 0, step_nchunk = 0;  // the decode attention's chunking (attn_step_layout)
@@ -307,6 +327,7 @@ void layout(hwk_qwen3 *m, uint8_t *base) {
   m->embed = cv.take<f16>(base, 2ull * c.vocab * c.hidden);
   m->cos_t = cv.take<float>(base, 4ull * c.max_ctx * (c.head_dim / 2));
   m->sin_t = cv.take<float>(base, 4ull * c.max_ctx * (c.head_dim / 2));
+  m->rope_now = cv.take<float>(base, 4ull * c.head_dim);
   m->hist = cv.take<int32_t>(base, 4ull * (c.max_ctx + 1));
   m->pos = cv.take<int32_t>(base, 4);
   m->counter = cv.take<uint32_t>(base, 4);
@@ -342,17 +363,17 @@ char *capture(hwk_qwen3 *m, int i, uint32_t n);
 // The decode step on stream st: the token hist[*pos] at position *pos.
 char *step(hwk_qwen3 *m, hipStream_t st) {
   const hwk_qwen3_config &c = m->c;
-  hipLaunchKernelGGL(k_embed_ids, dim3(embed_blocks(c.hidden), 1), dim3(256), 0, st, m->hist, m->pos, 0u, m->embed,
-                     m->h, c.hidden, c.vocab);
+  hipLaunchKernelGGL(k_step_embed, dim3(embed_blocks(c.hidden)), dim3(256), 0, st, m->hist, m->pos, m->embed, m->h,
+                     c.hidden, c.vocab, m->cos_t, m->sin_t, m->rope_now);
   HWK_Q(hwk::launched("qwen3 embed"));
   for (auto &ly : m->L) {
     HWK_Q(hwk::mxfp4_gemv_x(st, ly.qkv.w, ly.qkv.e, nullptr, m->h, ly.in_norm, m->eps, m->qkv, m->qkv_n, c.hidden,
                             HWK_OUT_F32, false));
     // attention partials over chunks of the cache, merged by the o_proj GEMV into its input
-    HWK_Q(hwk::attn_step(st, m->qkv, ly.q_norm, ly.k_norm, m->cos_t, m->sin_t, m->eps, ly.kc, ly.vc, m->ws, m->ws_bytes,
+    HWK_Q(hwk::attn_step(st, m->qkv, ly.q_norm, ly.k_norm, m->rope_now, m->eps, ly.kc, ly.vc, m->ws, m->ws_bytes,
                          &m->ap, m->pos));
-    HWK_Q(hwk::mxfp4_gemv_merge(st, ly.o.w, ly.o.e, m->ws, c.heads, c.heads / c.kv_heads, m->step_chunk, m->step_nchunk,
-                                m->pos, m->h, c.hidden, HWK_OUT_ADD_F32));
+    HWK_Q(hwk::mxfp4_gemv_merge(st, ly.o.w, ly.o.e, m->ws, c.heads, c.heads / c.kv_heads, m->step_nchunk, m->h,
+                                c.hidden, HWK_OUT_ADD_F32));
     HWK_Q(hwk::mxfp4_gemv_x(st, ly.gu.w, ly.gu.e, nullptr, m->h, ly.post_norm, m->eps, m->a16, 2 * c.inter, c.hidden,
                             HWK_OUT_F16, true));
     HWK_Q(hwk_mxfp4_gemv(st, ly.down.w, ly.down.e, m->a16, m->h, c.hidden, c.inter, HWK_OUT_ADD_F32));
