@@ -18,5 +18,6 @@ struct hwk_co_geometry {
   uint32_t grid_div;     // grid.x = ceil(argument / grid_div) (a fixed grid: grid.x = grid_div)
   uint32_t grid_per_cu;  // grid.x at most grid_per_cu * the device's CUs (0: no cap)
   uint32_t lds_bytes;    // dynamic LDS a workgroup
-  uint32_t reserved[3];
+  uint32_t nullable;     // bit i: buffer argument i may be the null address (hwk_run_set_null)
+  uint32_t reserved[2];
 };

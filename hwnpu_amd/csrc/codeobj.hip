@@ -260,6 +260,7 @@ constexpr uint32_t kMaxKernargBytes = 4096;
 struct KArg {
   uint32_t index, offset, size;
   bool buffer;
+  bool nullable = false;  // the manifest lets the caller pass the null address
   std::string name;
 };
 
@@ -355,6 +356,12 @@ char *parse(const void *image, size_t n, std::vector<Kernel> &out) {
           if (g.grid_arg != HWK_CO_FIXED_GRID)
             HWK_CHECK(g.grid_arg < kk.args.size() && kk.args[g.grid_arg].size == 4 && !kk.args[g.grid_arg].buffer,
                       "hwk_module_load: manifest grid argument %u of %s is not a 4-byte value", g.grid_arg, g.kernel);
+          for (uint32_t i = 0; i < 32; i++) {
+            if (!(g.nullable >> i & 1)) continue;
+            HWK_CHECK(i < kk.args.size() && kk.args[i].buffer,
+                      "hwk_module_load: manifest marks argument %u of %s nullable, which is not a buffer", i, g.kernel);
+            kk.args[i].nullable = true;
+          }
           kk.geom = g;
           kk.has_geom = true;
         }
@@ -465,6 +472,7 @@ HWK_API char *hwk_module_kernel_arg(hwk_module *m, uint32_t kernel, uint32_t arg
   out->offset = a.offset;
   out->size = a.size;
   out->buffer = a.buffer ? 1 : 0;
+  out->nullable = a.nullable ? 1 : 0;
   snprintf(out->name, sizeof out->name, "%s", a.name.c_str());
   snprintf(out->type, sizeof out->type, "%s", type_of(a));
   return nullptr;
@@ -520,6 +528,19 @@ HWK_API char *hwk_run_set_buffer_at(hwk_run *r, uint32_t index, hwk_buf *b, size
   if (a->size != 8)
     return record(r, hwk::errf("hwk_run_set_buffer: buffer argument %s has size %u", a->name.c_str(), a->size));
   const uint64_t addr = (uint64_t)(uintptr_t)b->ptr + off;
+  memcpy(r->args.data() + a->offset, &addr, 8);
+  r->set[index] = 1;
+  return nullptr;
+}
+
+HWK_API char *hwk_run_set_null(hwk_run *r, uint32_t index) {
+  HWK_CHECK(r, "hwk_run_set_null: null run");
+  const KArg *a = arg_of(r, index);
+  if (!a) return record(r, hwk::errf("hwk_run_set_null: kernel %s has no argument %u", r->k->name.c_str(), index));
+  if (!a->buffer || !a->nullable)
+    return record(r, hwk::errf("hwk_run_set_null: argument %u (%s) of %s is not an optional buffer", index,
+                               a->name.c_str(), r->k->name.c_str()));
+  const uint64_t addr = 0;
   memcpy(r->args.data() + a->offset, &addr, 8);
   r->set[index] = 1;
   return nullptr;

@@ -1,379 +1,17 @@
-// Prefill / verify GEMM (K3) on gfx950: Y (M, N) = X (M, K) W^T, X fp16, W int8 per output channel
-// or MXFP4, fp32 accumulation on the fp16 MFMA (v_mfma_f32_16x16x32_f16).
-//
-// A workgroup of 4 waves (one a SIMD, 2 x 2) computes a BM x BN tile of Y; a wave holds a
-// (BM/2) x (BN/2) block of 16 x 16 accumulator tiles. K goes 128 at a time:
-//   X: the tile's 128-column slab goes through LDS (two buffers, one barrier a step), 16-byte chunks
-//      placed at chunk ^ (row & 15) so that the 16 rows one MFMA operand load touches fall in 16
-//      different bank groups (a row is 256 bytes, the width of the 64 banks);
-//   W: each wave loads its own columns' codes straight into registers (16 or 32 bytes a lane per 16
-//      columns a step) and converts them there: int8 exactly to fp16 (the channel scale applied to
-//      the fp32 result), MXFP4 by the hardware fp4 conversion with the block scale folded in.
-// Loads run two steps ahead of the multiply (register stages), so a step's global latency hides
-// behind the two steps before it. A lane's 32 values of K a step are the same set in its X and W
-// operands, so each MFMA sums 32 true products (which lane holds which k is a free choice of the
-// kernel, made for contiguous loads).
-//
-// MXFP4 exactness: a code times its block scale is an fp16 value when the scale's exponent is in
-// [-23, 13]. A row (output channel) whose finite block exponents leave that range is shifted by a
-// power of two s0 chosen per row (the largest exponent mapped to 13) and its fp32 result scaled back
-// by 2^s0, which is exact; rows whose exponents span more than 36 lose the low bits of their
-// smallest blocks (values below 2^-24 of the shifted scale). Scale e = 0 is 0 and e = 255 is +Inf,
-// as in the reference's Dequantize (internal/mxfp4/mxfp4.go:77).
-//
-// Tile order is XCD-aware: the workgroups that share a weight panel run on the same XCD, so its L2
-// holds the panel once; the host picks the tile shape that fills the 256 CUs best.
+// Prefill / verify GEMM (K3) on gfx950: the kernels of hwk_i8_gemm and hwk_mxfp4_gemm and the choice
+// of tile shape (the device code is in gemm_kernels.h).
+#include "gemm_kernels.h"
 #include "hwk_common.h"
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int KS = 128;     // K a step
-constexpr int CH = KS / 8;  // 16-byte chunks of an X row a step
-constexpr int KK = KS / 32;  // MFMAs a step for one (16-row, 16-column) tile
-constexpr int NS = 2;       // register stages: loads run NS steps ahead
-constexpr int kOutSwiGLU = HWK_OUT_SWIGLU_F16;
-
-// 4 int8 codes (one dword) as 4 exact fp16 values (two dwords).
-__device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t w) {
-  const uint32_t u = w ^ 0x80808080u;
-  const h2 bias = {(f16)1152.0f, (f16)1152.0f};
-  const h2 lo = h2_of_bits(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
-  const h2 hi = h2_of_bits(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
-  return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-}
-
-// 8 int8 codes (two dwords) as a half8 operand.
-__device__ __forceinline__ half8 i8x8_to_half8(uint32_t a, uint32_t b) {
-  const uint2 p = i8x4_to_f16x4(a), q = i8x4_to_f16x4(b);
-  const u32x4 v = {p.x, p.y, q.x, q.y};
-  return __builtin_bit_cast(half8, v);
-}
-
-// 8 e2m1 codes (one dword, even element in the low nibble) times scale s as a half8 operand.
-__device__ __forceinline__ half8 fp4x8_to_half8(uint32_t w, float s) {
-  const u32x4 v = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0)),
-                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 1)),
-                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 2)),
-                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 3))};
-  return __builtin_bit_cast(half8, v);
-}
-
-__device__ __forceinline__ u32x4 load16(const void *p) { return *(const u32x4 *)p; }
-
-// The X chunk (of CH a row a step) that MFMA kk of lane group q reads: the k offsets of a lane's
-// operands in the step. int8: two 16-byte weight loads a lane at q*16 and 64 + q*16 (each 16 rows x 64
-// contiguous bytes a load instruction); MXFP4: one 32-value block a lane at q*32.
-template <bool MX>
-__device__ __forceinline__ int xchunk(int q, int kk) {
-  if constexpr (MX) return 4 * q + kk;
-  return kk < 2 ? 2 * q + kk : 8 + 2 * q + (kk - 2);
-}
+using namespace hwk_gemm;
 
 template <int BM, int BN, bool MX, int WM, int WN>
-struct Cfg {
-  static constexpr int NT = 64 * WM * WN;                   // threads: WM x WN waves over the tile
-  static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16 x 16 tiles a wave
-  static constexpr int AL = BM * CH / NT;                   // X chunks a thread stages a step
-  static constexpr int BL = MX ? 1 : 2;                     // 16-byte weight loads a lane a step a tile
-  static_assert(BM * CH % NT == 0 && TM * WM * 16 == BM && TN * WN * 16 == BN, "tile shape");
-};
-
-template <int BM, int BN, bool MX, int WM, int WN>
-struct Stage {
-  u32x4 a[Cfg<BM, BN, MX, WM, WN>::AL];
-  u32x4 b[Cfg<BM, BN, MX, WM, WN>::TN][Cfg<BM, BN, MX, WM, WN>::BL];
-  uint32_t e[Cfg<BM, BN, MX, WM, WN>::TN];  // MXFP4 block scale bytes
-  uint32_t k0;                      // the step's K offset
-};
-
-// Issue the global loads of the step at K offset k0 into s: X (load_x) and the weights (load_w).
-// Out-of-range rows and columns read the last row/column (their results are not stored); K past the
-// end reads in-range data, which zero_tail clears when the stage is consumed (a select here would wait
-// for the load at once). Every load is issued unconditionally (a load under a branch would be waited
-// for at the join).
-template <int BM, int BN, bool MX, int WM, int WN>
-__device__ __forceinline__ void load_x(Stage<BM, BN, MX, WM, WN> &s, const u32x4 *__restrict__ X, uint32_t M, uint32_t K,
-                                       uint32_t m0, uint32_t k0, int t) {
-  using C = Cfg<BM, BN, MX, WM, WN>;
-  s.k0 = k0;
-#pragma unroll
-  for (int i = 0; i < C::AL; i++) {
-    const int c = t + C::NT * i, row = c / CH, ch = c % CH;
-    const uint32_t m = min(m0 + row, M - 1);
-    s.a[i] = X[((size_t)m * K + min(k0 + ch * 8, K - 8)) / 8];
-  }
-}
-
-template <int BM, int BN, bool MX, int WM, int WN>
-__device__ __forceinline__ void load_w(Stage<BM, BN, MX, WM, WN> &s, const uint8_t *__restrict__ W,
-                                       const uint8_t *__restrict__ E, uint32_t K, uint32_t k0,
-                                       const uint32_t (&brow)[Cfg<BM, BN, MX, WM, WN>::TN], int q) {
-  using C = Cfg<BM, BN, MX, WM, WN>;
-  if constexpr (MX) {
-    const uint32_t blk = min(k0 + q * 32, K - 32) / 32;
-#pragma unroll
-    for (int j = 0; j < C::TN; j++) {
-      const size_t bi = (size_t)brow[j] * (K / 32) + blk;
-      s.b[j][0] = load16(W + bi * 16);
-      s.e[j] = E[bi];
-    }
-  } else {
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const uint32_t kc = min(k0 + h * 64 + q * 16, K - 16);
-#pragma unroll
-      for (int j = 0; j < C::TN; j++) s.b[j][h] = load16(W + (size_t)brow[j] * K + kc);
-    }
-  }
-}
-
-// A step reaching past K: its X chunks and weight loads past K become zeros (MXFP4: scale 0).
-template <int BM, int BN, bool MX, int WM, int WN>
-__device__ __forceinline__ void zero_tail(Stage<BM, BN, MX, WM, WN> &s, uint32_t K, int t, int q) {
-  using C = Cfg<BM, BN, MX, WM, WN>;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int i = 0; i < C::AL; i++)
-    if (s.k0 + ((t + C::NT * i) % CH) * 8 >= K) s.a[i] = zero;
-#pragma unroll
-  for (int j = 0; j < C::TN; j++) {
-    if constexpr (MX) {
-      if (s.k0 + q * 32 >= K) {
-        s.b[j][0] = zero;
-        s.e[j] = 0u;
-      }
-    } else {
-#pragma unroll
-      for (int h = 0; h < 2; h++)
-        if (s.k0 + h * 64 + q * 16 >= K) s.b[j][h] = zero;
-    }
-  }
-}
-
-// The block scale of exponent byte e in a row shifted by 2^-s0 (see the header): 0 for e = 0 or a
-// shifted exponent below the float range, +Inf for e = 255.
-__device__ __forceinline__ float shifted_scale(uint32_t e, int s0) {
-  const float v = __uint_as_float((uint32_t)max((int)e - s0, 0) << 23);  // below the float range: +0
-  return e == 255u ? __builtin_inff() : e == 0u ? 0.0f : v;
-}
-
-// The row shifts s0 of the tile's BN weight rows (n0 .. n0+BN-1, clamped to N-1): 0 for a row whose
-// finite, nonzero block exponents are all in [-23, 13]; else the largest mapped to 13. The workgroup's
-// threads scan the rows' scale bytes (16-byte chunks when every row starts 16-byte aligned, all of a
-// thread's loads issued before any is used; bytes otherwise) and combine per row in LDS (hs: the
-// largest exponent byte other than 255, ls: the smallest other than 0 and 255). hs and ls are set
-// to 0 and 255 by the caller before a barrier; another barrier follows before they are read.
-template <int BN, int NT>
-__device__ __forceinline__ void scan_shifts(const uint8_t *__restrict__ E, uint32_t n0, uint32_t N, uint32_t nb,
-                                            bool quads, int t, int *hs, int *ls) {
-  auto take = [&](uint32_t e, uint32_t &h, uint32_t &l) {
-    h = max(h, e == 255u ? 0u : e);
-    l = min(l, (e == 0u || e == 255u) ? 255u : e);
-  };
-  if (quads) {
-    const uint32_t nch = nb / 16, total = BN * nch;
-    for (uint32_t base = 0; base < total; base += 4 * NT) {
-      u32x4 v[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t c = min(base + t + NT * i, total - 1), row = c / nch;
-        v[i] = *(const u32x4 *)(E + (size_t)min(n0 + row, N - 1) * nb + (c % nch) * 16);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t c = base + t + NT * i;
-        if (c >= total) continue;
-        uint32_t h = 0, l = 255;
-#pragma unroll
-        for (int w = 0; w < 4; w++)
-#pragma unroll
-          for (int b = 0; b < 4; b++) take((v[i][w] >> (8 * b)) & 255u, h, l);
-        atomicMax(&hs[c / nch], (int)h);
-        atomicMin(&ls[c / nch], (int)l);
-      }
-    }
-  } else {
-    for (uint32_t c = t; c < BN * nb; c += NT) {
-      const uint32_t row = c / nb;
-      uint32_t h = 0, l = 255;
-      take(E[(size_t)min(n0 + row, N - 1) * nb + c % nb], h, l);
-      atomicMax(&hs[row], (int)h);
-      atomicMin(&ls[row], (int)l);
-    }
-  }
-}
-
-// The shift of a row from its scanned bytes.
-__device__ __forceinline__ int shift_of(int hi, int lo) {
-  if (hi == 0) return 0;  // no finite nonzero scale
-  const int emax = hi - 127, emin = lo - 127;
-  return (emax <= 13 && emin >= -23) ? 0 : emax - 13;
-}
-
-// Workgroup id -> tile: consecutive ids go round the XCDs, so ids x, x+8, x+16, ... share an XCD;
-// those take the M tiles of one N panel in turn.
-__device__ __forceinline__ void tile_of(uint32_t id, uint32_t mt, uint32_t nt, uint32_t &tm, uint32_t &tn) {
-  const uint32_t total = mt * nt;
-  const uint32_t xcd = id % 8, j = id / 8;
-  uint32_t lin = id;
-  if (total % 8 == 0) {
-    const uint32_t per = total / 8;  // tiles an XCD runs
-    lin = xcd * per + j;
-  }
-  tn = lin / mt;
-  tm = lin % mt;
-}
-
-template <int BM, int BN, bool MX, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MX && WM * WN == 4 ? 2 : 1))) void k_gemm(const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
-                                             const uint8_t *__restrict__ E, const uint16_t *__restrict__ S,
-                                             void *__restrict__ Y, uint32_t M, uint32_t N, uint32_t K, int mode,
-                                             bool equads) {
-  using C = Cfg<BM, BN, MX, WM, WN>;
-  constexpr int TM = C::TM, TN = C::TN, NT = C::NT;
-  __shared__ __attribute__((aligned(16))) u32x4 As[2][BM * CH];
-  __shared__ int hs[MX ? BN : 1], ls[MX ? BN : 1];  // the row shift scan (MXFP4)
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int r16 = lane & 15, q = lane >> 4;
-  uint32_t tm, tn;
-  tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
-  const uint32_t m0 = tm * BM, n0 = tn * BN;
-  const uint32_t nw = n0 + wn * (BN / WN);  // the wave's first column
-  uint32_t brow[TN];
-#pragma unroll
-  for (int j = 0; j < TN; j++) brow[j] = min(nw + j * 16 + r16, N - 1);
-
-  const uint32_t steps = (K + KS - 1) / KS;
-  auto kofs = [&](uint32_t j) -> uint32_t { return min(j, steps) * KS; };  // past the end: reads zeros
-  Stage<BM, BN, MX, WM, WN> st[NS];
-#pragma unroll
-  for (int s = 0; s < NS; s++) {
-    load_x<BM, BN, MX, WM, WN>(st[s], X, M, K, m0, kofs(s), t);
-    load_w<BM, BN, MX, WM, WN>(st[s], W, E, K, kofs(s), brow, q);
-  }
-  int s0[TN];
-#pragma unroll
-  for (int j = 0; j < TN; j++) s0[j] = 0;
-  if constexpr (MX) {
-    if (t < BN) {
-      hs[t] = 0;
-      ls[t] = 255;
-    }
-    __syncthreads();
-    scan_shifts<BN, NT>(E, n0, N, K / 32, equads, t, hs, ls);
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-      const uint32_t r = brow[j] - n0;
-      s0[j] = shift_of(hs[r], ls[r]);
-    }
-  }
-
-  floatx4 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int j = 0; j < TN; j++) acc[i][j] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
-
-  // Steps in groups of NS (a partial last group multiplies zeros: its loads read past K). A step:
-  // its X slab into LDS, barrier, the next X loads of its stage, then for each kk its weight operands
-  // converted next to the MFMAs that take them (the VALU work overlaps the matrix core), then the
-  // next weight loads of its stage. Issue order is pinned: the wait counter is in order, so a stage
-  // consumed before the loads behind it is waited for without waiting for them.
-  for (uint32_t j0 = 0; j0 < steps; j0 += NS) {
-#pragma unroll
-    for (int s = 0; s < NS; s++) {
-      const uint32_t j = j0 + s;
-      u32x4 *buf = As[s & 1];  // NS is even: step j uses buffer j & 1
-      if (st[s].k0 + KS > K) zero_tail<BM, BN, MX, WM, WN>(st[s], K, t, q);  // uniform: only a ragged step
-#pragma unroll
-      for (int i = 0; i < C::AL; i++) {
-        const int c = t + NT * i, row = c / CH, ch = c % CH;
-        buf[row * CH + (ch ^ (row & 15))] = st[s].a[i];
-      }
-      __syncthreads();
-      issue_order();
-      load_x<BM, BN, MX, WM, WN>(st[s], X, M, K, m0, kofs(j + NS), t);
-      issue_order();
-      float sc[TN];
-#pragma unroll
-      for (int jn = 0; jn < TN; jn++) sc[jn] = MX ? shifted_scale(st[s].e[jn], s0[jn]) : 0.0f;
-      // the operands of kk + 1 (X from LDS, weights converted) are fetched before the MFMAs of kk
-      auto operands = [&](half8 (&af)[TM], half8 (&bf)[TN], int kk) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-          const int row = wm * (BM / WM) + i * 16 + r16;
-          af[i] = __builtin_bit_cast(half8, buf[row * CH + (xchunk<MX>(q, kk) ^ (row & 15))]);
-        }
-#pragma unroll
-        for (int jn = 0; jn < TN; jn++) {
-          if constexpr (MX) {
-            bf[jn] = fp4x8_to_half8(st[s].b[jn][0][kk], sc[jn]);
-          } else {
-            const u32x4 v = st[s].b[jn][kk >> 1];
-            bf[jn] = i8x8_to_half8(v[(kk & 1) * 2], v[(kk & 1) * 2 + 1]);
-          }
-        }
-      };
-      half8 af[2][TM], bf[2][TN];
-      operands(af[0], bf[0], 0);
-#pragma unroll
-      for (int kk = 0; kk < KK; kk++) {
-        if (kk + 1 < KK) operands(af[(kk + 1) & 1], bf[(kk + 1) & 1], kk + 1);
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-          for (int jn = 0; jn < TN; jn++)
-            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[kk & 1][i], bf[kk & 1][jn], acc[i][jn], 0, 0, 0);
-      }
-      issue_order();
-      load_w<BM, BN, MX, WM, WN>(st[s], W, E, K, kofs(j + NS), brow, q);
-      issue_order();
-    }
-  }
-  // D of tile (i, j): lane holds rows q*4 + r, column r16
-  if (mode == kOutSwiGLU) {
-    // columns (2c, 2c+1) are (gate, up) of output c, held by lanes r16 and r16 ^ 1 for the same four
-    // rows: the gate lane takes the up values of rows 0, 1 and computes those outputs, the up lane
-    // takes the gate values of rows 2, 3 and computes those. Every lane joins the swaps; columns past
-    // N (a tile wider than N) store nothing, and with N % 16 == 0 a pair is wholly below N or not.
-    const bool gate = (r16 & 1) == 0;
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-      const uint32_t n = nw + j * 16 + r16, c = n / 2;
-      const float sc = MX ? 1.0f : (float)__builtin_bit_cast(f16, S[min(n, N - 1)]);
-#pragma unroll
-      for (int i = 0; i < TM; i++) {
-        float v[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) v[r] = MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc;
-        const float o0 = __shfl_xor(gate ? v[2] : v[0], 1, 64), o1 = __shfl_xor(gate ? v[3] : v[1], 1, 64);
-        const uint32_t mr = m0 + wm * (BM / WM) + i * 16 + q * 4 + (gate ? 0 : 2);  // the lane's first row
-        const float y0 = gate ? swiglu_value(v[0], o0) : swiglu_value(o0, v[2]);
-        const float y1 = gate ? swiglu_value(v[1], o1) : swiglu_value(o1, v[3]);
-        if (n < N && mr < M) ((f16 *)Y)[(size_t)mr * (N / 2) + c] = (f16)y0;
-        if (n < N && mr + 1 < M) ((f16 *)Y)[(size_t)(mr + 1) * (N / 2) + c] = (f16)y1;
-      }
-    }
-    return;
-  }
-#pragma unroll
-  for (int j = 0; j < TN; j++) {
-    const uint32_t n = nw + j * 16 + r16;
-    if (n >= N) continue;
-    const float sc = MX ? 1.0f : (float)__builtin_bit_cast(f16, S[n]);
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint32_t m = m0 + wm * (BM / WM) + i * 16 + q * 4 + r;
-        if (m < M) store_out(Y, (size_t)m * N + n, MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc, mode);
-      }
-  }
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MX && WM * WN == 4 ? 2 : 1))) void k_gemm(
+    const u32x4 *__restrict__ X, const uint8_t *__restrict__ W, const uint8_t *__restrict__ E,
+    const uint16_t *__restrict__ S, void *__restrict__ Y, uint32_t M, uint32_t N, uint32_t K, int mode, bool equads) {
+  gemm_wg<BM, BN, MX, WM, WN>(blockIdx.x, X, W, E, S, Y, M, N, K, mode, equads);
 }
 
 // The tile shape for (m, n): the fewest rounds of workgroups over the CUs, a round weighted by the

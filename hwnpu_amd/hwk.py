@@ -12,7 +12,7 @@ import ctypes as C
 import os
 import threading
 
-ABI = 3
+ABI = 4
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libhwk.so")
@@ -65,8 +65,8 @@ class KernelInfo(C.Structure):
 
 class KernelArg(C.Structure):
     """hwk_kernel_arg (include/hwk.h)."""
-    _fields_ = [("index", U32), ("offset", U32), ("size", U32), ("buffer", U32), ("name", C.c_char * 64),
-                ("type", C.c_char * 32)]
+    _fields_ = [("index", U32), ("offset", U32), ("size", U32), ("buffer", U32), ("nullable", U32),
+                ("name", C.c_char * 64), ("type", C.c_char * 32)]
 
 
 class Qwen3Config(C.Structure):
@@ -108,6 +108,7 @@ SIGNATURES = {
     "hwk_run_set_arg": (ERR, [P, U32, P, SZ]),
     "hwk_run_set_buffer": (ERR, [P, U32, P]),
     "hwk_run_set_buffer_at": (ERR, [P, U32, P, SZ, SZ]),
+    "hwk_run_set_null": (ERR, [P, U32]),
     "hwk_run_err": (ERR, [P]),
     "hwk_run_submit": (ERR, [P, P]),
     "hwk_run_wait": (ERR, [P, U32, C.POINTER(C.c_int)]),

@@ -31,6 +31,7 @@ class KernelArg:
     offset: int
     size: int
     buffer: bool
+    nullable: bool = False  # an optional buffer: Run.set_null passes the null address
 
 
 @dataclass
@@ -138,7 +139,8 @@ class Program:
             for a in range(ki.args):
                 ka = hwk.KernelArg()
                 L.hwk_module_kernel_arg(self._h, i, a, C.byref(ka))
-                args.append(KernelArg(ka.index, ka.name.decode(), ka.type.decode(), ka.offset, ka.size, bool(ka.buffer)))
+                args.append(KernelArg(ka.index, ka.name.decode(), ka.type.decode(), ka.offset, ka.size, bool(ka.buffer),
+                                      bool(ka.nullable)))
             out.append(KernelInfo(ki.name.decode(), args, ki.cus, ki.block, ki.kernarg_bytes, bool(ki.runnable)))
         return out
 
@@ -195,6 +197,10 @@ class Run:
 
     def set_buffer_at(self, index: int, b: Buffer, off: int, n: int) -> "Run":
         return self._set(hwk.load().hwk_run_set_buffer_at, index, b._h if b else None, off, n)
+
+    def set_null(self, index: int) -> "Run":
+        """An optional buffer argument (KernelArg.nullable) set to the null address."""
+        return self._set(hwk.load().hwk_run_set_null, index)
 
     def err(self) -> str | None:
         try:

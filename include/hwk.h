@@ -29,7 +29,7 @@ extern "C" {
 
 /* The ABI version: a binding refuses a library of another (reference xrtshim.h:25-26, the XS_ABI
  * check of internal/backend/amdxrt/shim.go:25-26). */
-#define HWK_ABI 3
+#define HWK_ABI 4
 
 typedef struct hwk_device hwk_device;
 typedef struct hwk_buf hwk_buf;
@@ -99,7 +99,9 @@ HWK_API char *hwk_event_elapsed_ns(void *start, void *end, uint64_t *ns);
  * Its kernels and their arguments are read from the object's AMDGPU metadata; the launch geometry of
  * each kernel from the object's own manifest (the `hwk_co_manifest` constant array: workgroup size,
  * and grid.x as a function of one 4-byte argument), so that no call takes grid or block sizes. The
- * library's own code object is lib/hwk_gfx950.hsaco (the batch-1 MXFP4 GEMV and a streaming read). */
+ * library's own code object is lib/hwk_gfx950.hsaco: the batch-1 MXFP4 GEMV, the split-K decode
+ * attention and its merge, the int8 and MXFP4 prefill GEMMs, the MoE route, gate_up and down, and a
+ * streaming read (the same device code as the entry points below). */
 
 /* A kernel of a loaded module (reference types.KernelInfo). */
 typedef struct hwk_kernel_info {
@@ -120,6 +122,7 @@ typedef struct hwk_kernel_arg {
   uint32_t offset; /* byte offset in the argument buffer */
   uint32_t size;   /* bytes */
   uint32_t buffer; /* 1: a device address, set with hwk_run_set_buffer*; 0: a value, hwk_run_set_arg */
+  uint32_t nullable; /* a buffer argument the kernel accepts as null (hwk_run_set_null), per the manifest */
   char name[64];
   char type[32];   /* "void *" for a buffer, else "uint8_t", "uint16_t", "uint32_t", "uint64_t" or "bytes" */
 } hwk_kernel_arg;
@@ -140,6 +143,11 @@ HWK_API char *hwk_run_set_arg(hwk_run *r, uint32_t index, const void *value, siz
  * value argument or a range past the buffer is an error (device.go:367-394). */
 HWK_API char *hwk_run_set_buffer(hwk_run *r, uint32_t index, hwk_buf *b);
 HWK_API char *hwk_run_set_buffer_at(hwk_run *r, uint32_t index, hwk_buf *b, size_t off, size_t n);
+/* A buffer argument the kernel's manifest marks as optional set to the null address (an absent bias,
+ * say); any other argument is an error. No counterpart in the reference, whose NPU kernels take no
+ * optional buffers: a code object's kernels here do (the MoE biases, the router bias). A buffer
+ * argument left unset refuses hwk_run_submit. */
+HWK_API char *hwk_run_set_null(hwk_run *r, uint32_t index);
 /* The first error a setter recorded (a copy), or NULL. */
 HWK_API char *hwk_run_err(hwk_run *r);
 /* Launches on the stream with the manifest's geometry. An error while the run's previous

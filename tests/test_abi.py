@@ -37,11 +37,11 @@ def test_binding_covers_header():
 
 
 def test_abi_version():
-    assert hwk.load().hwk_abi() == hwk.ABI == 3
+    assert hwk.load().hwk_abi() == hwk.ABI == 4
 
 
 def test_wrong_abi_refused(tmp_path, monkeypatch):
-    monkeypatch.setattr(hwk, "ABI", 4)
+    monkeypatch.setattr(hwk, "ABI", hwk.ABI + 1)
     monkeypatch.setattr(hwk, "_lib", None)
     with pytest.raises(hwk.HwkLibraryError):
         hwk.load()

@@ -20,9 +20,15 @@ def by_name(kernels):
     return {k.name: k for k in kernels}
 
 
+CO_KERNELS = {"hwk_co_mxfp4_gemv", "hwk_co_stream_read", "hwk_co_attn_decode_f16_g1", "hwk_co_attn_decode_f16_g2",
+              "hwk_co_attn_decode_f16_g4", "hwk_co_attn_decode_i8_g4", "hwk_co_attn_merge", "hwk_co_i8_gemm",
+              "hwk_co_mxfp4_gemm", "hwk_co_moe_route", "hwk_co_moe_gate_up", "hwk_co_moe_down"}
+
+
 def test_kernels_from_metadata():
     ks = by_name(Program.load(None, image()).kernels())
-    assert set(ks) == {"hwk_co_mxfp4_gemv", "hwk_co_stream_read"}
+    assert set(ks) == CO_KERNELS
+    assert all(k.runnable and k.block > 0 for k in ks.values())
     g = ks["hwk_co_mxfp4_gemv"]
     assert [(a.index, a.name, a.offset, a.size, a.buffer) for a in g.args] == [
         (0, "w", 0, 8, True), (1, "e", 8, 8, True), (2, "x", 16, 8, True), (3, "y", 24, 8, True),
@@ -32,6 +38,22 @@ def test_kernels_from_metadata():
     r = ks["hwk_co_stream_read"]
     assert [(a.name, a.size, a.buffer) for a in r.args] == [("p", 8, True), ("n16", 4, False), ("sink", 8, True)]
     assert r.block == 256 and r.runnable
+    a = ks["hwk_co_attn_decode_f16_g4"]
+    assert [x.name for x in a.args] == ["q", "k", "v", "ws_o", "ws_m", "ws_l", "out", "groups", "kv_heads", "mode",
+                                        "len", "cap", "chunk", "nchunk", "kpw", "scale_bits"]
+    assert [x.buffer for x in a.args] == [True] * 7 + [False] * 9 and a.block == 256
+    g = ks["hwk_co_i8_gemm"]
+    assert [(x.name, x.size) for x in g.args][-1] == ("tiles", 4) and g.block == 256
+
+
+def test_optional_buffers_from_manifest():
+    """The manifest marks the buffers a kernel accepts as null (the MoE biases, the router bias); no
+    other argument is optional."""
+    ks = by_name(Program.load(None, image()).kernels())
+    opt = {k: [a.name for a in v.args if a.nullable] for k, v in ks.items()}
+    assert opt["hwk_co_moe_route"] == ["bias"]
+    assert opt["hwk_co_moe_gate_up"] == ["gb"] and opt["hwk_co_moe_down"] == ["db"]
+    assert all(not v for k, v in opt.items() if "moe" not in k)
 
 
 def test_inspection_module_cannot_run():
@@ -51,7 +73,7 @@ def test_offload_bundle_is_unpacked():
     ent += struct.pack("<QQQ", off, len(elf), len(triples[1])) + triples[1]
     blob = head + ent
     blob += b"\0" * (off - len(blob)) + elf
-    assert set(by_name(Program.load(None, blob).kernels())) == {"hwk_co_mxfp4_gemv", "hwk_co_stream_read"}
+    assert set(by_name(Program.load(None, blob).kernels())) == CO_KERNELS
     no950 = blob.replace(b"gfx950", b"gfx942", 1)
     with pytest.raises(hwk.HwkError, match="gfx950"):
         Program.load(None, no950)

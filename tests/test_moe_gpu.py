@@ -115,10 +115,11 @@ def _np(*ts):
     return [t.cpu().numpy() for t in ts]
 
 
-@pytest.mark.parametrize("T", [1, 5, 8])
+@pytest.mark.parametrize("T", [1, 2, 5, 8])
 def test_moe_layer_route_folded(dev, orc, T):
-    """hwk_moe_layer (route folded into the gate_up launch): idx bit-exact to the oracle's Choose, w
-    within one ulp, the output as hwk_moe_experts' on the same choice (and the oracle's)."""
+    """hwk_moe_layer (route folded into the gate_up launch up to 2 tokens, a route launch past that):
+    idx bit-exact to the oracle's Choose, w within one ulp, the output as hwk_moe_experts' on the
+    same choice (and the oracle's)."""
     print(f"moe layer T={T}", flush=True)
     x, logits, gw, ge, dw, de = experts_case(T)
     out, idx, w = ops.moe_layer(x, logits, 4, gw, ge, dw, de)
@@ -132,6 +133,34 @@ def test_moe_layer_route_folded(dev, orc, T):
     check_close(out.cpu().numpy(), want)
     same = ops.moe_experts(x, idx, w, gw, ge, dw, de)
     check_close(out.cpu().numpy(), same.cpu().numpy(), tol=1e-6)
+
+
+@pytest.mark.parametrize("T,row", [(1, 0), (5, 3)])
+def test_moe_layer_score_collision(dev, orc, T, row):
+    """A float32 score collision at the top-k boundary: token `row` has three clear leaders and, for
+    the fourth place, expert 5 (logit 0.5) against expert 7 (the next float32 above 0.5): relative to
+    the maximum 9 both differences round to -8.5, their scores are equal, and Choose's stable order
+    takes the lower index 5 where an order by logit would take 7. The layer (the route folded into
+    gate_up at T = 1, a route launch at T = 5) must use expert 5: idx bit-exact, output as the
+    oracle's."""
+    x, logits, gw, ge, dw, de = experts_case(T)
+    lg = logits.cpu().numpy()
+    lg[row, :] = -5.0
+    lg[row, :3] = [9.0, 8.5, 8.0]
+    lg[row, 5] = 0.5
+    lg[row, 7] = np.nextafter(np.float32(0.5), np.float32(1.0))
+    assert lg[row, 7] > lg[row, 5] and np.float32(lg[row, 7] - 9.0) == np.float32(lg[row, 5] - 9.0)
+    logits.copy_(torch.from_numpy(lg))
+    oi, _ = orc.choose(lg[row], 4)
+    assert list(oi) == [0, 1, 2, 5]
+    out, idx, w = ops.moe_layer(x, logits, 4, gw, ge, dw, de)
+    ii, ww = idx.cpu().numpy(), w.cpu().numpy()
+    for t in range(T):
+        oi, ow = orc.choose(lg[t], 4)
+        assert np.array_equal(ii[t], oi), (t, ii[t], oi)
+        assert np.all(ulp_diff(ww[t], ow) <= 1)
+    want = orc.experts(x.cpu().numpy().astype(np.float32), ii, ww, *_np(gw, ge, dw, de))
+    check_close(out.cpu().numpy(), want)
 
 
 @pytest.mark.parametrize("T,exp_hi", [(1, False), (5, False), (3, True)])
