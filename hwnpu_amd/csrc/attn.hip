@@ -362,23 +362,32 @@ __global__ void k_kv_quantize_i8(const f16 *__restrict__ x, int8_t *__restrict__
   }
 }
 
-// The split of hwk_attn_decode: workgroups of W waves (8 from 8,192 keys, fp16 caches below 32,768;
-// else 4: measured fastest for each), each wave kpw keys (a multiple of 16), chunk = W*kpw keys a
-// workgroup. kpw is sized so that the launch runs about 2048 waves (8 a CU, each with two tiles of
-// loads in flight), between 32 and 256 keys, more when a head would exceed kMaxChunks chunks. A
-// caller's split (a multiple of 64) is the chunk.
+// The split of hwk_attn_decode: workgroups of W waves, each wave kpw keys (a multiple of 16), chunk =
+// W*kpw keys a workgroup. W = 8 for int8 caches from 8,192 keys and for fp16 caches of 8,192 to
+// 16,383 keys, else 4. Below 16,384 keys kpw is sized so that the launch runs about 2048 waves (8 a
+// CU, each with two tiles of loads in flight), between 32 and 256 keys, more when a head would exceed
+// kMaxChunks chunks; from 16,384 keys a kv head takes 32 chunks, so that the merge reads 32 partials a
+// query head (measured at 16K and 32K keys over chunks of 512-2048 keys and 4 or 8 waves: the
+// fastest, with the merge's cost growing with the chunks and the split's with the keys a workgroup).
+// A caller's split (a multiple of 64) is the chunk.
 uint32_t decode_waves(const hwk_attn_params *p) {
-  return p->len >= 8192 && (p->kv_int8 || p->len < 32768) ? 8u : 4u;
+  if (p->kv_int8) return p->len >= 8192 ? 8u : 4u;
+  return p->len >= 8192 && p->len < 16384 ? 8u : 4u;
 }
 
 uint32_t pick_kpw(const hwk_attn_params *p) {
   const uint32_t W = decode_waves(p);
   if (p->split) return p->split / W;
-  const uint64_t keys = (uint64_t)p->len * p->kv_heads;
-  uint64_t kpw = (keys + 2047) / 2048;
+  uint64_t kpw;
+  if (p->len >= 16384) {
+    kpw = ((uint64_t)p->len + 32ull * W - 1) / (32ull * W);
+  } else {
+    const uint64_t keys = (uint64_t)p->len * p->kv_heads;
+    kpw = (keys + 2047) / 2048;
+    if (kpw < 32) kpw = 32;
+    if (kpw > 256) kpw = 256;
+  }
   kpw = (kpw + 15) / 16 * 16;
-  if (kpw < 32) kpw = 32;
-  if (kpw > 256) kpw = 256;
   const uint64_t min_kpw = ((uint64_t)p->len + (uint64_t)kMaxChunks * W - 1) / ((uint64_t)kMaxChunks * W);
   if (kpw < min_kpw) kpw = (min_kpw + 15) / 16 * 16;
   return (uint32_t)kpw;

@@ -1,11 +1,23 @@
 """Writes the greedy-decode fixture of the synthetic 28-layer model (qwen3_c5_greedy.json) with the
 CPU oracle (oracle/qwen3.c): the checkpoint of seed 0 and weight std 0.02, a 1024-token prompt of
 ids uniform over the vocabulary, then 64 greedy steps. Also the weights' checksums, so that a GPU
-test can tell a mismatch of the weights from one of the forward pass.
+test can tell a mismatch of the weights from one of the forward pass, and each step's top-2 gap.
 
-    python tests/golden/make_qwen3_golden.py [--steps 64] [--out tests/golden/qwen3_c5_greedy.json]
+    python tests/golden/make_qwen3_golden.py [--steps 64] [--min-gap G] [--out tests/golden/qwen3_c5_greedy.json]
 
-Takes a few minutes on 8 cores and about 8 GB of memory.
+The prompt's ids come from the synth stream named c5.prompt, or with --min-gap from the first of
+the streams c5.prompt, c5.prompt.1, c5.prompt.2, ... whose 64 greedy steps keep every top-2 logit gap
+of the oracle at or above G. A free-running greedy comparison can only be as exact as the gaps
+allow: a GPU that sums in another fp32 order flips fp16 roundings of the activations, which moves
+the logits by about 1e-3 (measured on the GPU between two summation orders of the decode attention:
+top-2 margin change rms 1.7e-3, max 5.5e-3), and a step whose gap is smaller than that may pick
+the other token with either order. The fixture therefore uses a prompt whose trajectory has no such
+step, chosen by the rule above before any GPU comparison.
+
+The committed fixture was made with --min-gap 0.008 (above the 5.5e-3 measured maximum): the
+streams c5.prompt to c5.prompt.8 each had a step below it, c5.prompt.9 none (smallest gap 0.0126).
+Each prompt takes about 2.5 minutes of prefill on 8 cores and about 8 GB of memory, and a
+trajectory stops at its first gap below G; the search above took 27 minutes.
 """
 from __future__ import annotations
 
@@ -30,35 +42,58 @@ PROMPT = 1024
 PROMPT_NAME = "c5.prompt"
 
 
-def prompt_tokens():
-    return synth_np.uniform_int(PROMPT, 0, C5["vocab"], PROMPT_NAME).astype(np.int32)
+def prompt_tokens(name=PROMPT_NAME):
+    return synth_np.uniform_int(PROMPT, 0, C5["vocab"], name).astype(np.int32)
+
+
+def gap_of(logits):
+    srt = np.sort(logits)
+    return float(srt[-1] - srt[-2])
+
+
+def trajectory(m, name, steps, min_gap, t0):
+    """The greedy tokens and top-2 gaps after prompt `name`; None at the first gap below min_gap."""
+    tok, logits = m.run(prompt_tokens(name), 0)
+    print(f"{name}: prefill {time.time() - t0:.1f}s -> {tok}", flush=True)
+    out, gaps = [tok], [gap_of(logits)]
+    for i in range(steps - 1):
+        if gaps[-1] < min_gap:
+            print(f"{name}: step {i} gap {gaps[-1]:.5f} < {min_gap}", flush=True)
+            return None
+        tok, logits = m.run([tok], PROMPT + i)
+        out.append(tok)
+        gaps.append(gap_of(logits))
+        if i % 8 == 0:
+            print(f"{name}: step {i + 1} {time.time() - t0:.1f}s -> {tok}", flush=True)
+    if gaps[-1] < min_gap:
+        return None
+    return out, gaps
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--min-gap", type=float, default=0.0)
+    ap.add_argument("--tries", type=int, default=64)
     ap.add_argument("--out", default=os.path.join(HERE, "qwen3_c5_greedy.json"))
     args = ap.parse_args()
     t0 = time.time()
     m = oracle.Qwen3(**C5, theta=1e6, eps=1e-6, seed=0, std=0.02)
     print(f"weights {time.time() - t0:.1f}s", flush=True)
-    toks = prompt_tokens()
-    tok, logits = m.run(toks, 0)
-    print(f"prefill {time.time() - t0:.1f}s -> {tok}", flush=True)
-    out, gaps = [tok], []
-    for i in range(args.steps - 1):
-        srt = np.sort(logits)
-        gaps.append(float(srt[-1] - srt[-2]))
-        tok, logits = m.run([tok], PROMPT + i)
-        out.append(tok)
-        if i % 8 == 0:
-            print(f"step {i + 1} {time.time() - t0:.1f}s -> {tok}", flush=True)
-    srt = np.sort(logits)
-    gaps.append(float(srt[-1] - srt[-2]))
+    for k in range(args.tries if args.min_gap > 0 else 1):
+        name = PROMPT_NAME if k == 0 else f"{PROMPT_NAME}.{k}"
+        got = trajectory(m, name, args.steps, args.min_gap, t0)
+        if got:
+            break
+    else:
+        raise SystemExit(f"no prompt of {args.tries} keeps every gap at or above {args.min_gap}")
+    out, gaps = got
     doc = {
         "what": "greedy tokens of the synthetic Qwen3 (28 layers) after a 1024-token prompt, CPU oracle",
         "config": C5, "theta": 1e6, "eps": 1e-6, "seed": 0, "std": 0.02,
-        "prompt": {"n": PROMPT, "name": PROMPT_NAME, "rule": "uniform ints [0, vocab), synth key c5.prompt"},
+        "prompt": {"n": PROMPT, "name": name, "rule": f"uniform ints [0, vocab), synth key {name}",
+                   "min_gap": args.min_gap,
+                   "choice": "the first of c5.prompt, c5.prompt.1, ... whose oracle top-2 gaps all reach min_gap"},
         "checksums": dict(zip(["blocks", "scales", "embed"], m.checksums())),
         "tokens": out,
         "top2_gaps": [round(g, 6) for g in gaps],
