@@ -7,29 +7,32 @@ namespace {
 
 using namespace hwk_gemm;
 
-template <int BM, int BN, bool MX, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MX && WM * WN == 4 ? 2 : 1))) void k_gemm(
+template <int BM, int BN, bool MX, int WM, int WN, int KG>
+__global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_eu(MX && WM * WN * KG == 4 ? 2 : 1))) void k_gemm(
     const u32x4 *__restrict__ X, const uint8_t *__restrict__ W, const uint8_t *__restrict__ E,
     const uint16_t *__restrict__ S, void *__restrict__ Y, uint32_t M, uint32_t N, uint32_t K, int mode, bool equads) {
-  gemm_wg<BM, BN, MX, WM, WN>(blockIdx.x, X, W, E, S, Y, M, N, K, mode, equads);
+  gemm_wg<BM, BN, MX, WM, WN, KG>(blockIdx.x, X, W, E, S, Y, M, N, K, mode, equads);
 }
 
 // The tile shape for (m, n): the fewest rounds of workgroups over the CUs, a round weighted by the
 // tile's work and its per-tile overheads (larger tiles reuse their loads more). When every tile
 // gets a CU of its own, 8 waves (2 x 4, two a SIMD: one computes while the other waits) beat 4 by
 // 5-12 % on the prompt's shapes; with several tiles a CU, 4-wave workgroups fill the SIMDs as well.
+// An int8 tile of 2 x 2 waves can be doubled into two k groups (8 waves) instead: its SIMDs then
+// split the tile's k, which lets a smaller tile use 8 waves (128 x 96 fills the 256 CUs at 512 x 6144).
 struct Shape {
-  int bm, bn, wm, wn;  // tile, waves over its rows and columns
+  int bm, bn, wm, wn, kg;  // tile, waves over its rows and columns, k groups
 };
-constexpr Shape kShapes[] = {{128, 128, 2, 2}, {128, 96, 2, 2}, {128, 64, 2, 2}, {64, 128, 2, 2},
-                             {128, 128, 2, 4}, {128, 64, 2, 4}};
-Shape pick_shape(uint32_t m, uint32_t n, int cus) {
+constexpr Shape kShapes[] = {{128, 128, 2, 2, 1}, {128, 96, 2, 2, 1}, {128, 64, 2, 2, 1}, {64, 128, 2, 2, 1},
+                             {128, 128, 2, 4, 1}, {128, 64, 2, 4, 1}, {128, 96, 2, 2, 2}};
+Shape pick_shape(uint32_t m, uint32_t n, int cus, bool mx) {
   Shape best = kShapes[0];
   double best_cost = 1e300;
   for (const Shape &s : kShapes) {
+    if (mx && s.kg != 1) continue;
     const uint64_t tiles = (uint64_t)((m + s.bm - 1) / s.bm) * ((n + s.bn - 1) / s.bn);
     const uint64_t rounds = (tiles + cus - 1) / cus;
-    const bool eight = s.wm * s.wn == 8;
+    const bool eight = s.wm * s.wn * s.kg == 8;
     if (eight && tiles > (uint64_t)cus) continue;
     const double cost = (double)rounds * s.bm * s.bn * (1.0 + 32.0 / s.bm + 32.0 / s.bn) * (eight ? 0.75 : 1.0);
     if (cost < best_cost) {
@@ -52,25 +55,30 @@ template <bool MX>
 char *launch(hipStream_t st, const void *x, const void *w, const void *e, const void *s, void *y, uint32_t m,
              uint32_t n, uint32_t k, int mode, const char *what) {
   static const int cus = device_cus();
-  const Shape sh = pick_shape(m, n, cus);
+  const Shape sh = pick_shape(m, n, cus, MX);
   const uint32_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn);
   const bool equads = MX && (k / 32) % 16 == 0 && hwk::aligned(e, 16);
   const dim3 grid(tiles);
   const u32x4 *X = (const u32x4 *)x;
   const uint8_t *W = (const uint8_t *)w, *E = (const uint8_t *)e;
   const uint16_t *S = (const uint16_t *)s;
-#define HWK_GEMM_IF(BMv, BNv, WMv, WNv)                                                                          \
-  if (sh.bm == BMv && sh.bn == BNv && sh.wm == WMv && sh.wn == WNv)                                               \
-    hipLaunchKernelGGL((k_gemm<BMv, BNv, MX, WMv, WNv>), grid, dim3(64 * WMv * WNv), 0, st, X, W, E, S, y, m, n, k, \
-                       mode, equads);                                                                             \
+#define HWK_GEMM_IF(BMv, BNv, WMv, WNv, KGv)                                                                   \
+  if (sh.bm == BMv && sh.bn == BNv && sh.wm == WMv && sh.wn == WNv && sh.kg == KGv)                               \
+    hipLaunchKernelGGL((k_gemm<BMv, BNv, MX, WMv, WNv, KGv>), grid, dim3(64 * WMv * WNv * KGv), 0, st, X, W, E, S, \
+                       y, m, n, k, mode, equads);                                                                 \
   else
-  HWK_GEMM_IF(128, 128, 2, 2)
-  HWK_GEMM_IF(128, 96, 2, 2)
-  HWK_GEMM_IF(128, 64, 2, 2)
-  HWK_GEMM_IF(64, 128, 2, 2)
-  HWK_GEMM_IF(128, 128, 2, 4)
-  HWK_GEMM_IF(128, 64, 2, 4)
-  HWK_CHECK(false, "%s: no kernel for the %dx%d tile", what, sh.bm, sh.bn);
+  HWK_GEMM_IF(128, 128, 2, 2, 1)
+  HWK_GEMM_IF(128, 96, 2, 2, 1)
+  HWK_GEMM_IF(128, 64, 2, 2, 1)
+  HWK_GEMM_IF(64, 128, 2, 2, 1)
+  HWK_GEMM_IF(128, 128, 2, 4, 1)
+  HWK_GEMM_IF(128, 64, 2, 4, 1)
+  if constexpr (!MX) {
+    HWK_GEMM_IF(128, 96, 2, 2, 2)
+    HWK_CHECK(false, "%s: no kernel for the %dx%d tile", what, sh.bm, sh.bn);
+  } else {
+    HWK_CHECK(false, "%s: no kernel for the %dx%d tile", what, sh.bm, sh.bn);
+  }
 #undef HWK_GEMM_IF
   return hwk::launched(what);
 }

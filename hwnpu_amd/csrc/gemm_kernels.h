@@ -77,21 +77,27 @@ __device__ __forceinline__ int xchunk(int q, int kk) {
   return kk < 2 ? 2 * q + kk : 8 + 2 * q + (kk - 2);
 }
 
-template <int BM, int BN, bool MX, int WM, int WN>
+// KG k groups of WM x WN waves: group g takes MFMAs g*KK/KG .. of every step of the whole tile, and
+// the groups' accumulators are summed at the end (int8 only: 2 groups make an 8-wave workgroup of a
+// tile that 4 waves would hold, so that a CU's SIMDs split the tile's k as well as its columns).
+template <int BM, int BN, bool MX, int WM, int WN, int KG>
 struct Cfg {
-  static constexpr int NT = 64 * WM * WN;                   // threads: WM x WN waves over the tile
+  static constexpr int NT = 64 * WM * WN * KG;              // threads: KG groups of WM x WN waves
   static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16 x 16 tiles a wave
   static constexpr int AL = BM * CH / NT;                   // X chunks a thread stages a step
-  static constexpr int BL = MX ? 1 : 2;                     // 16-byte weight loads a lane a step a tile
+  static constexpr int BL = MX ? 1 : 2 / KG;                // 16-byte weight loads a lane a step a tile
+  static constexpr int KKG = KK / KG;                       // MFMAs a tile a step a wave
   static_assert(BM * CH % NT == 0 && TM * WM * 16 == BM && TN * WN * 16 == BN, "tile shape");
+  static_assert(KG == 1 || (KG == 2 && !MX), "k groups: int8 only");
+  static_assert(KG == 1 || BM * BN * 4 <= 2 * BM * CH * 16, "the k groups' sum goes through the X buffers");
 };
 
-template <int BM, int BN, bool MX, int WM, int WN>
+template <int BM, int BN, bool MX, int WM, int WN, int KG>
 struct Stage {
-  u32x4 a[Cfg<BM, BN, MX, WM, WN>::AL];
-  u32x4 b[Cfg<BM, BN, MX, WM, WN>::TN][Cfg<BM, BN, MX, WM, WN>::BL];
-  uint32_t e[Cfg<BM, BN, MX, WM, WN>::TN];  // MXFP4 block scale bytes
-  uint32_t k0;                      // the step's K offset
+  u32x4 a[Cfg<BM, BN, MX, WM, WN, KG>::AL];
+  u32x4 b[Cfg<BM, BN, MX, WM, WN, KG>::TN][Cfg<BM, BN, MX, WM, WN, KG>::BL];
+  uint32_t e[Cfg<BM, BN, MX, WM, WN, KG>::TN];  // MXFP4 block scale bytes
+  uint32_t k0;                                  // the step's K offset
 };
 
 // Issue the global loads of the step at K offset k0 into s: X (load_x) and the weights (load_w).
@@ -99,10 +105,10 @@ struct Stage {
 // end reads in-range data, which zero_tail clears when the stage is consumed (a select here would wait
 // for the load at once). Every load is issued unconditionally (a load under a branch would be waited
 // for at the join).
-template <int BM, int BN, bool MX, int WM, int WN>
-__device__ __forceinline__ void load_x(Stage<BM, BN, MX, WM, WN> &s, const u32x4 *__restrict__ X, uint32_t M, uint32_t K,
-                                       uint32_t m0, uint32_t k0, int t) {
-  using C = Cfg<BM, BN, MX, WM, WN>;
+template <int BM, int BN, bool MX, int WM, int WN, int KG>
+__device__ __forceinline__ void load_x(Stage<BM, BN, MX, WM, WN, KG> &s, const u32x4 *__restrict__ X, uint32_t M,
+                                       uint32_t K, uint32_t m0, uint32_t k0, int t) {
+  using C = Cfg<BM, BN, MX, WM, WN, KG>;
   s.k0 = k0;
 #pragma unroll
   for (int i = 0; i < C::AL; i++) {
@@ -112,11 +118,12 @@ __device__ __forceinline__ void load_x(Stage<BM, BN, MX, WM, WN> &s, const u32x4
   }
 }
 
-template <int BM, int BN, bool MX, int WM, int WN>
-__device__ __forceinline__ void load_w(Stage<BM, BN, MX, WM, WN> &s, const uint8_t *__restrict__ W,
+// (int8: a k group's half of the step's 128 codes a row, h = g, when KG = 2)
+template <int BM, int BN, bool MX, int WM, int WN, int KG>
+__device__ __forceinline__ void load_w(Stage<BM, BN, MX, WM, WN, KG> &s, const uint8_t *__restrict__ W,
                                        const uint8_t *__restrict__ E, uint32_t K, uint32_t k0,
-                                       const uint32_t (&brow)[Cfg<BM, BN, MX, WM, WN>::TN], int q) {
-  using C = Cfg<BM, BN, MX, WM, WN>;
+                                       const uint32_t (&brow)[Cfg<BM, BN, MX, WM, WN, KG>::TN], int q, int g) {
+  using C = Cfg<BM, BN, MX, WM, WN, KG>;
   if constexpr (MX) {
     const uint32_t blk = min(k0 + q * 32, K - 32) / 32;
 #pragma unroll
@@ -127,8 +134,8 @@ __device__ __forceinline__ void load_w(Stage<BM, BN, MX, WM, WN> &s, const uint8
     }
   } else {
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const uint32_t kc = min(k0 + h * 64 + q * 16, K - 16);
+    for (int h = 0; h < C::BL; h++) {
+      const uint32_t kc = min(k0 + (KG == 1 ? h : g) * 64 + q * 16, K - 16);
 #pragma unroll
       for (int j = 0; j < C::TN; j++) s.b[j][h] = load16(W + (size_t)brow[j] * K + kc);
     }
@@ -136,9 +143,9 @@ __device__ __forceinline__ void load_w(Stage<BM, BN, MX, WM, WN> &s, const uint8
 }
 
 // A step reaching past K: its X chunks and weight loads past K become zeros (MXFP4: scale 0).
-template <int BM, int BN, bool MX, int WM, int WN>
-__device__ __forceinline__ void zero_tail(Stage<BM, BN, MX, WM, WN> &s, uint32_t K, int t, int q) {
-  using C = Cfg<BM, BN, MX, WM, WN>;
+template <int BM, int BN, bool MX, int WM, int WN, int KG>
+__device__ __forceinline__ void zero_tail(Stage<BM, BN, MX, WM, WN, KG> &s, uint32_t K, int t, int q, int g) {
+  using C = Cfg<BM, BN, MX, WM, WN, KG>;
   const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int i = 0; i < C::AL; i++)
@@ -152,8 +159,8 @@ __device__ __forceinline__ void zero_tail(Stage<BM, BN, MX, WM, WN> &s, uint32_t
       }
     } else {
 #pragma unroll
-      for (int h = 0; h < 2; h++)
-        if (s.k0 + h * 64 + q * 16 >= K) s.b[j][h] = zero;
+      for (int h = 0; h < C::BL; h++)
+        if (s.k0 + (KG == 1 ? h : g) * 64 + q * 16 >= K) s.b[j][h] = zero;
     }
   }
 }
@@ -232,17 +239,18 @@ __device__ __forceinline__ void tile_of(uint32_t id, uint32_t mt, uint32_t nt, u
   tm = lin % mt;
 }
 
-template <int BM, int BN, bool MX, int WM, int WN>
+template <int BM, int BN, bool MX, int WM, int WN, int KG = 1>
 __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
                                         const uint8_t *__restrict__ E, const uint16_t *__restrict__ S,
                                         void *__restrict__ Y, uint32_t M, uint32_t N, uint32_t K, int mode,
                                         bool equads) {
-  using C = Cfg<BM, BN, MX, WM, WN>;
-  constexpr int TM = C::TM, TN = C::TN, NT = C::NT;
+  using C = Cfg<BM, BN, MX, WM, WN, KG>;
+  constexpr int TM = C::TM, TN = C::TN, NT = C::NT, KKG = C::KKG;
   __shared__ __attribute__((aligned(16))) u32x4 As[2][BM * CH];
   __shared__ int hs[MX ? BN : 1], ls[MX ? BN : 1];  // the row shift scan (MXFP4)
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave / WN, wn = wave % WN;
+  const int g = wave / (WM * WN), wl = wave % (WM * WN);  // k group, wave in the group
+  const int wm = wl / WN, wn = wl % WN;
   const int r16 = lane & 15, q = lane >> 4;
   uint32_t tm, tn;
   tile_of(bx, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
@@ -254,11 +262,11 @@ __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X
 
   const uint32_t steps = (K + KS - 1) / KS;
   auto kofs = [&](uint32_t j) -> uint32_t { return min(j, steps) * KS; };  // past the end: reads zeros
-  Stage<BM, BN, MX, WM, WN> st[NS];
+  Stage<BM, BN, MX, WM, WN, KG> st[NS];
 #pragma unroll
   for (int s = 0; s < NS; s++) {
-    load_x<BM, BN, MX, WM, WN>(st[s], X, M, K, m0, kofs(s), t);
-    load_w<BM, BN, MX, WM, WN>(st[s], W, E, K, kofs(s), brow, q);
+    load_x<BM, BN, MX, WM, WN, KG>(st[s], X, M, K, m0, kofs(s), t);
+    load_w<BM, BN, MX, WM, WN, KG>(st[s], W, E, K, kofs(s), brow, q, g);
   }
   int s0[TN];
 #pragma unroll
@@ -294,7 +302,7 @@ __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X
     for (int s = 0; s < NS; s++) {
       const uint32_t j = j0 + s;
       u32x4 *buf = As[s & 1];  // NS is even: step j uses buffer j & 1
-      if (st[s].k0 + KS > K) zero_tail<BM, BN, MX, WM, WN>(st[s], K, t, q);  // uniform: only a ragged step
+      if (st[s].k0 + KS > K) zero_tail<BM, BN, MX, WM, WN, KG>(st[s], K, t, q, g);  // uniform: only a ragged step
 #pragma unroll
       for (int i = 0; i < C::AL; i++) {
         const int c = t + NT * i, row = c / CH, ch = c % CH;
@@ -302,24 +310,26 @@ __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X
       }
       __syncthreads();
       issue_order();
-      load_x<BM, BN, MX, WM, WN>(st[s], X, M, K, m0, kofs(j + NS), t);
+      load_x<BM, BN, MX, WM, WN, KG>(st[s], X, M, K, m0, kofs(j + NS), t);
       issue_order();
       float sc[TN];
 #pragma unroll
       for (int jn = 0; jn < TN; jn++) sc[jn] = MX ? shifted_scale(st[s].e[jn], s0[jn]) : 0.0f;
-      // the operands of kk + 1 (X from LDS, weights converted) are fetched before the MFMAs of kk
+      // the operands of kk + 1 (X from LDS, weights converted) are fetched before the MFMAs of kk; kk
+      // counts the group's MFMAs (the step's MFMA g*KKG + kk)
       auto operands = [&](half8 (&af)[TM], half8 (&bf)[TN], int kk) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
           const int row = wm * (BM / WM) + i * 16 + r16;
-          af[i] = __builtin_bit_cast(half8, buf[row * CH + (xchunk<MX>(q, kk) ^ (row & 15))]);
+          const int ch = KG == 1 ? xchunk<MX>(q, kk) : xchunk<MX>(q, g * KKG + kk);
+          af[i] = __builtin_bit_cast(half8, buf[row * CH + (ch ^ (row & 15))]);
         }
 #pragma unroll
         for (int jn = 0; jn < TN; jn++) {
           if constexpr (MX) {
             bf[jn] = fp4x8_to_half8(st[s].b[jn][0][kk], sc[jn]);
           } else {
-            const u32x4 v = st[s].b[jn][kk >> 1];
+            const u32x4 v = st[s].b[jn][kk >> 1];  // KG = 2: the group's half, loaded alone
             bf[jn] = i8x8_to_half8(v[(kk & 1) * 2], v[(kk & 1) * 2 + 1]);
           }
         }
@@ -327,8 +337,8 @@ __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X
       half8 af[2][TM], bf[2][TN];
       operands(af[0], bf[0], 0);
 #pragma unroll
-      for (int kk = 0; kk < KK; kk++) {
-        if (kk + 1 < KK) operands(af[(kk + 1) & 1], bf[(kk + 1) & 1], kk + 1);
+      for (int kk = 0; kk < KKG; kk++) {
+        if (kk + 1 < KKG) operands(af[(kk + 1) & 1], bf[(kk + 1) & 1], kk + 1);
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -336,9 +346,27 @@ __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X
             acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[kk & 1][i], bf[kk & 1][jn], acc[i][jn], 0, 0, 0);
       }
       issue_order();
-      load_w<BM, BN, MX, WM, WN>(st[s], W, E, K, kofs(j + NS), brow, q);
+      load_w<BM, BN, MX, WM, WN, KG>(st[s], W, E, K, kofs(j + NS), brow, q, g);
       issue_order();
     }
+  }
+  if constexpr (KG == 2) {
+    // group 1's accumulators to group 0 through the X buffers (every wave is done with them after
+    // the barrier), summed in group 0, which writes the tile
+    floatx4 *red = (floatx4 *)&As[0][0];
+    __syncthreads();
+    if (g == 1) {
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) red[((wl * TM + i) * TN + j) * 64 + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (g == 1) return;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) acc[i][j] += red[((wl * TM + i) * TN + j) * 64 + lane];
   }
   // D of tile (i, j): lane holds rows q*4 + r, column r16
   if (mode == kOutSwiGLU) {

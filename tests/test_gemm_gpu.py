@@ -24,8 +24,10 @@ def check_close(got, want, tol=TOL):
     assert err <= tol * rms(want), f"max|d|={err:.4g} rms={rms(want):.4g} ratio={err / rms(want):.3g}"
 
 
+# (512, 6144, 2048) and (500, 6000, 2080) take the 128 x 96 tile of two k groups (the latter with a
+# ragged last step and partial edge tiles); the others the one-group tiles
 @pytest.mark.parametrize("m,n,k", [(512, 6144, 2048), (5, 6144, 2048), (1, 128, 32), (130, 200, 96), (7, 1000, 4096),
-                                   (256, 256, 6144), (300, 130, 2880)])
+                                   (256, 256, 6144), (300, 130, 2880), (500, 6000, 2080)])
 def test_i8_gemm_parity(dev, orc, m, n, k):
     print(f"i8_gemm m={m} n={n} k={k}", flush=True)
     name = f"k3i8.{m}.{n}.{k}"
@@ -101,7 +103,7 @@ def test_mxfp4_gemm_edge_exponents(dev, orc):
 
 
 @pytest.mark.parametrize("kind,m,n,k", [("mx", 1024, 3072, 2048), ("mx", 33, 96, 256), ("mx", 5, 512, 6144),
-                                        ("i8", 200, 1536, 2048), ("i8", 7, 32, 96)])
+                                        ("i8", 200, 1536, 2048), ("i8", 7, 32, 96), ("i8", 512, 6144, 2048)])
 def test_gemm_swiglu_output(dev, kind, m, n, k):
     """out_mode "swiglu" (the prompt's gate/up projection with its SwiGLU in the epilogue) equals the
     fp32 output followed by hwk_silu_mul over the column pairs (g, u) = (2c, 2c+1), bit for bit; both
