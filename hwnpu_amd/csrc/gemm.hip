@@ -14,6 +14,15 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
   gemm_wg<BM, BN, MX, WM, WN, KG>(blockIdx.x, X, W, E, S, Y, M, N, K, mode, equads);
 }
 
+template <int BM, int BN, bool MX, int WM, int WN, int KG, int RS>
+__global__ __launch_bounds__(64 * WM * WN * KG) void k_gemm_ring(const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
+                                                              const uint8_t *__restrict__ E,
+                                                              const uint16_t *__restrict__ S, void *__restrict__ Y,
+                                                              uint32_t M, uint32_t N, uint32_t K, int mode,
+                                                              bool equads) {
+  gemm_ring_wg<BM, BN, MX, WM, WN, KG, RS>(blockIdx.x, X, W, E, S, Y, M, N, K, mode, equads);
+}
+
 // The tile shape for (m, n): the fewest rounds of workgroups over the CUs, a round weighted by the
 // tile's work and its per-tile overheads (larger tiles reuse their loads more). When every tile
 // gets a CU of its own, 8 waves (2 x 4, two a SIMD: one computes while the other waits) beat 4 by
@@ -21,10 +30,10 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
 // An int8 tile of 2 x 2 waves can be doubled into two k groups (8 waves) instead: its SIMDs then
 // split the tile's k, which lets a smaller tile use 8 waves (128 x 96 fills the 256 CUs at 512 x 6144).
 struct Shape {
-  int bm, bn, wm, wn, kg;  // tile, waves over its rows and columns, k groups
+  int bm, bn, wm, wn, kg, rs;  // tile, waves over its rows and columns, k groups, ring depth (ring form)
 };
-constexpr Shape kShapes[] = {{128, 128, 2, 2, 1}, {128, 96, 2, 2, 1}, {128, 64, 2, 2, 1}, {64, 128, 2, 2, 1},
-                             {128, 128, 2, 4, 1}, {128, 64, 2, 4, 1}, {128, 96, 2, 2, 2}};
+constexpr Shape kShapes[] = {{128, 128, 2, 2, 1, 0}, {128, 96, 2, 2, 1, 0}, {128, 64, 2, 2, 1, 0}, {64, 128, 2, 2, 1, 0},
+                             {128, 128, 2, 4, 1, 0}, {128, 64, 2, 4, 1, 0}, {128, 96, 2, 2, 2, 0}};
 Shape pick_shape(uint32_t m, uint32_t n, int cus, bool mx) {
   Shape best = kShapes[0];
   double best_cost = 1e300;
@@ -43,6 +52,25 @@ Shape pick_shape(uint32_t m, uint32_t n, int cus, bool mx) {
   return best;
 }
 
+// The ring form (K a multiple of 128; see gemm_kernels.h) for the tiles 128 columns wide, as 8 waves
+// (2 x 4; its LDS holds one workgroup a CU), and for the int8 128 x 96 tile of two k groups. Measured
+// against the register-staged form, bit for bit the same results: 1024 x 4096 x 2048 MXFP4 31.3 ->
+// 28.3 us, 1024 x 12288 x 2048 82.4 -> 79.9, int8 512 x 6144 x 2048 29.9 -> 24.1. The tiles 64
+// columns wide stay register-staged: with one MFMA column a wave (or two k groups) the ring form
+// measured slower there (1024 x 2048 x 6144: 47.5 -> 55.8-60.5 us; 1024 x 2048 x 2048: 21.0 ->
+// 22.2), and so did 64-row tiles with deeper rings.
+bool ring_shape(Shape &sh, bool mx) {
+  if (sh.bm == 128 && sh.bn == 128) {
+    sh = {128, 128, 2, 4, 1, 3};
+    return true;
+  }
+  if (!mx && sh.bm == 128 && sh.bn == 96 && sh.kg == 2) {
+    sh.rs = 3;
+    return true;
+  }
+  return false;
+}
+
 int device_cus() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
@@ -55,13 +83,31 @@ template <bool MX>
 char *launch(hipStream_t st, const void *x, const void *w, const void *e, const void *s, void *y, uint32_t m,
              uint32_t n, uint32_t k, int mode, const char *what) {
   static const int cus = device_cus();
-  const Shape sh = pick_shape(m, n, cus, MX);
+  // the ring form needs whole 128-column steps and 4-byte aligned scale rows
+  Shape sh = pick_shape(m, n, cus, MX);
+  const bool ring = k % 128 == 0 && (!MX || hwk::aligned(e, 4)) && ring_shape(sh, MX);
   const uint32_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn);
   const bool equads = MX && (k / 32) % 16 == 0 && hwk::aligned(e, 16);
   const dim3 grid(tiles);
   const u32x4 *X = (const u32x4 *)x;
   const uint8_t *W = (const uint8_t *)w, *E = (const uint8_t *)e;
   const uint16_t *S = (const uint16_t *)s;
+#define HWK_RING_IF(BMv, BNv, WMv, WNv, KGv, RSv)                                                              \
+  if (sh.bm == BMv && sh.bn == BNv && sh.wm == WMv && sh.wn == WNv && sh.kg == KGv && sh.rs == RSv)               \
+    hipLaunchKernelGGL((k_gemm_ring<BMv, BNv, MX, WMv, WNv, KGv, RSv>), grid, dim3(64 * WMv * WNv * KGv), 0, st, X, W, \
+                       E, S, y, m, n, k, mode, equads);                                                           \
+  else
+  if (ring) {
+    HWK_RING_IF(128, 128, 2, 4, 1, 3)
+    if constexpr (!MX) {
+      HWK_RING_IF(128, 96, 2, 2, 2, 3)
+      HWK_CHECK(false, "%s: no ring kernel for the %dx%d tile", what, sh.bm, sh.bn);
+    } else {
+      HWK_CHECK(false, "%s: no ring kernel for the %dx%d tile", what, sh.bm, sh.bn);
+    }
+    return hwk::launched(what);
+  }
+#undef HWK_RING_IF
 #define HWK_GEMM_IF(BMv, BNv, WMv, WNv, KGv)                                                                   \
   if (sh.bm == BMv && sh.bn == BNv && sh.wm == WMv && sh.wn == WNv && sh.kg == KGv)                               \
     hipLaunchKernelGGL((k_gemm<BMv, BNv, MX, WMv, WNv, KGv>), grid, dim3(64 * WMv * WNv * KGv), 0, st, X, W, E, S, \

@@ -32,6 +32,7 @@
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 namespace hwk_gemm {
 
@@ -88,8 +89,7 @@ struct Cfg {
   static constexpr int BL = MX ? 1 : 2 / KG;                // 16-byte weight loads a lane a step a tile
   static constexpr int KKG = KK / KG;                       // MFMAs a tile a step a wave
   static_assert(BM * CH % NT == 0 && TM * WM * 16 == BM && TN * WN * 16 == BN, "tile shape");
-  static_assert(KG == 1 || (KG == 2 && !MX), "k groups: int8 only");
-  static_assert(KG == 1 || BM * BN * 4 <= 2 * BM * CH * 16, "the k groups' sum goes through the X buffers");
+  static_assert(KG == 1 || KG == 2, "one or two k groups");
 };
 
 template <int BM, int BN, bool MX, int WM, int WN, int KG>
@@ -239,6 +239,52 @@ __device__ __forceinline__ void tile_of(uint32_t id, uint32_t mt, uint32_t nt, u
   tm = lin % mt;
 }
 
+// The tile's store: D of MFMA tile (i, j) of the wave, lane (r16, q) holding rows q*4 + r of column
+// r16; int8 results take the column's scale, MXFP4 results the row shift back (2^s0, exact).
+template <int BM, int WM, int TM, int TN, bool MX>
+__device__ __forceinline__ void store_tile(const floatx4 (&acc)[TM][TN], const int (&s0)[TN],
+                                           const uint16_t *__restrict__ S, void *__restrict__ Y, uint32_t M,
+                                           uint32_t N, uint32_t m0, uint32_t nw, int wm, int r16, int q, int mode) {
+  if (mode == kOutSwiGLU) {
+    // columns (2c, 2c+1) are (gate, up) of output c, held by lanes r16 and r16 ^ 1 for the same four
+    // rows: the gate lane takes the up values of rows 0, 1 and computes those outputs, the up lane
+    // takes the gate values of rows 2, 3 and computes those. Every lane joins the swaps; columns past
+    // N (a tile wider than N) store nothing, and with N % 16 == 0 a pair is wholly below N or not.
+    const bool gate = (r16 & 1) == 0;
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const uint32_t n = nw + j * 16 + r16, c = n / 2;
+      const float sc = MX ? 1.0f : (float)__builtin_bit_cast(f16, S[min(n, N - 1)]);
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[r] = MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc;
+        const float o0 = __shfl_xor(gate ? v[2] : v[0], 1, 64), o1 = __shfl_xor(gate ? v[3] : v[1], 1, 64);
+        const uint32_t mr = m0 + wm * (BM / WM) + i * 16 + q * 4 + (gate ? 0 : 2);  // the lane's first row
+        const float y0 = gate ? swiglu_value(v[0], o0) : swiglu_value(o0, v[2]);
+        const float y1 = gate ? swiglu_value(v[1], o1) : swiglu_value(o1, v[3]);
+        if (n < N && mr < M) ((f16 *)Y)[(size_t)mr * (N / 2) + c] = (f16)y0;
+        if (n < N && mr + 1 < M) ((f16 *)Y)[(size_t)(mr + 1) * (N / 2) + c] = (f16)y1;
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const uint32_t n = nw + j * 16 + r16;
+    if (n >= N) continue;
+    const float sc = MX ? 1.0f : (float)__builtin_bit_cast(f16, S[n]);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = m0 + wm * (BM / WM) + i * 16 + q * 4 + r;
+        if (m < M) store_out(Y, (size_t)m * N + n, MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc, mode);
+      }
+  }
+}
+
 template <int BM, int BN, bool MX, int WM, int WN, int KG = 1>
 __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
                                         const uint8_t *__restrict__ E, const uint16_t *__restrict__ S,
@@ -246,6 +292,8 @@ __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X
                                         bool equads) {
   using C = Cfg<BM, BN, MX, WM, WN, KG>;
   constexpr int TM = C::TM, TN = C::TN, NT = C::NT, KKG = C::KKG;
+  static_assert(KG == 1 || !MX, "k groups here: int8 only");
+  static_assert(KG == 1 || BM * BN * 4 <= 2 * BM * CH * 16, "the k groups' sum goes through the X buffers");
   __shared__ __attribute__((aligned(16))) u32x4 As[2][BM * CH];
   __shared__ int hs[MX ? BN : 1], ls[MX ? BN : 1];  // the row shift scan (MXFP4)
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -368,45 +416,265 @@ __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X
 #pragma unroll
       for (int j = 0; j < TN; j++) acc[i][j] += red[((wl * TM + i) * TN + j) * 64 + lane];
   }
-  // D of tile (i, j): lane holds rows q*4 + r, column r16
-  if (mode == kOutSwiGLU) {
-    // columns (2c, 2c+1) are (gate, up) of output c, held by lanes r16 and r16 ^ 1 for the same four
-    // rows: the gate lane takes the up values of rows 0, 1 and computes those outputs, the up lane
-    // takes the gate values of rows 2, 3 and computes those. Every lane joins the swaps; columns past
-    // N (a tile wider than N) store nothing, and with N % 16 == 0 a pair is wholly below N or not.
-    const bool gate = (r16 & 1) == 0;
+  store_tile<BM, WM, TM, TN, MX>(acc, s0, S, Y, M, N, m0, nw, wm, r16, q, mode);
+}
+
+
+// ---- The ring form (K a multiple of 128): X and the weights both go straight from memory into LDS ----
+//
+// Every global load of the main loop is a load into LDS (global_load_lds_dwordx4: lane i of an
+// instruction writes 16 bytes at the instruction's LDS base + 16 i), into a ring of RS buffers a
+// stream (a template parameter), issued RS-1 steps ahead of the MFMAs that read them, and waited for
+// by an explicit count
+// (the wait counter is in order, and every step issues the same number of loads: past the last step
+// they reread in-range data into a buffer nobody reads). No load result lives in a register across
+// steps, so the loop carries nothing for the compiler to wait on at its head. The swizzles are applied
+// on the source side (which 16-byte chunk a lane fetches), so that the MFMA operand reads of 16
+// lanes land in distinct banks:
+//   X   slot p: row p / CH, chunk (p % CH) ^ (row & 15)                       (256-byte rows)
+//   W   slot p: column p / WCH, chunk (p % WCH) ^ ((column / CPB) & (WCH-1))    (WCH chunks a column a
+//       step: int8 8 = 128 codes, MXFP4 4 = 128 values; CPB columns share a 256-byte bank row)
+//   E   (MXFP4) slot p: column p, the 4 scale bytes of the step (4-byte loads)
+// An LDS buffer of BYTES, one variable per (BYTES, I, TAG): the buffers of a ring are distinct
+// variables, so that the compiler can tell an LDS read of one from the loads into LDS in flight for
+// the others.
+template <typename T, int COUNT, int I, int TAG>
+__device__ __forceinline__ T *lds_buf() {
+  __shared__ __attribute__((aligned(16))) T b[COUNT];
+  return b;
+}
+template <typename T, int COUNT, int TAG, int N>
+struct RingBufs {
+  static __device__ __forceinline__ void fill(T **p) {
+    RingBufs<T, COUNT, TAG, N - 1>::fill(p);
+    p[N - 1] = lds_buf<T, COUNT, N - 1, TAG>();
+  }
+};
+template <typename T, int COUNT, int TAG>
+struct RingBufs<T, COUNT, TAG, 0> {
+  static __device__ __forceinline__ void fill(T **) {}
+};
+
+template <int BM, int BN, bool MX, int WM, int WN, int KG, int RS>
+struct RCfg {
+  using C = Cfg<BM, BN, MX, WM, WN, KG>;
+  static constexpr int NT = C::NT, NW = NT / 64;
+  static constexpr int WCH = MX ? 4 : 8;                             // 16-byte weight chunks a column a step
+  static constexpr int CPB = 256 / (WCH * 16);                       // columns a 256-byte bank row
+  static constexpr int AX = BM * CH / NT;                            // X loads a lane a step
+  static constexpr int AW = (BN * WCH + NT - 1) / NT;                // weight loads a lane a step
+  static constexpr int WSLOTS = AW * NT;                             // weight slots a buffer (padded)
+  static constexpr int LS = AX + AW + (MX ? 1 : 0);                  // loads a lane a step (E: one)
+  static_assert(BM * CH % NT == 0, "X loads a lane");
+  static_assert(!MX || BN <= NT, "scale slots");
+  static_assert((RS - 1) * LS <= 63, "loads in flight past the wait counter");
+};
+
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// LDS writes and reads of this wave done (lgkmcnt 0; the other counters not waited for)
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+// A workgroup barrier that waits for no memory counter (__syncthreads would wait for every load into
+// LDS in flight, the ring's prefetches included): the caller has waited for its own part.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void to_lds16(const void *src, void *lds) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void to_lds4(const void *src, void *lds) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 4, 0, 0);
+}
+
+// The loads of the step at K offset k0 (clamped to the last step: a step past the end rereads it).
+template <int BM, int BN, bool MX, int WM, int WN, int KG, int RS>
+__device__ __forceinline__ void ring_load(u32x4 *xb, u32x4 *wb, uint32_t *eb, const u32x4 *__restrict__ X,
+                                          const uint8_t *__restrict__ W, const uint8_t *__restrict__ E,
+                                          uint32_t M, uint32_t N, uint32_t K, uint32_t m0, uint32_t n0, uint32_t k0,
+                                          int wave, int lane) {
+  using R = RCfg<BM, BN, MX, WM, WN, KG, RS>;
+  k0 = min(k0, K - KS);
+#pragma unroll
+  for (int a = 0; a < R::AX; a++) {
+    const int base = (a * R::NW + wave) * 64, p = base + lane, row = p / CH, ch = (p % CH) ^ (row & 15);
+    to_lds16(X + ((size_t)min(m0 + row, M - 1) * K + k0 + ch * 8) / 8, xb + base);
+  }
+  const size_t rowb = MX ? K / 2 : K;  // weight bytes a column
+  const uint32_t kb = MX ? k0 / 2 : k0;
+#pragma unroll
+  for (int a = 0; a < R::AW; a++) {
+    const int base = (a * R::NW + wave) * 64, p = base + lane, col = p / R::WCH;
+    const int c = (p % R::WCH) ^ ((col / R::CPB) & (R::WCH - 1));
+    to_lds16(W + (size_t)min(n0 + col, N - 1) * rowb + kb + c * 16, wb + base);
+  }
+  if constexpr (MX) {
+    const int p = wave * 64 + lane;  // slots past BN: padding nobody reads
+    to_lds4(E + (size_t)min(n0 + p, N - 1) * (K / 32) + k0 / 32, eb + wave * 64);
+  }
+}
+
+template <int BM, int BN, bool MX, int WM, int WN, int KG, int RS>
+__device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
+                                             const uint8_t *__restrict__ E, const uint16_t *__restrict__ S,
+                                             void *__restrict__ Y, uint32_t M, uint32_t N, uint32_t K, int mode,
+                                             bool equads) {
+  using C = Cfg<BM, BN, MX, WM, WN, KG>;
+  using R = RCfg<BM, BN, MX, WM, WN, KG, RS>;
+  constexpr int TM = C::TM, TN = C::TN, NT = C::NT, KKG = C::KKG, LS = R::LS;
+  static_assert(RS >= 2 && RS <= 6, "ring depth");
+  u32x4 *xr[RS], *wr[RS];
+  uint32_t *er[RS];
+  RingBufs<u32x4, BM * CH, 0, RS>::fill(xr);
+  RingBufs<u32x4, R::WSLOTS, 1, RS>::fill(wr);
+  RingBufs<uint32_t, MX ? R::NW * 64 : 1, 2, RS>::fill(er);
+  __shared__ int hs[MX ? BN : 1], ls[MX ? BN : 1];  // the row shift scan (MXFP4)
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int g = wave / (WM * WN), wl = wave % (WM * WN);  // k group, wave in the group
+  const int wm = wl / WN, wn = wl % WN;
+  const int r16 = lane & 15, q = lane >> 4;
+  uint32_t tm, tn;
+  tile_of(bx, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const uint32_t nw = n0 + wn * (BN / WN);  // the wave's first column
+  const uint32_t steps = K / KS;
+#pragma unroll
+  for (int s = 0; s < RS - 1; s++)
+    ring_load<BM, BN, MX, WM, WN, KG, RS>(xr[s], wr[s], er[s], X, W, E, M, N, K, m0, n0, s * KS, wave, lane);
+  int s0[TN];
+#pragma unroll
+  for (int j = 0; j < TN; j++) s0[j] = 0;
+  if constexpr (MX) {
+    if (t < BN) {
+      hs[t] = 0;
+      ls[t] = 255;
+    }
+    wait_lds();
+    ring_barrier();
+    scan_shifts<BN, NT>(E, n0, N, K / 32, equads, t, hs, ls);
+    wait_lds();
+    ring_barrier();
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-      const uint32_t n = nw + j * 16 + r16, c = n / 2;
-      const float sc = MX ? 1.0f : (float)__builtin_bit_cast(f16, S[min(n, N - 1)]);
+      const uint32_t r = min(nw + j * 16 + r16, N - 1) - n0;
+      s0[j] = shift_of(hs[r], ls[r]);
+    }
+  }
+
+  floatx4 acc[TM][TN];
 #pragma unroll
-      for (int i = 0; i < TM; i++) {
-        float v[4];
+  for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) v[r] = MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc;
-        const float o0 = __shfl_xor(gate ? v[2] : v[0], 1, 64), o1 = __shfl_xor(gate ? v[3] : v[1], 1, 64);
-        const uint32_t mr = m0 + wm * (BM / WM) + i * 16 + q * 4 + (gate ? 0 : 2);  // the lane's first row
-        const float y0 = gate ? swiglu_value(v[0], o0) : swiglu_value(o0, v[2]);
-        const float y1 = gate ? swiglu_value(v[1], o1) : swiglu_value(o1, v[3]);
-        if (n < N && mr < M) ((f16 *)Y)[(size_t)mr * (N / 2) + c] = (f16)y0;
-        if (n < N && mr + 1 < M) ((f16 *)Y)[(size_t)(mr + 1) * (N / 2) + c] = (f16)y1;
+    for (int j = 0; j < TN; j++) acc[i][j] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  // A step j: wait for this wave's loads of step j (those of step j+1 stay in flight), a barrier
+  // (every wave's loads of step j have landed, and every wave is done with the buffers of step j-1),
+  // the loads of step j+RS-1 into those buffers, then the step's weight operands from LDS and the
+  // MFMAs, each kk's weights converted next to the MFMAs that take them.
+  for (uint32_t j0 = 0; j0 < steps; j0 += RS) {
+#pragma unroll
+    for (int s = 0; s < RS; s++) {
+      const uint32_t j = j0 + s;
+      if (j >= steps) break;
+      wait_loads<(RS - 2) * LS>();
+      ring_barrier();
+      issue_order();
+      ring_load<BM, BN, MX, WM, WN, KG, RS>(xr[(s + RS - 1) % RS], wr[(s + RS - 1) % RS], er[(s + RS - 1) % RS], X, W,
+                                            E, M, N, K, m0, n0, (j + RS - 1) * KS, wave, lane);
+      issue_order();
+      const u32x4 *xb = xr[s], *wb = wr[s];
+      // the wave's weight codes of the step: int8 the 16 codes of half h = kk/2 (of the group's half)
+      // at q*16; MXFP4 the dwords kk of the 32-value block q (a k group's two: bytes 8g ..), and the
+      // MXFP4 scales
+      u32x4 wv[TN][C::BL];
+      uint32_t wd[TN][KKG];
+      float sc[TN];
+#pragma unroll
+      for (int jn = 0; jn < TN; jn++) {
+        const int col = wn * (BN / WN) + jn * 16 + r16;
+        if constexpr (MX) {
+          const int slot = col * R::WCH + (q ^ ((col / R::CPB) & (R::WCH - 1)));
+          if constexpr (KG == 1) {
+            const u32x4 v = wb[slot];
+#pragma unroll
+            for (int kk = 0; kk < KKG; kk++) wd[jn][kk] = v[kk];
+          } else {
+            const u32x2 v = *((const u32x2 *)&wb[slot] + g);
+#pragma unroll
+            for (int kk = 0; kk < KKG; kk++) wd[jn][kk] = v[kk];
+          }
+          sc[jn] = shifted_scale((er[s][col] >> (8 * q)) & 255u, s0[jn]);
+        } else {
+#pragma unroll
+          for (int h = 0; h < C::BL; h++) {
+            const int c = (KG == 1 ? h : g) * 4 + q;
+            wv[jn][h] = wb[col * R::WCH + (c ^ ((col / R::CPB) & (R::WCH - 1)))];
+          }
+        }
+      }
+      auto operands = [&](half8 (&af)[TM], half8 (&bf)[TN], int kk) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          const int row = wm * (BM / WM) + i * 16 + r16;
+          const int ch = KG == 1 ? xchunk<MX>(q, kk) : xchunk<MX>(q, g * KKG + kk);
+          af[i] = __builtin_bit_cast(half8, xb[row * CH + (ch ^ (row & 15))]);
+        }
+#pragma unroll
+        for (int jn = 0; jn < TN; jn++) {
+          if constexpr (MX) {
+            bf[jn] = fp4x8_to_half8(wd[jn][kk], sc[jn]);
+          } else {
+            const u32x4 v = wv[jn][kk >> 1];
+            bf[jn] = i8x8_to_half8(v[(kk & 1) * 2], v[(kk & 1) * 2 + 1]);
+          }
+        }
+      };
+      half8 af[2][TM], bf[2][TN];
+      operands(af[0], bf[0], 0);
+#pragma unroll
+      for (int kk = 0; kk < KKG; kk++) {
+        if (kk + 1 < KKG) operands(af[(kk + 1) & 1], bf[(kk + 1) & 1], kk + 1);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int jn = 0; jn < TN; jn++)
+            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[kk & 1][i], bf[kk & 1][jn], acc[i][jn], 0, 0, 0);
       }
     }
-    return;
   }
+  wait_loads<0>();  // no load into LDS may land after the workgroup ends
+  if constexpr (KG == 2) {
+    // group 1's accumulators to group 0 through the X buffers, summed in group 0, which writes the
+    // tile (BM x BN fp32: 2 buffers hold BM x 128)
+    static_assert(BM * BN * 4 <= 2 * BM * CH * 16, "the k groups' sum goes through two X buffers");
+    constexpr int HALF = BM * CH;  // float4 slots a buffer
+    wait_lds();
+    ring_barrier();
+    if (g == 1) {
 #pragma unroll
-  for (int j = 0; j < TN; j++) {
-    const uint32_t n = nw + j * 16 + r16;
-    if (n >= N) continue;
-    const float sc = MX ? 1.0f : (float)__builtin_bit_cast(f16, S[n]);
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          const int r = ((wl * TM + i) * TN + j) * 64;  // wave-uniform
+          floatx4 *d = r < HALF ? (floatx4 *)xr[0] + r : (floatx4 *)xr[1] + (r - HALF);
+          d[lane] = acc[i][j];
+        }
+    }
+    wait_lds();
+    ring_barrier();
+    if (g == 1) return;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint32_t m = m0 + wm * (BM / WM) + i * 16 + q * 4 + r;
-        if (m < M) store_out(Y, (size_t)m * N + n, MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc, mode);
+      for (int j = 0; j < TN; j++) {
+        const int r = ((wl * TM + i) * TN + j) * 64;
+        const floatx4 *d = r < HALF ? (const floatx4 *)xr[0] + r : (const floatx4 *)xr[1] + (r - HALF);
+        acc[i][j] += d[lane];
       }
   }
+  store_tile<BM, WM, TM, TN, MX>(acc, s0, S, Y, M, N, m0, nw, wm, r16, q, mode);
 }
 
 }  // namespace hwk_gemm
