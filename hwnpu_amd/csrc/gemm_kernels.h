@@ -571,8 +571,9 @@ __device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restric
 
   // A step j: wait for this wave's loads of step j (those of step j+1 stay in flight), a barrier
   // (every wave's loads of step j have landed, and every wave is done with the buffers of step j-1),
-  // the loads of step j+RS-1 into those buffers, then the step's weight operands from LDS and the
-  // MFMAs, each kk's weights converted next to the MFMAs that take them.
+  // the loads of step j+RS-1 into those buffers, then the step's operands from LDS (every X operand
+  // of the step read at once: read one at a time before its MFMA, each read's latency showed) and
+  // the MFMAs, each kk's weights converted next to the MFMAs that take them.
   for (uint32_t j0 = 0; j0 < steps; j0 += RS) {
 #pragma unroll
     for (int s = 0; s < RS; s++) {
@@ -614,13 +615,23 @@ __device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restric
           }
         }
       }
-      auto operands = [&](half8 (&af)[TM], half8 (&bf)[TN], int kk) __attribute__((always_inline)) {
+      // every X operand of the step read from LDS at once, pinned in registers (an empty asm per value
+      // after all the reads), so that the reads are all in flight together
+      u32x4 ax[KKG][TM];
+#pragma unroll
+      for (int kk = 0; kk < KKG; kk++)
 #pragma unroll
         for (int i = 0; i < TM; i++) {
           const int row = wm * (BM / WM) + i * 16 + r16;
           const int ch = KG == 1 ? xchunk<MX>(q, kk) : xchunk<MX>(q, g * KKG + kk);
-          af[i] = __builtin_bit_cast(half8, xb[row * CH + (ch ^ (row & 15))]);
+          ax[kk][i] = xb[row * CH + (ch ^ (row & 15))];
         }
+      issue_order();
+#pragma unroll
+      for (int kk = 0; kk < KKG; kk++)
+#pragma unroll
+        for (int i = 0; i < TM; i++) asm volatile("" : "+v"(ax[kk][i]));
+      auto bops = [&](half8 (&bf)[TN], int kk) __attribute__((always_inline)) {
 #pragma unroll
         for (int jn = 0; jn < TN; jn++) {
           if constexpr (MX) {
@@ -631,16 +642,17 @@ __device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restric
           }
         }
       };
-      half8 af[2][TM], bf[2][TN];
-      operands(af[0], bf[0], 0);
+      half8 bf[2][TN];
+      bops(bf[0], 0);
 #pragma unroll
       for (int kk = 0; kk < KKG; kk++) {
-        if (kk + 1 < KKG) operands(af[(kk + 1) & 1], bf[(kk + 1) & 1], kk + 1);
+        if (kk + 1 < KKG) bops(bf[(kk + 1) & 1], kk + 1);
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
           for (int jn = 0; jn < TN; jn++)
-            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[kk & 1][i], bf[kk & 1][jn], acc[i][jn], 0, 0, 0);
+            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ax[kk][i]), bf[kk & 1][jn],
+                                                                acc[i][jn], 0, 0, 0);
       }
     }
   }
