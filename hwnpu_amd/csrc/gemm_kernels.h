@@ -285,6 +285,99 @@ __device__ __forceinline__ void store_tile(const floatx4 (&acc)[TM][TN], const i
   }
 }
 
+// The same stores through LDS: the wave's block (RW x CW) into its region st of LDS, as the values
+// stored (fp16 rounded, or SwiGLU'd pairs, or scaled fp32), then 16-byte pieces of its rows to Y: an
+// MFMA tile's lanes hold one column each, so a direct store instruction writes 2 or 4 bytes a lane.
+// Every value is rounded and combined as store_tile does it. The fp32 rows are padded (P32 = CW + 4
+// floats) so that the 4 row groups of a write land in different banks (P32 = CW where the padded
+// block does not fit); the fp16 rows are not (padding them measured no faster: their reads of 16
+// bytes a lane then conflict). Needs Y 16-byte aligned and N a multiple of the piece (4 fp32, 8 fp16
+// or 16 SwiGLU columns): staged() tells.
+__device__ __forceinline__ bool staged(const void *Y, uint32_t N, int mode) {
+  const uint32_t piece = mode == kOutSwiGLU ? 16 : mode == HWK_OUT_F16 ? 8 : 4;
+  return ((uintptr_t)Y & 15) == 0 && N % piece == 0;
+}
+template <int TM, int TN, int P32>
+struct StageRows {
+  static constexpr int RW = TM * 16, CW = TN * 16;
+  static constexpr int P16 = CW, PH = CW / 2 + 8;  // fp16 rows: full width, SwiGLU half width (padded)
+  static constexpr int FLOATS = RW * P32;              // a region, in floats (the largest of the three)
+  static_assert(P32 == CW || P32 == CW + 4, "fp32 row stride");
+  static_assert(RW * P16 * 2 <= FLOATS * 4 && RW * PH * 2 <= FLOATS * 4, "fp16 rows fit the region");
+};
+template <int BM, int WM, int TM, int TN, bool MX, int P32>
+__device__ __forceinline__ void store_tile_staged(const floatx4 (&acc)[TM][TN], const int (&s0)[TN],
+                                                  const uint16_t *__restrict__ S, void *__restrict__ Y, uint32_t M,
+                                                  uint32_t N, uint32_t m0, uint32_t nw, int wm, int lane, int mode,
+                                                  float *st) {
+  using G = StageRows<TM, TN, P32>;
+  constexpr int RW = G::RW, CW = G::CW;
+  const int r16 = lane & 15, q = lane >> 4;
+  const uint32_t r0 = m0 + wm * RW;
+  auto value = [&](int i, int j, int r) __attribute__((always_inline)) {
+    const float sc = MX ? 1.0f : (float)__builtin_bit_cast(f16, S[min(nw + j * 16 + r16, N - 1)]);
+    return MX ? ldexpf(acc[i][j][r], s0[j]) : acc[i][j][r] * sc;
+  };
+  if (mode == kOutSwiGLU) {
+    // the pairs as store_tile makes them: gate lane rows 0, 1 of its quad, up lane rows 2, 3
+    f16 *h = (f16 *)st;
+    const bool gate = (r16 & 1) == 0;
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[r] = value(i, j, r);
+        const float o0 = __shfl_xor(gate ? v[2] : v[0], 1, 64), o1 = __shfl_xor(gate ? v[3] : v[1], 1, 64);
+        const int row = i * 16 + q * 4 + (gate ? 0 : 2), c = (j * 16 + r16) / 2;
+        h[row * G::PH + c] = (f16)(gate ? swiglu_value(v[0], o0) : swiglu_value(o0, v[2]));
+        h[(row + 1) * G::PH + c] = (f16)(gate ? swiglu_value(v[1], o1) : swiglu_value(o1, v[3]));
+      }
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // this wave's LDS writes done
+    constexpr int CPR = CW / 16;  // 8 outputs a piece
+    for (int c = lane; c < RW * CPR; c += 64) {
+      const int row = c / CPR, k = c % CPR;
+      const uint32_t m = r0 + row, n = nw + k * 16;
+      if (m < M && n < N)
+        *(u32x4 *)((f16 *)Y + (size_t)m * (N / 2) + n / 2) = *(const u32x4 *)(h + row * G::PH + k * 8);
+    }
+  } else if (mode == HWK_OUT_F16) {
+    f16 *h = (f16 *)st;
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) h[(i * 16 + q * 4 + r) * G::P16 + j * 16 + r16] = (f16)f32_value(value(i, j, r));
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+    constexpr int CPR = CW / 8;
+    for (int c = lane; c < RW * CPR; c += 64) {
+      const int row = c / CPR, k = c % CPR;
+      const uint32_t m = r0 + row, n = nw + k * 8;
+      if (m < M && n < N) *(u32x4 *)((f16 *)Y + (size_t)m * N + n) = *(const u32x4 *)(h + row * G::P16 + k * 8);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) st[(i * 16 + q * 4 + r) * P32 + j * 16 + r16] = value(i, j, r);
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+    constexpr int CPR = CW / 4;
+    for (int c = lane; c < RW * CPR; c += 64) {
+      const int row = c / CPR, k = c % CPR;
+      const uint32_t m = r0 + row, n = nw + k * 4;
+      if (m >= M || n >= N) continue;
+      floatx4 v = *(const floatx4 *)(st + row * P32 + k * 4);
+      floatx4 *y = (floatx4 *)((float *)Y + (size_t)m * N + n);
+      if (mode == HWK_OUT_ADD_F32) v = *y + v;
+      *y = v;
+    }
+  }
+}
+
 template <int BM, int BN, bool MX, int WM, int WN, int KG = 1>
 __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
                                         const uint8_t *__restrict__ E, const uint16_t *__restrict__ S,
@@ -410,11 +503,24 @@ __device__ __forceinline__ void gemm_wg(uint32_t bx, const u32x4 *__restrict__ X
         for (int j = 0; j < TN; j++) red[((wl * TM + i) * TN + j) * 64 + lane] = acc[i][j];
     }
     __syncthreads();
+    if (g == 0) {
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] += red[((wl * TM + i) * TN + j) * 64 + lane];
+    }
+    __syncthreads();  // group 0 is done with the sums' buffers, which its stores reuse
     if (g == 1) return;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int j = 0; j < TN; j++) acc[i][j] += red[((wl * TM + i) * TN + j) * 64 + lane];
+  }
+  if (staged(Y, N, mode)) {
+    // a wave's block in region wl of the X buffers (rows padded where that fits)
+    constexpr int CW = TN * 16, PAD = WM * WN * TM * 16 * (CW + 4) <= 2 * BM * CH * 4 ? CW + 4 : CW;
+    using G = StageRows<TM, TN, PAD>;
+    static_assert(WM * WN * G::FLOATS <= 2 * BM * CH * 4, "the staged blocks fit the X buffers");
+    if constexpr (KG == 1) __syncthreads();  // every wave is done with the X buffers
+    store_tile_staged<BM, WM, TM, TN, MX, PAD>(acc, s0, S, Y, M, N, m0, nw, wm, lane, mode,
+                                               (float *)&As[0][0] + wl * G::FLOATS);
+    return;
   }
   store_tile<BM, WM, TM, TN, MX>(acc, s0, S, Y, M, N, m0, nw, wm, r16, q, mode);
 }
@@ -676,15 +782,32 @@ __device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restric
     }
     wait_lds();
     ring_barrier();
+    if (g == 0) {
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          const int r = ((wl * TM + i) * TN + j) * 64;
+          const floatx4 *d = r < HALF ? (const floatx4 *)xr[0] + r : (const floatx4 *)xr[1] + (r - HALF);
+          acc[i][j] += d[lane];
+        }
+    }
+    wait_lds();
+    ring_barrier();  // group 0 is done with the sums' buffers, which its stores reuse
     if (g == 1) return;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const int r = ((wl * TM + i) * TN + j) * 64;
-        const floatx4 *d = r < HALF ? (const floatx4 *)xr[0] + r : (const floatx4 *)xr[1] + (r - HALF);
-        acc[i][j] += d[lane];
-      }
+  }
+  if (staged(Y, N, mode)) {
+    // a wave's block in region wl of the X buffers, PER regions a buffer
+    using G = StageRows<TM, TN, TN * 16 + 4>;
+    constexpr int PER = BM * CH * 4 / G::FLOATS;
+    static_assert(PER >= 1 && (WM * WN + PER - 1) / PER <= RS, "the staged blocks fit the X buffers");
+    if constexpr (KG == 1) {
+      wait_lds();
+      ring_barrier();  // every wave is done with the ring's buffers
+    }
+    store_tile_staged<BM, WM, TM, TN, MX, TN * 16 + 4>(acc, s0, S, Y, M, N, m0, nw, wm, lane, mode,
+                                                       (float *)xr[wl / PER] + (wl % PER) * G::FLOATS);
+    return;
   }
   store_tile<BM, WM, TM, TN, MX>(acc, s0, S, Y, M, N, m0, nw, wm, r16, q, mode);
 }
