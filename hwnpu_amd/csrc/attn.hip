@@ -27,32 +27,36 @@ __global__ __launch_bounds__(64 * W) void k_attn_decode(const f16 *__restrict__ 
 
 // ---- the model's decode attention (K4m): k_attn_decode's tiles with the step's own q, k, v ----
 //
-// Workgroup (kv head h, chunk c) of W waves over the keys [c*chunk, min((c+1)*chunk, p+1)) for the token
-// at position p = *pos; the grid covers the cache's capacity and a workgroup whose chunk starts past p
-// attends no key and leaves a partial of weight 0 (l = 0). Prologue: q for the kv head's G query heads
-// comes from the fp32 projection qkv (heads + 2*kvh rows of 128) through the per-head RMSNorm and RoPE
-// (the step's cos/sin row, cos | sin of 64 values each, made by the step's first kernel); the workgroup
-// whose chunk holds p (the owner) also makes the new k (normed, rotated) and v, writes them to the
-// caches at p for later steps and keeps them in LDS: the tile holding p takes them from there in place
-// of its load of row p, so the owner waits on no store. Every load of the prologue and both tiles is
-// issued before the first wait (the tiles' rows do not depend on p). Each workgroup leaves its partial
-// (o unnormalized, m in natural-log units, l) per query head with plain stores at slot
-// (h*nchunk + c)*G + g; the o_proj GEMV merges them (mxfp4_gemv_x's X_MERGE).
-template <int G, int W, bool ONE>
-__global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ qkv, const float *__restrict__ qn,
-                                                      const float *__restrict__ kn, const float *__restrict__ rope,
-                                                      double eps, f16 *__restrict__ kc, f16 *__restrict__ vc,
-                                                      float *__restrict__ ws_o, float *__restrict__ ws_m,
-                                                      float *__restrict__ ws_l, const int32_t *__restrict__ pos,
-                                                      uint32_t heads, uint32_t kvh, uint32_t cap, uint32_t chunk,
-                                                      uint32_t nchunk, uint32_t kpw, float scale_log2) {
+// Workgroup (kv head h, chunk c, query-head group sub) of W waves over the keys [c*chunk, min((c+1)*chunk,
+// p+1)) for the token at position p = *pos, for G of the kv head's gd query heads (heads h*gd + sub*G ..
+// +G; blockIdx = sub * kvh * nchunk + h * nchunk + c). The gd/G workgroups of one (h, c) read the same
+// cache rows: the grid spreads the attention's VALU work over that many more CUs (a kv head's two query
+// heads in two workgroups of one head each: 1,393 -> 1,409 tokens/s on the C5 decode step), and with
+// kvh * nchunk a multiple of 8 they run on one XCD and share its L2. The grid covers the cache's
+// capacity and a workgroup whose chunk starts past p attends no key and leaves a partial of weight 0
+// (l = 0). Prologue: q for the workgroup's G query heads comes from the fp32 projection qkv (heads +
+// 2*kvh rows of 128) through the per-head RMSNorm and RoPE (the step's cos/sin row, cos | sin of 64
+// values each, made by the step's first kernel); the workgroups whose chunk holds p (the owners) also
+// make the new k (normed, rotated) and v and keep them in LDS, and the first of them (sub 0) writes
+// them to the caches at p for later steps: the tile holding p takes them from LDS in place of its load
+// of row p, so no owner waits on a store. Every load of the prologue and both tiles is issued before
+// the first wait (the tiles' rows do not depend on p). Each workgroup leaves its partial (o
+// unnormalized, m in natural-log units, l) per query head with plain stores at slot
+// (h*nchunk + c)*gd + sub*G + g; the o_proj GEMV merges them (mxfp4_gemv_x's X_MERGE).
+template <int G, int W, bool ONE, bool KEEP>
+__device__ __forceinline__ void attn_step_wg(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                             const float *__restrict__ kn, const float *__restrict__ rope, double eps,
+                                             f16 *__restrict__ kc, f16 *__restrict__ vc, float *__restrict__ ws_o,
+                                             float *__restrict__ ws_m, float *__restrict__ ws_l,
+                                             const int32_t *__restrict__ pos, uint32_t heads, uint32_t kvh,
+                                             uint32_t cap, uint32_t chunk, uint32_t nchunk, uint32_t kpw,
+                                             float scale_log2, uint32_t gd, uint32_t h, uint32_t c, uint32_t sub) {
   __shared__ float sm[W][G], sl[W][G];
   __shared__ float sacc[W][G][128];
   __shared__ __attribute__((aligned(16))) f16 qs[G][128];
   __shared__ __attribute__((aligned(16))) f16 knew[128], vnew[128];
-  kernarg_now(qkv, qn, kn, rope, eps, kc, vc, ws_o, ws_m, ws_l, pos, heads, kvh, cap, chunk, nchunk, kpw, scale_log2);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t h = blockIdx.x / nchunk, c = blockIdx.x % nchunk;
+  const uint32_t q0 = h * gd + sub * G;
   const uint32_t begin = c * chunk;
   const size_t head_base = (size_t)h * cap;
   // the position first (written by the previous step's argmax), then every load that does not depend
@@ -62,7 +66,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
   // wait counter: the position's wait holds nothing else, the RoPE's none of the tiles.
   const int32_t pv = load_first(pos);
   const uint32_t j0 = (uint32_t)wave < (uint32_t)G + 2 ? (uint32_t)wave : (uint32_t)G + 1;
-  auto job_row = [&](uint32_t j) { return j < G ? h * G + j : j == G ? heads + h : heads + kvh + h; };
+  auto job_row = [&](uint32_t j) { return j < G ? q0 + j : j == G ? heads + h : heads + kvh + h; };
   const float *nwp = j0 < G ? qn : kn;
   const float x0 = qkv[(size_t)job_row(j0) * 128 + lane], x1 = qkv[(size_t)job_row(j0) * 128 + lane + 64];
   const float nw0 = nwp[lane], nw1 = nwp[lane + 64];
@@ -70,9 +74,9 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
   issue_order();
   const uint32_t kb = begin + wave * kpw;
   KTile<false> ta, tb;
-  load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, kb, cap, lane);
+  load_ktile<false, KEEP>(ta, kc, vc, nullptr, nullptr, head_base, kb, cap, lane);
   issue_order();
-  if constexpr (!ONE) load_ktile<false>(tb, kc, vc, nullptr, nullptr, head_base, kb + 16, cap, lane);
+  if constexpr (!ONE) load_ktile<false, KEEP>(tb, kc, vc, nullptr, nullptr, head_base, kb + 16, cap, lane);
   issue_order();
   const uint32_t p = (uint32_t)__builtin_amdgcn_readfirstlane(pv), len = p + 1;
   // a workgroup whose chunk starts past p attends no key (no early exit: the compiler would move the
@@ -90,16 +94,20 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
     if (j == G + 1) {
       vnew[lane] = (f16)a0;
       vnew[lane + 64] = (f16)a1;
-      vc[(head_base + p) * 128 + lane] = (f16)a0;
-      vc[(head_base + p) * 128 + lane + 64] = (f16)a1;
+      if (sub == 0) {
+        vc[(head_base + p) * 128 + lane] = (f16)a0;
+        vc[(head_base + p) * 128 + lane + 64] = (f16)a1;
+      }
     } else if (j < G) {
       qs[j][lane] = (f16)o0;
       qs[j][lane + 64] = (f16)o1;
     } else {
       knew[lane] = (f16)o0;
       knew[lane + 64] = (f16)o1;
-      kc[(head_base + p) * 128 + lane] = (f16)o0;
-      kc[(head_base + p) * 128 + lane + 64] = (f16)o1;
+      if (sub == 0) {
+        kc[(head_base + p) * 128 + lane] = (f16)o0;
+        kc[(head_base + p) * 128 + lane + 64] = (f16)o1;
+      }
     }
   };
   make_job(j0, x0, x1, nw0, nw1, (uint32_t)wave < jobs);
@@ -139,17 +147,17 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
     for (; i + 3 < nt; i += 2, key += 32) {
       patch(ta, key);
       attend_ktile<G, false>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
-      load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
+      load_ktile<false, KEEP>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
       patch(tb, key + 16);
       attend_ktile<G, false>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
-      load_ktile<false>(tb, kc, vc, nullptr, nullptr, head_base, key + 48, cap, lane);
+      load_ktile<false, KEEP>(tb, kc, vc, nullptr, nullptr, head_base, key + 48, cap, lane);
     }
     const uint32_t rem = nt - i;  // 0 .. 3
     if (rem >= 1) {
       patch(ta, key);
       attend_ktile<G, false>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
     }
-    if (rem == 3) load_ktile<false>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
+    if (rem == 3) load_ktile<false, KEEP>(ta, kc, vc, nullptr, nullptr, head_base, key + 32, cap, lane);
     if (rem >= 2) {
       patch(tb, key + 16);
       attend_ktile<G, false>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
@@ -174,7 +182,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
     sl[wave][lane] = ls;
   }
   __syncthreads();
-  const size_t base = ((size_t)h * nchunk + c) * G;
+  const size_t base = ((size_t)h * nchunk + c) * gd + sub * G;
   for (uint32_t t = threadIdx.x; t < (uint32_t)G * 128; t += 64 * W) {
     const uint32_t g = t / 128, d = t % 128;
     float top = -__builtin_inff();
@@ -195,6 +203,29 @@ __global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ 
       ws_l[base + g] = lsum;
     }
   }
+}
+
+// The workgroup's chunk is read with cache-allocating loads when it starts below keep_rows (the rows
+// of every layer's cache that the caller keeps in the memory-side cache), else with nontemporal ones.
+template <int G, int W, bool ONE>
+__global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                                      const float *__restrict__ kn, const float *__restrict__ rope,
+                                                      double eps, f16 *__restrict__ kc, f16 *__restrict__ vc,
+                                                      float *__restrict__ ws_o, float *__restrict__ ws_m,
+                                                      float *__restrict__ ws_l, const int32_t *__restrict__ pos,
+                                                      uint32_t heads, uint32_t kvh, uint32_t cap, uint32_t chunk,
+                                                      uint32_t nchunk, uint32_t kpw, float scale_log2, uint32_t gd,
+                                                      uint32_t keep_rows) {
+  kernarg_now(qkv, qn, kn, rope, eps, kc, vc, ws_o, ws_m, ws_l, pos, heads, kvh, cap, chunk, nchunk, kpw, scale_log2, gd,
+              keep_rows);
+  const uint32_t nkc = kvh * nchunk, sub = blockIdx.x / nkc, rest = blockIdx.x % nkc;
+  const uint32_t h = rest / nchunk, c = rest % nchunk;
+  if (c * chunk < keep_rows)
+    attn_step_wg<G, W, ONE, true>(qkv, qn, kn, rope, eps, kc, vc, ws_o, ws_m, ws_l, pos, heads, kvh, cap, chunk,
+                                  nchunk, kpw, scale_log2, gd, h, c, sub);
+  else
+    attn_step_wg<G, W, ONE, false>(qkv, qn, kn, rope, eps, kc, vc, ws_o, ws_m, ws_l, pos, heads, kvh, cap, chunk,
+                                   nchunk, kpw, scale_log2, gd, h, c, sub);
 }
 
 // Merge of chunks (the reference's Merge rule, paged.go:252-310): top = the largest m among
@@ -490,7 +521,8 @@ char *hwk::attn_decode_dev(hipStream_t st, const void *q, const void *k, const v
 
 // The model step's split: 4 waves a workgroup, kpw keys a wave (32: two tiles, both in flight), chunk =
 // 4*kpw keys; kpw grows past 32 so that a kv head has at most kStepMaxChunks chunks (the o_proj GEMV
-// merges every chunk's partial in its prologue). (Eight waves of one tile each were measured no faster.)
+// merges every chunk's partial in its prologue); one query head a workgroup (two for 4 or more a kv
+// head). (Eight waves of one tile each were measured no faster, with one or two heads a workgroup.)
 constexpr int kStepWaves = 4;
 constexpr uint32_t kStepMaxChunks = 16;
 
@@ -510,7 +542,7 @@ size_t hwk::attn_step_workspace_bytes(const hwk_attn_params *p) {
 
 char *hwk::attn_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *rope, double eps,
                      void *kc, void *vc, void *workspace, size_t workspace_bytes, const hwk_attn_params *p,
-                     const int32_t *pos) {
+                     const int32_t *pos, uint32_t keep_rows) {
   HWK_CHECK(p && qkv && qn && kn && rope && kc && vc && workspace && pos, "attn_step: null argument");
   HWK_CHECK(p->head_dim == 128 && !p->kv_int8, "attn_step: fp16 caches of head_dim 128 only");
   HWK_CHECK(p->kv_heads > 0 && p->heads % p->kv_heads == 0, "attn_step: %u heads over %u", p->heads, p->kv_heads);
@@ -525,12 +557,11 @@ char *hwk::attn_step(hipStream_t st, const float *qkv, const float *qn, const fl
   constexpr int W = kStepWaves;
   const uint32_t kpw = chunk / W;
 #define HWK_STEP2(GG, ONE)                                                                                        \
-  hipLaunchKernelGGL((k_attn_step<GG, W, ONE>), dim3(p->kv_heads * nchunk), dim3(64 * W), 0, st, qkv, qn, kn, rope,   \
-                     eps, (f16 *)kc, (f16 *)vc, ws_o, ws_m, ws_l, pos, p->heads, p->kv_heads, p->capacity, chunk,      \
-                     nchunk, kpw, scale_log2)
-  if (G == 1) HWK_STEP2(1, false);
-  else if (G == 2) HWK_STEP2(2, false);
-  else HWK_STEP2(4, false);
+  hipLaunchKernelGGL((k_attn_step<GG, W, ONE>), dim3(p->kv_heads * nchunk * (G / GG)), dim3(64 * W), 0, st, qkv, qn, kn, \
+                     rope, eps, (f16 *)kc, (f16 *)vc, ws_o, ws_m, ws_l, pos, p->heads, p->kv_heads, p->capacity, chunk, \
+                     nchunk, kpw, scale_log2, G, keep_rows)
+  if (G == 1 || G == 2) HWK_STEP2(1, false);
+  else HWK_STEP2(2, false);
 #undef HWK_STEP2
   return hwk::launched("attn_step");
 }

@@ -100,15 +100,20 @@ __device__ __forceinline__ uint32_t kstep_dim(int s, int lane) {
   return I8 ? 64 * (s >> 1) + 16 * (lane >> 4) + 8 * (s & 1) : 32 * s + 8 * (lane >> 4);
 }
 
-template <bool I8>
+// KEEP: the cache rows are read with ordinary (cache-allocating) loads, for rows that later calls read
+// again and that fit the memory-side cache together (the model's decode step keeps a prefix of every
+// layer's cache there; its weights stream with nontemporal loads and do not evict it); otherwise
+// with nontemporal loads, which leave the memory-side cache to other data.
+template <bool I8, bool KEEP = false>
 __device__ __forceinline__ void load_ktile(KTile<I8> &t, const void *__restrict__ k, const void *__restrict__ v,
                                            const uint16_t *__restrict__ ks, const uint16_t *__restrict__ vs,
                                            size_t head_base, uint32_t key0, uint32_t rows, int lane) {
+  auto ld = [](const void *a) { return KEEP ? *(const uint4 *)a : load_stream((const uint4 *)a); };
   const size_t rk = head_base + min(key0 + (lane & 15), rows - 1);
   if constexpr (I8) {
 #pragma unroll
     for (int j = 0; j < 2; j++)
-      t.kraw[j] = load_stream((const uint4 *)((const int8_t *)k + rk * 128 + 64 * j + 16 * (lane >> 4)));
+      t.kraw[j] = ld((const int8_t *)k + rk * 128 + 64 * j + 16 * (lane >> 4));
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const size_t rv = head_base + min(key0 + 4 * (lane >> 4) + r, rows - 1);
@@ -118,11 +123,11 @@ __device__ __forceinline__ void load_ktile(KTile<I8> &t, const void *__restrict_
     }
   } else {
 #pragma unroll
-    for (int s = 0; s < 4; s++) t.k[s] = half8_of(load_stream((const uint4 *)((const f16 *)k + rk * 128 + kstep_dim<false>(s, lane))));
+    for (int s = 0; s < 4; s++) t.k[s] = half8_of(ld((const f16 *)k + rk * 128 + kstep_dim<false>(s, lane)));
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const size_t rv = head_base + min(key0 + 4 * (lane >> 4) + r, rows - 1);
-      t.v[r] = half8_of(load_stream((const uint4 *)((const f16 *)v + rv * 128 + (lane & 15) * 8)));
+      t.v[r] = half8_of(ld((const f16 *)v + rv * 128 + (lane & 15) * 8));
     }
   }
 }

@@ -44,11 +44,13 @@ char *attn_decode_dev(hipStream_t st, const void *q, const void *k, const void *
 // (kv head * nchunk + chunk) * G + g of the workspace: o (slots, 128) | m (slots) | l (slots). Every
 // chunk of the capacity is written; a chunk past *pos has l = 0 and weighs nothing in the merge.
 // attn_step_layout gives the chunking (fixed by the capacity), which the merging consumer needs.
+// Cache rows below keep_rows are read with cache-allocating loads (the caller sizes it so that those
+// rows of every layer fit the memory-side cache together), the others with nontemporal loads.
 void attn_step_layout(const hwk_attn_params *p, uint32_t *chunk, uint32_t *nchunk);
 size_t attn_step_workspace_bytes(const hwk_attn_params *p);
 char *attn_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *rope, double eps,
                 void *kc, void *vc, void *workspace, size_t workspace_bytes, const hwk_attn_params *p,
-                const int32_t *pos);
+                const int32_t *pos, uint32_t keep_rows);
 
 }  // namespace hwk
 

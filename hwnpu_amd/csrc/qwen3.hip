@@ -264,6 +264,10 @@ struct hwk_qwen3 {
   int32_t *hist, *pos;
   uint32_t *counter, *part_i;
   uint32_t step_chunk = 0, step_nchunk = 0;  // the decode attention's chunking (attn_step_layout)
+  // a decode step reading at most keep_rows cache rows of every layer reads them with cache-allocating
+  // loads (they then stay in the memory-side cache from step to step), a later one with nontemporal
+  // loads
+  uint32_t keep_rows = 0;
   float *part_v, *logits;
   uint64_t *cache_tab;  // the K/V caches' base pointers in the export order (kv_k_N_new / kv_v_N_new sorted)
   float *vlogits;       // a verify's logits (kMaxVerify, vocab) and greedy tokens (kMaxVerify)
@@ -278,14 +282,21 @@ struct hwk_qwen3 {
   bool started = false;
   hipStream_t cap = nullptr;
   // the decode step captured once as a graph of one step and one of kGraphSteps steps (a step
-  // reads its token and position on the device and advances them, so consecutive replays chain)
-  hipGraphExec_t exec[2] = {nullptr, nullptr};
-  hipGraph_t graph[2] = {nullptr, nullptr};
+  // reads its token and position on the device and advances them, so consecutive replays chain),
+  // each with the cache rows read nontemporally [0][.] or kept [1][.]
+  hipGraphExec_t exec[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+  hipGraph_t graph[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
 };
 
 namespace {
 
 constexpr uint32_t kMaxVerify = 8;  // rows a speculative verify takes
+// The most KV cache bytes (all layers) a decode step reads with cache-allocating loads: up to that
+// many, the rows stay in the device's 256 MB memory-side cache from one step to the next (the
+// weights stream past it with nontemporal loads; their fp4 scale bytes, 1/17 of them, are the other
+// data it keeps). Measured on the C5 decode (28 layers, 4 KB a position): keeping the rows gains
+// 1.2-2.4 % up to position 1,695 (195 MB) and loses 1.5 % from 1,696 on; nontemporal loads past it.
+constexpr uint64_t kKeepCacheBytes = 176ull << 20;
 
 struct Carver {
   size_t off = 0;
@@ -357,11 +368,16 @@ void layout(hwk_qwen3 *m, uint8_t *base) {
 // Steps a replay of the long graph runs: the gap between graph launches is paid once for them.
 constexpr uint32_t kGraphSteps = 8;
 
-// Captures graph slot i (n decode steps) on the model's private stream the first time it is needed.
-char *capture(hwk_qwen3 *m, int i, uint32_t n);
+// Captures graph slot [keep][i] (n decode steps) on the model's private stream the first time it is
+// needed.
+char *capture(hwk_qwen3 *m, int keep, int i, uint32_t n);
 
-// The decode step on stream st: the token hist[*pos] at position *pos.
-char *step(hwk_qwen3 *m, hipStream_t st) {
+// Whether steps whose last one writes position last (and reads cache rows 0 .. last) keep the rows.
+bool keeps(const hwk_qwen3 *m, uint32_t last) { return last < m->keep_rows; }
+
+// The decode step on stream st: the token hist[*pos] at position *pos; keep: the attention reads the
+// cache rows with cache-allocating loads.
+char *step(hwk_qwen3 *m, hipStream_t st, bool keep) {
   const hwk_qwen3_config &c = m->c;
   hipLaunchKernelGGL(k_step_embed, dim3(embed_blocks(c.hidden)), dim3(256), 0, st, m->hist, m->pos, m->embed, m->h,
                      c.hidden, c.vocab, m->cos_t, m->sin_t, m->rope_now);
@@ -371,7 +387,7 @@ char *step(hwk_qwen3 *m, hipStream_t st) {
                             HWK_OUT_F32, false));
     // attention partials over chunks of the cache, merged by the o_proj GEMV into its input
     HWK_Q(hwk::attn_step(st, m->qkv, ly.q_norm, ly.k_norm, m->rope_now, m->eps, ly.kc, ly.vc, m->ws, m->ws_bytes,
-                         &m->ap, m->pos));
+                         &m->ap, m->pos, keep ? UINT32_MAX : 0u));
     HWK_Q(hwk::mxfp4_gemv_merge(st, ly.o.w, ly.o.e, m->ws, c.heads, c.heads / c.kv_heads, m->step_nchunk, m->h,
                                 c.hidden, HWK_OUT_ADD_F32));
     HWK_Q(hwk::mxfp4_gemv_x(st, ly.gu.w, ly.gu.e, nullptr, m->h, ly.post_norm, m->eps, m->a16, 2 * c.inter, c.hidden,
@@ -385,11 +401,11 @@ char *step(hwk_qwen3 *m, hipStream_t st) {
   return hwk::launched("qwen3 argmax");
 }
 
-char *capture(hwk_qwen3 *m, int i, uint32_t n) {
-  if (m->exec[i]) return nullptr;
+char *capture(hwk_qwen3 *m, int keep, int i, uint32_t n) {
+  if (m->exec[keep][i]) return nullptr;
   HWK_TRY("hipStreamBeginCapture", hipStreamBeginCapture(m->cap, hipStreamCaptureModeRelaxed));
   char *err = nullptr;
-  for (uint32_t s = 0; s < n && !err; s++) err = step(m, m->cap);
+  for (uint32_t s = 0; s < n && !err; s++) err = step(m, m->cap, keep != 0);
   hipGraph_t g = nullptr;
   hipError_t e = hipStreamEndCapture(m->cap, &g);
   if (err) {
@@ -397,8 +413,8 @@ char *capture(hwk_qwen3 *m, int i, uint32_t n) {
     return err;
   }
   if (e != hipSuccess) return hwk::hip_err("hipStreamEndCapture", e);
-  m->graph[i] = g;
-  HWK_TRY("hipGraphInstantiate", hipGraphInstantiate(&m->exec[i], g, nullptr, nullptr, 0));
+  m->graph[keep][i] = g;
+  HWK_TRY("hipGraphInstantiate", hipGraphInstantiate(&m->exec[keep][i], g, nullptr, nullptr, 0));
   return nullptr;
 }
 
@@ -520,6 +536,10 @@ HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
   ap.split = 0;
   hwk::attn_step_layout(&ap, &m->step_chunk, &m->step_nchunk);
   m->ws_bytes = hwk::attn_step_workspace_bytes(&ap);
+  {
+    const uint64_t row = (uint64_t)c.layers * c.kv_heads * c.head_dim * 2 * sizeof(uint16_t);
+    m->keep_rows = (uint32_t)std::min<uint64_t>(kKeepCacheBytes / row, c.max_ctx);
+  }
   layout(m, nullptr);
   hipError_t e = hipMalloc((void **)&m->base, m->bytes);
   if (e != hipSuccess) {
@@ -567,10 +587,11 @@ HWK_API char *hwk_qwen3_new(const hwk_qwen3_config *cfg, hwk_qwen3 **out) {
 
 HWK_API void hwk_qwen3_free(hwk_qwen3 *m) {
   if (!m) return;
-  for (int i = 0; i < 2; i++) {
-    if (m->exec[i]) (void)hipGraphExecDestroy(m->exec[i]);
-    if (m->graph[i]) (void)hipGraphDestroy(m->graph[i]);
-  }
+  for (int k = 0; k < 2; k++)
+    for (int i = 0; i < 2; i++) {
+      if (m->exec[k][i]) (void)hipGraphExecDestroy(m->exec[k][i]);
+      if (m->graph[k][i]) (void)hipGraphDestroy(m->graph[k][i]);
+    }
   if (m->cap) (void)hipStreamDestroy(m->cap);
   if (m->base) {
     (void)hipDeviceSynchronize();
@@ -683,7 +704,7 @@ HWK_API char *hwk_qwen3_step(hwk_qwen3 *m, void *stream) {
   HWK_CHECK(m->started, "hwk_qwen3_step: no prompt yet");
   HWK_CHECK((uint64_t)m->host_pos + 1 < m->c.max_ctx, "hwk_qwen3_step: position %u is the last of %u", m->host_pos,
             m->c.max_ctx);
-  HWK_Q(step(m, (hipStream_t)stream));
+  HWK_Q(step(m, (hipStream_t)stream, keeps(m, m->host_pos)));
   m->host_pos++;
   m->verify_n = 0;
   return nullptr;
@@ -695,10 +716,21 @@ HWK_API char *hwk_qwen3_decode(hwk_qwen3 *m, void *stream, uint32_t steps) {
   HWK_CHECK((uint64_t)m->host_pos + steps < m->c.max_ctx, "hwk_qwen3_decode: %u steps from %u pass %u", steps,
             m->host_pos, m->c.max_ctx);
   const uint32_t many = steps / kGraphSteps, one = steps % kGraphSteps;
-  if (many) HWK_Q(capture(m, 1, kGraphSteps));
-  if (one) HWK_Q(capture(m, 0, 1));
-  for (uint32_t i = 0; i < many; i++) HWK_TRY("hipGraphLaunch", hipGraphLaunch(m->exec[1], (hipStream_t)stream));
-  for (uint32_t i = 0; i < one; i++) HWK_TRY("hipGraphLaunch", hipGraphLaunch(m->exec[0], (hipStream_t)stream));
+  // each replay takes the graph of its last position's cache policy; every graph a replay needs is
+  // captured before the first launch
+  for (int pass = 0; pass < 2; pass++) {
+    uint32_t p = m->host_pos;
+    for (uint32_t i = 0; i < many + one; i++) {
+      const int len = i < many ? 1 : 0;
+      const uint32_t n = len ? kGraphSteps : 1;
+      const int keep = keeps(m, p + n - 1) ? 1 : 0;
+      if (pass == 0)
+        HWK_Q(capture(m, keep, len, n));
+      else
+        HWK_TRY("hipGraphLaunch", hipGraphLaunch(m->exec[keep][len], (hipStream_t)stream));
+      p += n;
+    }
+  }
   m->host_pos += steps;
   m->verify_n = 0;
   return nullptr;
@@ -706,8 +738,10 @@ HWK_API char *hwk_qwen3_decode(hwk_qwen3 *m, void *stream, uint32_t steps) {
 
 HWK_API char *hwk_qwen3_capture(hwk_qwen3 *m) {
   HWK_CHECK(m, "hwk_qwen3_capture: null model");
-  HWK_Q(capture(m, 1, kGraphSteps));
-  HWK_Q(capture(m, 0, 1));
+  for (int keep = 0; keep < 2; keep++) {
+    HWK_Q(capture(m, keep, 1, kGraphSteps));
+    HWK_Q(capture(m, keep, 0, 1));
+  }
   return nullptr;
 }
 
