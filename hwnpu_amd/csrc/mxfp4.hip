@@ -245,10 +245,10 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   __shared__ uint4 xs[NT * XD / 4];  // x (at least XC chunks)
   __shared__ double red[WPB];
   constexpr int MS = XM == X_MERGE ? 64 * BPL / 4 * kMergeMaxChunks : 1;  // (head, chunk) slots (X_MERGE)
-  constexpr int MPER = (MS + NT - 1) / NT;                                 // slots a thread stages
-  __shared__ __align__(16) float mm[MS + 64];  // m of (head, chunk); past MS one spare slot a lane
-  __shared__ __align__(16) float ml[MS + 64];  // l of (head, chunk)
-  __shared__ __align__(16) float mw[MS];       // weight of (head, chunk)
+  constexpr int MPER = (MS + NT - 1) / NT;                                 // slots a thread takes
+  static_assert(kMergeMaxChunks == 16 && NT % 16 == 0, "a head's chunks are one 16-lane DPP group");
+  __shared__ __align__(16) float ml[MS + 64];  // l of (head, chunk); past MS one spare slot a lane
+  __shared__ __align__(16) float mw[MS + 64];  // weight of (head, chunk)
   kernarg_now(w, e, y, n, nb, in.x16, in.h, in.nw, in.eps, in.ws, in.G, in.nchunk);
   const int t = threadIdx.x, lane = t & 63;
   const uint32_t k = nb * 32;
@@ -259,12 +259,11 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   uint32_t xv[XD];
   float4 ov[XM == X_MERGE ? M4 : 1][XM == X_MERGE ? MB : 1];
   float mv[XM == X_MERGE ? MPER : 1], lv[XM == X_MERGE ? MPER : 1];
-  uint32_t md[XM == X_MERGE ? MPER : 1];
   // every chunk of the partials is read: one past the step's position has l = 0 and weighs nothing
   const uint32_t live = XM == X_MERGE ? in.nchunk : 1;
   if constexpr (XM == X_MERGE) {
     // the partials: o of this thread's x values (4 consecutive dims of one query head a group), and
-    // every (head, chunk)'s m and l into LDS
+    // the m and l of (head, chunk) slots
     const uint32_t heads = k / 128, slots = heads * in.nchunk;
     const float *ws_m = in.ws + (size_t)slots * 128, *ws_l = ws_m + slots;
 #pragma unroll
@@ -277,16 +276,17 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
         ov[j][c] = *(const float4 *)(in.ws + slot * 128 + d);
       }
     }
-    // m and l into registers here, into LDS (every thread writing, past heads * live into its spare
-    // slot) once the weight loads are issued: a load whose only use sits under a branch would be
-    // sunk into it, behind the weight loads, with a wait for those too
+    // slot i = t + j*NT is (head i/16, chunk i%16): 16 lanes a head, so that the head's top is a
+    // 16-lane DPP max in registers (a chunk past live reads chunk live - 1 and a head past the last
+    // the last head's, unused); used once the weight loads are issued, with no use under a branch (a
+    // load whose only use sits under a branch would be sunk into it, behind the weight loads)
 #pragma unroll
     for (int j = 0; j < MPER; j++) {
-      const uint32_t i = t + j * NT, ic = min(i, heads * live - 1), hq = ic / live, cc = ic % live;
+      const uint32_t i = t + j * NT, hq = min(i / kMergeMaxChunks, heads - 1);
+      const uint32_t cc = min(i % kMergeMaxChunks, live - 1);
       const size_t slot = ((size_t)(hq / in.G) * in.nchunk + cc) * in.G + hq % in.G;
       mv[j] = ws_m[slot];
       lv[j] = ws_l[slot];
-      md[j] = i < heads * live ? hq * kMergeMaxChunks + cc : MS + lane;
     }
   } else if constexpr (XM == X_NORM) {
 #pragma unroll
@@ -340,67 +340,45 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
       if (t + j * NT < k) xh[t + j * NT] = (f16)f32_value((hv[j] * r) * wv[j]);
   } else if constexpr (XM == X_MERGE) {
     // the reference's Merge rule per query head: top = the largest m among chunks with l > 0, a chunk
-    // weighs exp(m - top), x = fp16(sum(w * o) / sum(w * l))
+    // weighs exp(m - top), x = fp16(sum(w * o) / sum(w * l)). Each slot's weight, and its l, into LDS
+    // (a chunk past live, of l <= 0 or of a head with none weighs 0; a thread past the slots writes
+    // its spare one)
+    const uint32_t heads = k / 128;
 #pragma unroll
     for (int j = 0; j < MPER; j++) {
-      mm[md[j]] = mv[j];
-      ml[md[j]] = lv[j];
+      const uint32_t i = t + j * NT;
+      const bool ok = (i < heads * kMergeMaxChunks) & (i % kMergeMaxChunks < live) & (lv[j] > 0.0f);
+      const float top = group_max_dpp<kMergeMaxChunks>(ok ? mv[j] : -__builtin_inff());
+      const uint32_t at = i < heads * kMergeMaxChunks ? i : MS + lane;
+      mw[at] = ok & (top != -__builtin_inff()) ? expf(mv[j] - top) : 0.0f;
+      ml[at] = lv[j];
     }
     __syncthreads();
-    const uint32_t heads = k / 128;
     typedef float f32x4 __attribute__((ext_vector_type(4)));
-    // every (head, chunk)'s weight, once for the workgroup: top over the head's chunks (its m and l
-    // read from LDS at once and held in registers by an empty asm, so that the compiler does not
-    // move each read into the branch of its chunk, a wait apiece; slots past live hold stale values,
-    // read but not used), then exp(m - top), or 0 for a chunk past live, of l <= 0 or of a head
-    // with none
-    for (uint32_t i = t; i < heads * kMergeMaxChunks; i += NT) {
-      const uint32_t hq = i / kMergeMaxChunks, c = i % kMergeMaxChunks;
-      const float *hm = mm + hq * kMergeMaxChunks, *hl = ml + hq * kMergeMaxChunks;
-      f32x4 m4[kMergeMaxChunks / 4], l4[kMergeMaxChunks / 4];
-#pragma unroll
-      for (int q = 0; q < (int)kMergeMaxChunks / 4; q++) {
-        m4[q] = ((const f32x4 *)hm)[q];
-        l4[q] = ((const f32x4 *)hl)[q];
-      }
-      const float mc = hm[c], lc = hl[c];
-#pragma unroll
-      for (int q = 0; q < (int)kMergeMaxChunks / 4; q++) asm volatile("" : "+v"(m4[q]), "+v"(l4[q]));
-      float top = -__builtin_inff();
-#pragma unroll
-      for (int cc = 0; cc < (int)kMergeMaxChunks; cc++)
-        if (((uint32_t)cc < live) & (l4[cc / 4][cc % 4] > 0.0f)) top = fmaxf(top, m4[cc / 4][cc % 4]);
-      const bool use = (c < live) & (lc > 0.0f) & (top != -__builtin_inff());
-      mw[i] = use ? expf(mc - top) : 0.0f;
-    }
-    __syncthreads();
 #pragma unroll
     for (int j = 0; j < M4; j++) {
       const uint32_t e = (uint32_t)(t + j * NT) * 4;
       if (e >= k) continue;
       const uint32_t hq = e / 128, d = e % 128;
       const float *hw = mw + hq * kMergeMaxChunks, *hl = ml + hq * kMergeMaxChunks;
-      // chunks in ascending order, the first MB unrolled with their weights and l read at once
+      // chunks in ascending order, the first MB with their weights and l read at once and no branch
+      // (a chunk of weight 0 adds +0: its o and l, a duplicate for a chunk past live, are finite)
       f32x4 w4[MB / 4], l4[MB / 4];
 #pragma unroll
       for (int q = 0; q < MB / 4; q++) {
         w4[q] = ((const f32x4 *)hw)[q];
         l4[q] = ((const f32x4 *)hl)[q];
       }
-#pragma unroll
-      for (int q = 0; q < MB / 4; q++) asm volatile("" : "+v"(w4[q]), "+v"(l4[q]));
       float den = 0.0f, n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
 #pragma unroll
       for (int c = 0; c < MB; c++) {
         const float wc = w4[c / 4][c % 4];
-        if (wc > 0.0f) {
-          const float4 o = ov[j][c];
-          den += wc * l4[c / 4][c % 4];
-          n0 += wc * o.x;
-          n1 += wc * o.y;
-          n2 += wc * o.z;
-          n3 += wc * o.w;
-        }
+        const float4 o = ov[j][c];
+        den += wc * l4[c / 4][c % 4];
+        n0 += wc * o.x;
+        n1 += wc * o.y;
+        n2 += wc * o.z;
+        n3 += wc * o.w;
       }
       for (uint32_t c = MB; c < live; c++) {
         const float wc = hw[c];
