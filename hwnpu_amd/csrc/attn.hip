@@ -205,22 +205,30 @@ __device__ __forceinline__ void attn_step_wg(const float *__restrict__ qkv, cons
   }
 }
 
-// The workgroup's chunk is read with cache-allocating loads when it starts below keep_rows (the rows
-// of every layer's cache that the caller keeps in the memory-side cache), else with nontemporal ones.
+// The arguments fit the 56 bytes the hardware preloads into SGPRs at wave launch
+// (-amdgpu-kernarg-preload-count), eps aside (loaded when first used): step = the step's RoPE row (cos
+// | sin, 64 each) followed by the position (int32); kc = the K cache, the V cache right after it
+// (kvh * cap rows of 128); ws = the partials o | m | l; qn = the q norm weights, the k norm weights
+// right after them; nk = nchunk | kpw << 16; hk = kvh | gd << 8 | keep << 16 (keep: the chunks are
+// read with cache-allocating loads, for a caller that keeps the rows in the memory-side cache, else
+// with nontemporal ones).
 template <int G, int W, bool ONE>
-__global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ qkv, const float *__restrict__ qn,
-                                                      const float *__restrict__ kn, const float *__restrict__ rope,
-                                                      double eps, f16 *__restrict__ kc, f16 *__restrict__ vc,
-                                                      float *__restrict__ ws_o, float *__restrict__ ws_m,
-                                                      float *__restrict__ ws_l, const int32_t *__restrict__ pos,
-                                                      uint32_t heads, uint32_t kvh, uint32_t cap, uint32_t chunk,
-                                                      uint32_t nchunk, uint32_t kpw, float scale_log2, uint32_t gd,
-                                                      uint32_t keep_rows) {
-  kernarg_now(qkv, qn, kn, rope, eps, kc, vc, ws_o, ws_m, ws_l, pos, heads, kvh, cap, chunk, nchunk, kpw, scale_log2, gd,
-              keep_rows);
+__global__ __launch_bounds__(64 * W) void k_attn_step(const float *__restrict__ step, const float *__restrict__ qkv,
+                                                      f16 *__restrict__ kc, float *__restrict__ ws,
+                                                      const float *__restrict__ qn, uint32_t cap, uint32_t nk,
+                                                      uint32_t hk, float scale_log2, double eps) {
+  kernarg_now(step, qkv, kc, ws, qn, cap, nk, hk, scale_log2);
+  const uint32_t nchunk = nk & 0xffffu, kpw = nk >> 16, kvh = hk & 0xffu, gd = (hk >> 8) & 0xffu;
+  const uint32_t heads = kvh * gd, chunk = kpw * W, slots = heads * nchunk;
+  const int32_t *pos = (const int32_t *)(step + 128);
+  f16 *vc = kc + (size_t)kvh * cap * 128;
+  float *ws_m = ws + (size_t)slots * 128, *ws_l = ws_m + slots;
+  const float *kn = qn + 128;
   const uint32_t nkc = kvh * nchunk, sub = blockIdx.x / nkc, rest = blockIdx.x % nkc;
   const uint32_t h = rest / nchunk, c = rest % nchunk;
-  if (c * chunk < keep_rows)
+  float *ws_o = ws;
+  const float *rope = step;
+  if ((hk >> 16) & 1u)
     attn_step_wg<G, W, ONE, true>(qkv, qn, kn, rope, eps, kc, vc, ws_o, ws_m, ws_l, pos, heads, kvh, cap, chunk,
                                   nchunk, kpw, scale_log2, gd, h, c, sub);
   else
@@ -542,7 +550,7 @@ size_t hwk::attn_step_workspace_bytes(const hwk_attn_params *p) {
 
 char *hwk::attn_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *rope, double eps,
                      void *kc, void *vc, void *workspace, size_t workspace_bytes, const hwk_attn_params *p,
-                     const int32_t *pos, uint32_t keep_rows) {
+                     const int32_t *pos, bool keep) {
   HWK_CHECK(p && qkv && qn && kn && rope && kc && vc && workspace && pos, "attn_step: null argument");
   HWK_CHECK(p->head_dim == 128 && !p->kv_int8, "attn_step: fp16 caches of head_dim 128 only");
   HWK_CHECK(p->kv_heads > 0 && p->heads % p->kv_heads == 0, "attn_step: %u heads over %u", p->heads, p->kv_heads);
@@ -551,15 +559,21 @@ char *hwk::attn_step(hipStream_t st, const float *qkv, const float *qn, const fl
   HWK_CHECK(workspace_bytes >= attn_step_workspace_bytes(p), "attn_step: workspace too small");
   uint32_t chunk, nchunk;
   attn_step_layout(p, &chunk, &nchunk);
-  const uint64_t slots = (uint64_t)p->heads * nchunk;
-  float *ws_o = (float *)workspace, *ws_m = ws_o + slots * 128, *ws_l = ws_m + slots;
+  float *ws_o = (float *)workspace;
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
   constexpr int W = kStepWaves;
   const uint32_t kpw = chunk / W;
+  // the kernel's compact arguments: the k norm weights, the V cache and the position each lie at a
+  // fixed offset from the q norm weights, the K cache and the RoPE row (the model's layout)
+  HWK_CHECK(kn == qn + 128 && (const f16 *)vc == (const f16 *)kc + (size_t)p->kv_heads * p->capacity * 128 &&
+                (const float *)pos == rope + 128,
+            "attn_step: the k norm, V cache or position not where the kernel takes them");
+  HWK_CHECK(p->kv_heads < 256 && G < 256 && nchunk < 65536 && kpw < 65536, "attn_step: %u kv heads, %u chunks",
+            p->kv_heads, nchunk);
+  const uint32_t nk = nchunk | kpw << 16, hk = p->kv_heads | G << 8 | (keep ? 1u : 0u) << 16;
 #define HWK_STEP2(GG, ONE)                                                                                        \
-  hipLaunchKernelGGL((k_attn_step<GG, W, ONE>), dim3(p->kv_heads * nchunk * (G / GG)), dim3(64 * W), 0, st, qkv, qn, kn, \
-                     rope, eps, (f16 *)kc, (f16 *)vc, ws_o, ws_m, ws_l, pos, p->heads, p->kv_heads, p->capacity, chunk, \
-                     nchunk, kpw, scale_log2, G, keep_rows)
+  hipLaunchKernelGGL((k_attn_step<GG, W, ONE>), dim3(p->kv_heads * nchunk * (G / GG)), dim3(64 * W), 0, st, rope, qkv, \
+                     (f16 *)kc, ws_o, qn, p->capacity, nk, hk, scale_log2, eps)
   if (G == 1 || G == 2) HWK_STEP2(1, false);
   else HWK_STEP2(2, false);
 #undef HWK_STEP2

@@ -44,13 +44,14 @@ char *attn_decode_dev(hipStream_t st, const void *q, const void *k, const void *
 // (kv head * nchunk + chunk) * G + g of the workspace: o (slots, 128) | m (slots) | l (slots). Every
 // chunk of the capacity is written; a chunk past *pos has l = 0 and weighs nothing in the merge.
 // attn_step_layout gives the chunking (fixed by the capacity), which the merging consumer needs.
-// Cache rows below keep_rows are read with cache-allocating loads (the caller sizes it so that those
-// rows of every layer fit the memory-side cache together), the others with nontemporal loads.
+// keep: the cache rows are read with cache-allocating loads (for a caller whose rows of every layer
+// fit the memory-side cache together), else with nontemporal loads. The kernel finds kn at qn + 128,
+// vc right after kc (kv_heads * capacity rows) and pos right after the RoPE row (rope + 128).
 void attn_step_layout(const hwk_attn_params *p, uint32_t *chunk, uint32_t *nchunk);
 size_t attn_step_workspace_bytes(const hwk_attn_params *p);
 char *attn_step(hipStream_t st, const float *qkv, const float *qn, const float *kn, const float *rope, double eps,
                 void *kc, void *vc, void *workspace, size_t workspace_bytes, const hwk_attn_params *p,
-                const int32_t *pos, uint32_t keep_rows);
+                const int32_t *pos, bool keep);
 
 }  // namespace hwk
 

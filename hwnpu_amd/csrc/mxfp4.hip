@@ -231,9 +231,16 @@ constexpr uint32_t kMergeMaxChunks = 16;
 // copied (X_F16) or made from the fp32 residual h by RMSNorm (X_NORM: every workgroup sums h^2 itself,
 // which hides behind its weight loads). SWIGLU: a wave's rows come in (gate, up) pairs and the output
 // is fp16 silu(gate) * up at the pair's index; otherwise y per MODE.
+//
+// The arguments are flat and ordered so that everything the prologue needs lies in the first 56
+// bytes, which the hardware preloads into SGPRs at wave launch (-amdgpu-kernarg-preload-count):
+// xa is x (X_F16), the residual h (X_NORM) or the partials (X_MERGE); xb the norm weights (X_NORM);
+// gn = G | nchunk << 16 (X_MERGE); eps (X_NORM), past them, is loaded when first used.
 template <int BPL, int RPW, int XM, bool SWIGLU, int WPB, int MODE>
 __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restrict__ w, const uint8_t *__restrict__ e,
-                                                           XIn in, void *__restrict__ y, uint32_t n, uint32_t nb) {
+                                                           const void *__restrict__ xa, void *__restrict__ y,
+                                                           uint32_t n, uint32_t nb, const float *__restrict__ xb,
+                                                           uint32_t gn, double eps) {
   static_assert(!SWIGLU || RPW % 2 == 0, "SwiGLU pairs rows");
   constexpr int NT = 64 * WPB;
   constexpr int PER = (64 * BPL * 32 + NT - 1) / NT;  // x values a thread makes (X_NORM)
@@ -249,7 +256,8 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   static_assert(kMergeMaxChunks == 16 && NT % 16 == 0, "a head's chunks are one 16-lane DPP group");
   __shared__ __align__(16) float ml[MS + 64];  // l of (head, chunk); past MS one spare slot a lane
   __shared__ __align__(16) float mw[MS + 64];  // weight of (head, chunk)
-  kernarg_now(w, e, y, n, nb, in.x16, in.h, in.nw, in.eps, in.ws, in.G, in.nchunk);
+  kernarg_now(w, e, xa, y, n, nb, xb, gn);
+  const XIn in{(const uint4 *)xa, (const float *)xa, xb, eps, (const float *)xa, gn & 0xffffu, gn >> 16};
   const int t = threadIdx.x, lane = t & 63;
   const uint32_t k = nb * 32;
   const uint32_t r0 = (blockIdx.x * WPB + (t >> 6)) * RPW;
@@ -919,8 +927,9 @@ template <int BPL, int XM, bool SWIGLU, int MODE>
 void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void *y, uint32_t n, uint32_t nb) {
   constexpr int WPB = 8, RPW = 2;
   const uint32_t sets = (n + RPW - 1) / RPW;
+  const void *xa = XM == X_F16 ? (const void *)in.x16 : XM == X_NORM ? (const void *)in.h : (const void *)in.ws;
   hipLaunchKernelGGL((k_mxfp4_gemv_x<BPL, RPW, XM, SWIGLU, WPB, MODE>), dim3((sets + WPB - 1) / WPB), dim3(64 * WPB), 0,
-                     st, (const uint4 *)w, (const uint8_t *)e, in, y, n, nb);
+                     st, (const uint4 *)w, (const uint8_t *)e, xa, y, n, nb, in.nw, in.G | in.nchunk << 16, in.eps);
 }
 
 template <int XM, bool SWIGLU, int MODE>
@@ -964,7 +973,7 @@ char *mxfp4_gemv_merge(hipStream_t st, const void *w, const void *e, const void 
   HWK_CHECK(w && e && workspace && y, "mxfp4_gemv_merge: null pointer");
   const uint32_t k = heads * 128;
   HWK_CHECK(heads >= 1 && k <= 64 * 4 * 32, "mxfp4_gemv_merge: %u heads of 128 (at most 8192 values)", heads);
-  HWK_CHECK(G >= 1 && heads % G == 0, "mxfp4_gemv_merge: G %u", G);
+  HWK_CHECK(G >= 1 && G < 65536 && heads % G == 0, "mxfp4_gemv_merge: G %u", G);
   HWK_CHECK(nchunk >= 1 && nchunk <= kMergeMaxChunks, "mxfp4_gemv_merge: %u chunks (at most %u)", nchunk,
             kMergeMaxChunks);
   HWK_CHECK(out_mode >= HWK_OUT_F32 && out_mode <= HWK_OUT_ADD_F32, "mxfp4_gemv_merge: out_mode %d", out_mode);

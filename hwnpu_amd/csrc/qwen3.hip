@@ -338,9 +338,10 @@ void layout(hwk_qwen3 *m, uint8_t *base) {
   m->embed = cv.take<f16>(base, 2ull * c.vocab * c.hidden);
   m->cos_t = cv.take<float>(base, 4ull * c.max_ctx * (c.head_dim / 2));
   m->sin_t = cv.take<float>(base, 4ull * c.max_ctx * (c.head_dim / 2));
-  m->rope_now = cv.take<float>(base, 4ull * c.head_dim);
+  // the step's RoPE row and, right after it, the position (the decode attention finds it there)
+  m->rope_now = cv.take<float>(base, 4ull * c.head_dim + 4);
+  m->pos = (int32_t *)(m->rope_now + c.head_dim);
   m->hist = cv.take<int32_t>(base, 4ull * (c.max_ctx + 1));
-  m->pos = cv.take<int32_t>(base, 4);
   m->counter = cv.take<uint32_t>(base, 4);
   m->part_i = cv.take<uint32_t>(base, 4 * kArgBlocks);
   m->part_v = cv.take<float>(base, 4 * kArgBlocks);
@@ -387,7 +388,7 @@ char *step(hwk_qwen3 *m, hipStream_t st, bool keep) {
                             HWK_OUT_F32, false));
     // attention partials over chunks of the cache, merged by the o_proj GEMV into its input
     HWK_Q(hwk::attn_step(st, m->qkv, ly.q_norm, ly.k_norm, m->rope_now, m->eps, ly.kc, ly.vc, m->ws, m->ws_bytes,
-                         &m->ap, m->pos, keep ? UINT32_MAX : 0u));
+                         &m->ap, m->pos, keep));
     HWK_Q(hwk::mxfp4_gemv_merge(st, ly.o.w, ly.o.e, m->ws, c.heads, c.heads / c.kv_heads, m->step_nchunk, m->h,
                                 c.hidden, HWK_OUT_ADD_F32));
     HWK_Q(hwk::mxfp4_gemv_x(st, ly.gu.w, ly.gu.e, nullptr, m->h, ly.post_norm, m->eps, m->a16, 2 * c.inter, c.hidden,
