@@ -236,7 +236,7 @@ constexpr uint32_t kMergeMaxChunks = 16;
 // bytes, which the hardware preloads into SGPRs at wave launch (-amdgpu-kernarg-preload-count):
 // xa is x (X_F16), the residual h (X_NORM) or the partials (X_MERGE); xb the norm weights (X_NORM);
 // gn = G | nchunk << 16 (X_MERGE); eps (X_NORM), past them, is loaded when first used.
-template <int BPL, int RPW, int XM, bool SWIGLU, int WPB, int MODE>
+template <int BPL, int RPW, int XM, bool SWIGLU, int WPB, int MODE, int MBC>
 __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restrict__ w, const uint8_t *__restrict__ e,
                                                            const void *__restrict__ xa, void *__restrict__ y,
                                                            uint32_t n, uint32_t nb, const float *__restrict__ xb,
@@ -247,7 +247,10 @@ __global__ __launch_bounds__(64 * WPB) void k_mxfp4_gemv_x(const uint4 *__restri
   constexpr int XC = 64 * BPL * 4;                    // 16-byte chunks of x LDS holds
   constexpr int XD = (64 * BPL * 16 + NT - 1) / NT;   // dwords of x a thread copies (X_F16)
   constexpr int M4 = (64 * BPL * 32 / 4 + NT - 1) / NT;  // groups of 4 x values a thread merges (X_MERGE)
-  constexpr int MB = M4 <= 1 ? (int)kMergeMaxChunks : kMergeBatch;  // chunks' o a thread loads up front
+  // chunks' o a thread loads up front: MBC, the launch's chunk count rounded up to 4, for one group a
+  // thread (a chunk past it would be a duplicate load of weight 0: 1,494 -> 1,516 tokens/s on the C5
+  // decode step against loading 16), else kMergeBatch
+  constexpr int MB = M4 <= 1 ? MBC : kMergeBatch;
   constexpr bool add = MODE == HWK_OUT_ADD_F32;
   __shared__ uint4 xs[NT * XD / 4];  // x (at least XC chunks)
   __shared__ double red[WPB];
@@ -928,8 +931,18 @@ void launch_x(hipStream_t st, const void *w, const void *e, const XIn &in, void 
   constexpr int WPB = 8, RPW = 2;
   const uint32_t sets = (n + RPW - 1) / RPW;
   const void *xa = XM == X_F16 ? (const void *)in.x16 : XM == X_NORM ? (const void *)in.h : (const void *)in.ws;
-  hipLaunchKernelGGL((k_mxfp4_gemv_x<BPL, RPW, XM, SWIGLU, WPB, MODE>), dim3((sets + WPB - 1) / WPB), dim3(64 * WPB), 0,
-                     st, (const uint4 *)w, (const uint8_t *)e, xa, y, n, nb, in.nw, in.G | in.nchunk << 16, in.eps);
+#define HWK_XL(MBC) hipLaunchKernelGGL((k_mxfp4_gemv_x<BPL, RPW, XM, SWIGLU, WPB, MODE, MBC>), dim3((sets + WPB - 1) / WPB), \
+                     dim3(64 * WPB), 0, st, (const uint4 *)w, (const uint8_t *)e, xa, y, n, nb, in.nw,              \
+                     in.G | in.nchunk << 16, in.eps)
+  if constexpr (XM == X_MERGE) {
+    if (in.nchunk <= 4) HWK_XL(4);
+    else if (in.nchunk <= 8) HWK_XL(8);
+    else if (in.nchunk <= 12) HWK_XL(12);
+    else HWK_XL(16);
+  } else {
+    HWK_XL(16);
+  }
+#undef HWK_XL
 }
 
 template <int XM, bool SWIGLU, int MODE>
