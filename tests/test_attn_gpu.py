@@ -96,8 +96,9 @@ def test_kv_quantize_rule(dev, orc):
     assert np.array_equal(qd.cpu().numpy(), qo)
 
 
+# 777, 5, 516 and 20: capacities whose last tile passes the last row (its loads clamped to it)
 @pytest.mark.parametrize("heads,kvh,L", [(32, 8, 512), (32, 8, 2048), (32, 8, 8192), (32, 8, 32768), (16, 8, 777),
-                                         (32, 8, 5)])
+                                         (32, 8, 5), (32, 8, 516), (16, 8, 20)])
 def test_attn_decode_int8(dev, orc, heads, kvh, L):
     print(f"attn int8 heads={heads} kv={kvh} L={L}", flush=True)
     q, k, v = case(heads, kvh, L, L, f"c3i8.{heads}.{L}")
