@@ -196,6 +196,81 @@ __device__ __forceinline__ void attend_ktile(KTile<I8> &t, const half8 (&qb)[4],
   }
 }
 
+// Two tiles (keys key0 .. key0+31) into the wave's running state at once: both tiles' scores (two
+// independent MFMA chains), one max, one rescale and one sum over the 32 keys, then both tiles' V
+// rows. The same arithmetic as attend_ktile over the pair's keys, with the running max taken over
+// both tiles before any exp (one online-softmax update instead of two: the serial chain of a tile's
+// softmax, issued by one wave a SIMD, is most of a tile's time).
+template <int G, bool I8>
+__device__ __forceinline__ void attend_pair(KTile<I8> &ta, KTile<I8> &tb, const half8 (&qb)[4], uint32_t key0,
+                                            uint32_t end, float scale_log2, int lane, float &m, float &ls,
+                                            float (&acc)[G][8]) {
+  KTile<I8> *tt[2] = {&ta, &tb};
+  if constexpr (I8) {
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      i8x16_to_half8x2(tt[u]->kraw[0], tt[u]->k[0], tt[u]->k[1]);
+      i8x16_to_half8x2(tt[u]->kraw[1], tt[u]->k[2], tt[u]->k[3]);
+    }
+  }
+  floatx4 sc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+  for (int s = 0; s < 4; s++)
+#pragma unroll
+    for (int u = 0; u < 2; u++) sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(tt[u]->k[s], qb[s], sc[u], 0, 0, 0);
+  float s2[2][4];
+  float tmax = -__builtin_inff();
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const uint32_t kr = key0 + 16 * u + 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float x = sc[u][i] * scale_log2;
+      if constexpr (I8) x *= (float)__builtin_bit_cast(f16, tt[u]->ksc[i]);
+      s2[u][i] = kr + i < end ? x : -__builtin_inff();
+      tmax = fmaxf(tmax, s2[u][i]);
+    }
+  }
+  tmax = row_groups_max(tmax);
+  const float mnew = fmaxf(m, tmax);
+  const bool none = mnew == -__builtin_inff();  // no key seen yet
+  const float alpha = none ? 1.0f : exp2f(m - mnew);
+  float p[2][4], psum = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      p[u][i] = none ? 0.0f : exp2f(s2[u][i] - mnew);
+      psum += p[u][i];
+    }
+  ls = ls * alpha + row_groups_sum(psum);
+  m = mnew;
+  float ag[G];
+  quad_heads<G>(alpha, ag);
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int d = 0; d < 8; d++) acc[g][d] *= ag[g];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const uint32_t kr = key0 + 16 * u + 4 * (lane >> 4);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      // a row past end was loaded from another row: zero it (p = 0 times NaN would be NaN)
+      const bool ok = kr + r < end;
+      half8 vr;
+      if constexpr (I8) vr = ok ? i8x8_to_half8(tt[u]->vraw[r]) : half8_of(make_uint4(0, 0, 0, 0));
+      else vr = ok ? tt[u]->v[r] : half8_of(make_uint4(0, 0, 0, 0));
+      float pg[G];
+      quad_heads<G>(I8 ? p[u][r] * (float)__builtin_bit_cast(f16, tt[u]->vsc[r]) : p[u][r], pg);
+#pragma unroll
+      for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int d = 0; d < 8; d++) acc[g][d] = fmaf(pg[g], (float)vr[d], acc[g][d]);
+    }
+  }
+}
+
 // Workgroup bx = (kv head h, chunk c) of W waves over keys [c*chunk, min((c+1)*chunk, len)) (len plus
 // *pos when pos is given); wave w takes keys [c*chunk + w*kpw, +kpw) a tile at a time with the next tile's
 // loads in flight. With one chunk a head the workgroup writes out; otherwise its partial (o
@@ -240,7 +315,7 @@ __device__ __forceinline__ void attn_decode_wg(uint32_t bx, const f16 *__restric
     attend_ktile<G, I8>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
     load_ktile<I8>(tb, k, v, ks, vs, head_base, key + 48, cap, lane);
   }
-  const uint32_t rem = nt - i;  // 0 .. 3
+  const uint32_t rem = nt - i;  // 0 .. 3 (attend_pair measured slower here: 8,192 fp16 keys 11.6 -> 12.1 us)
   if (rem >= 1) attend_ktile<G, I8>(ta, qb, key, ke, scale_log2, lane, m, ls, acc);
   if (rem == 3) load_ktile<I8>(ta, k, v, ks, vs, head_base, key + 32, cap, lane);
   if (rem >= 2) attend_ktile<G, I8>(tb, qb, key + 16, ke, scale_log2, lane, m, ls, acc);
