@@ -588,39 +588,56 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(15 | (3 
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 typedef __attribute__((address_space(3))) void lds_void;
+// The loads into LDS as inline assembly, so that the compiler inserts no wait of its own for them: its
+// wait insertion tracks the LDS targets of a few such loads only, and before an LDS read that none of
+// those covers it waits for every load in flight (vmcnt(0): in the software-pipelined loop below,
+// two steps of six drained the prefetch that way). The ring's explicit vmcnt waits and barriers order
+// them instead; the "memory" clobber keeps LDS reads and the barriers on their side of each load.
 __device__ __forceinline__ void to_lds16(const void *src, void *lds) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 16, 0, 0);
+  const uint32_t l = (uint32_t)(uintptr_t)(lds_void *)lds;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
 }
 __device__ __forceinline__ void to_lds4(const void *src, void *lds) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds, 4, 0, 0);
+  const uint32_t l = (uint32_t)(uintptr_t)(lds_void *)lds;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(l) : "memory", "m0");
 }
 
-// The loads of the step at K offset k0 (clamped to the last step: a step past the end rereads it).
+// The sources of a lane's loads into LDS, at K offset 0 (computed once; a step adds its K offset).
+// Out-of-range rows and columns read the last row/column.
 template <int BM, int BN, bool MX, int WM, int WN, int KG, int RS>
-__device__ __forceinline__ void ring_load(u32x4 *xb, u32x4 *wb, uint32_t *eb, const u32x4 *__restrict__ X,
-                                          const uint8_t *__restrict__ W, const uint8_t *__restrict__ E,
-                                          uint32_t M, uint32_t N, uint32_t K, uint32_t m0, uint32_t n0, uint32_t k0,
-                                          int wave, int lane) {
+struct RingSrc {
   using R = RCfg<BM, BN, MX, WM, WN, KG, RS>;
-  k0 = min(k0, K - KS);
+  const u32x4 *x[R::AX];
+  const uint8_t *w[R::AW];
+  const uint8_t *e;
+  uint32_t K;
+  __device__ __forceinline__ RingSrc(const u32x4 *X, const uint8_t *W, const uint8_t *E, uint32_t M, uint32_t N,
+                                     uint32_t K_, uint32_t m0, uint32_t n0, int wave, int lane)
+      : K(K_) {
 #pragma unroll
-  for (int a = 0; a < R::AX; a++) {
-    const int base = (a * R::NW + wave) * 64, p = base + lane, row = p / CH, ch = (p % CH) ^ (row & 15);
-    to_lds16(X + ((size_t)min(m0 + row, M - 1) * K + k0 + ch * 8) / 8, xb + base);
-  }
-  const size_t rowb = MX ? K / 2 : K;  // weight bytes a column
-  const uint32_t kb = MX ? k0 / 2 : k0;
+    for (int a = 0; a < R::AX; a++) {
+      const int p = (a * R::NW + wave) * 64 + lane, row = p / CH, ch = (p % CH) ^ (row & 15);
+      x[a] = X + ((size_t)min(m0 + row, M - 1) * K + ch * 8) / 8;
+    }
+    const size_t rowb = MX ? K / 2 : K;  // weight bytes a column
 #pragma unroll
-  for (int a = 0; a < R::AW; a++) {
-    const int base = (a * R::NW + wave) * 64, p = base + lane, col = p / R::WCH;
-    const int c = (p % R::WCH) ^ ((col / R::CPB) & (R::WCH - 1));
-    to_lds16(W + (size_t)min(n0 + col, N - 1) * rowb + kb + c * 16, wb + base);
+    for (int a = 0; a < R::AW; a++) {
+      const int p = (a * R::NW + wave) * 64 + lane, col = p / R::WCH;
+      const int c = (p % R::WCH) ^ ((col / R::CPB) & (R::WCH - 1));
+      w[a] = W + (size_t)min(n0 + col, N - 1) * rowb + c * 16;
+    }
+    e = MX ? E + (size_t)min(n0 + (uint32_t)(wave * 64 + lane), N - 1) * (K / 32) : nullptr;  // slots past BN: padding
   }
-  if constexpr (MX) {
-    const int p = wave * 64 + lane;  // slots past BN: padding nobody reads
-    to_lds4(E + (size_t)min(n0 + p, N - 1) * (K / 32) + k0 / 32, eb + wave * 64);
+  // The loads of the step at K offset k0 (clamped to the last step: a step past the end rereads it).
+  __device__ __forceinline__ void load(u32x4 *xb, u32x4 *wb, uint32_t *eb, uint32_t k0, int wave) const {
+    k0 = min(k0, K - KS);
+#pragma unroll
+    for (int a = 0; a < R::AX; a++) to_lds16(x[a] + k0 / 8, xb + (a * R::NW + wave) * 64);
+#pragma unroll
+    for (int a = 0; a < R::AW; a++) to_lds16(w[a] + (MX ? k0 / 2 : k0), wb + (a * R::NW + wave) * 64);
+    if constexpr (MX) to_lds4(e + k0 / 32, eb + wave * 64);
   }
-}
+};
 
 template <int BM, int BN, bool MX, int WM, int WN, int KG, int RS>
 __device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restrict__ X, const uint8_t *__restrict__ W,
@@ -631,11 +648,17 @@ __device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restric
   using R = RCfg<BM, BN, MX, WM, WN, KG, RS>;
   constexpr int TM = C::TM, TN = C::TN, NT = C::NT, KKG = C::KKG, LS = R::LS;
   static_assert(RS >= 2 && RS <= 6, "ring depth");
-  u32x4 *xr[RS], *wr[RS];
+  // one LDS variable a stage: X, then the weights, then the MXFP4 scales
+  constexpr int XB = BM * CH, WB = R::WSLOTS, EB = MX ? R::NW * 16 : 0;  // 16-byte slots
+  u32x4 *sr[RS], *xr[RS], *wr[RS];
   uint32_t *er[RS];
-  RingBufs<u32x4, BM * CH, 0, RS>::fill(xr);
-  RingBufs<u32x4, R::WSLOTS, 1, RS>::fill(wr);
-  RingBufs<uint32_t, MX ? R::NW * 64 : 1, 2, RS>::fill(er);
+  RingBufs<u32x4, XB + WB + EB, 0, RS>::fill(sr);
+#pragma unroll
+  for (int s = 0; s < RS; s++) {
+    xr[s] = sr[s];
+    wr[s] = sr[s] + XB;
+    er[s] = (uint32_t *)(sr[s] + XB + WB);
+  }
   __shared__ int hs[MX ? BN : 1], ls[MX ? BN : 1];  // the row shift scan (MXFP4)
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int g = wave / (WM * WN), wl = wave % (WM * WN);  // k group, wave in the group
@@ -646,9 +669,9 @@ __device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restric
   const uint32_t m0 = tm * BM, n0 = tn * BN;
   const uint32_t nw = n0 + wn * (BN / WN);  // the wave's first column
   const uint32_t steps = K / KS;
+  const RingSrc<BM, BN, MX, WM, WN, KG, RS> src(X, W, E, M, N, K, m0, n0, wave, lane);
 #pragma unroll
-  for (int s = 0; s < RS - 1; s++)
-    ring_load<BM, BN, MX, WM, WN, KG, RS>(xr[s], wr[s], er[s], X, W, E, M, N, K, m0, n0, s * KS, wave, lane);
+  for (int s = 0; s < RS - 1; s++) src.load(xr[s], wr[s], er[s], s * KS, wave);
   int s0[TN];
 #pragma unroll
   for (int j = 0; j < TN; j++) s0[j] = 0;
@@ -675,91 +698,106 @@ __device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restric
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
 
-  // A step j: wait for this wave's loads of step j (those of step j+1 stay in flight), a barrier
-  // (every wave's loads of step j have landed, and every wave is done with the buffers of step j-1),
-  // the loads of step j+RS-1 into those buffers, then the step's operands from LDS (every X operand
-  // of the step read at once: read one at a time before its MFMA, each read's latency showed) and
-  // the MFMAs, each kk's weights converted next to the MFMAs that take them.
-  for (uint32_t j0 = 0; j0 < steps; j0 += RS) {
+  // Software-pipelined steps: the operands of step j+1 are read from LDS (into the other register set)
+  // before the MFMAs of step j, so that the LDS reads of one step run under the MFMAs of the other
+  // (every operand of a step read at once: read one at a time before its MFMA, each read's latency
+  // showed). Step j: wait for this wave's LDS reads of step j (in registers: buffer j % RS is free)
+  // and its loads of step j+1, a barrier (every wave's loads of step j+1 have landed, every wave is
+  // done with buffer j % RS), the reads of step j+1, the loads of step j+RS into buffer j % RS, then
+  // the MFMAs of step j, each kk's weights converted next to the MFMAs that take them.
+  struct Ops {
+    u32x4 ax[KKG][TM];
+    u32x4 wv[TN][C::BL];  // int8: the wave's codes of the step
+    u32x2 wd[TN];         // MXFP4: the k group's dwords of block q (KG 2) or the first two (KG 1)
+    u32x2 wd2[TN];        // MXFP4 KG 1: the last two
+    uint32_t eb[TN];      // MXFP4: the block scale bytes of the step (4 a dword)
+  };
+  auto read_ops = [&](Ops &o, int b) __attribute__((always_inline)) {
+    const u32x4 *xb = xr[b], *wb = wr[b];
 #pragma unroll
-    for (int s = 0; s < RS; s++) {
-      const uint32_t j = j0 + s;
-      if (j >= steps) break;
-      wait_loads<(RS - 2) * LS>();
-      ring_barrier();
-      issue_order();
-      ring_load<BM, BN, MX, WM, WN, KG, RS>(xr[(s + RS - 1) % RS], wr[(s + RS - 1) % RS], er[(s + RS - 1) % RS], X, W,
-                                            E, M, N, K, m0, n0, (j + RS - 1) * KS, wave, lane);
-      issue_order();
-      const u32x4 *xb = xr[s], *wb = wr[s];
-      // the wave's weight codes of the step: int8 the 16 codes of half h = kk/2 (of the group's half)
-      // at q*16; MXFP4 the dwords kk of the 32-value block q (a k group's two: bytes 8g ..), and the
-      // MXFP4 scales
-      u32x4 wv[TN][C::BL];
-      uint32_t wd[TN][KKG];
-      float sc[TN];
+    for (int jn = 0; jn < TN; jn++) {
+      const int col = wn * (BN / WN) + jn * 16 + r16;
+      if constexpr (MX) {
+        const int slot = col * R::WCH + (q ^ ((col / R::CPB) & (R::WCH - 1)));
+        if constexpr (KG == 1) {
+          const u32x4 v = wb[slot];
+          o.wd[jn] = (u32x2){v[0], v[1]};
+          o.wd2[jn] = (u32x2){v[2], v[3]};
+        } else {
+          o.wd[jn] = *((const u32x2 *)&wb[slot] + g);
+        }
+        o.eb[jn] = er[b][col];
+      } else {
+#pragma unroll
+        for (int h = 0; h < C::BL; h++) {
+          const int c = (KG == 1 ? h : g) * 4 + q;
+          o.wv[jn][h] = wb[col * R::WCH + (c ^ ((col / R::CPB) & (R::WCH - 1)))];
+        }
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < KKG; kk++)
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int row = wm * (BM / WM) + i * 16 + r16;
+        const int ch = KG == 1 ? xchunk<MX>(q, kk) : xchunk<MX>(q, g * KKG + kk);
+        o.ax[kk][i] = xb[row * CH + (ch ^ (row & 15))];
+      }
+  };
+  auto mfma_ops = [&](const Ops &o) __attribute__((always_inline)) {
+    float sc[TN];
+    if constexpr (MX) {
+#pragma unroll
+      for (int jn = 0; jn < TN; jn++) sc[jn] = shifted_scale((o.eb[jn] >> (8 * q)) & 255u, s0[jn]);
+    }
+    auto bops = [&](half8 (&bf)[TN], int kk) __attribute__((always_inline)) {
 #pragma unroll
       for (int jn = 0; jn < TN; jn++) {
-        const int col = wn * (BN / WN) + jn * 16 + r16;
         if constexpr (MX) {
-          const int slot = col * R::WCH + (q ^ ((col / R::CPB) & (R::WCH - 1)));
-          if constexpr (KG == 1) {
-            const u32x4 v = wb[slot];
-#pragma unroll
-            for (int kk = 0; kk < KKG; kk++) wd[jn][kk] = v[kk];
-          } else {
-            const u32x2 v = *((const u32x2 *)&wb[slot] + g);
-#pragma unroll
-            for (int kk = 0; kk < KKG; kk++) wd[jn][kk] = v[kk];
-          }
-          sc[jn] = shifted_scale((er[s][col] >> (8 * q)) & 255u, s0[jn]);
+          const uint32_t w = KG == 1 ? (kk < 2 ? o.wd[jn][kk] : o.wd2[jn][kk - 2]) : o.wd[jn][kk];
+          bf[jn] = fp4x8_to_half8(w, sc[jn]);
         } else {
-#pragma unroll
-          for (int h = 0; h < C::BL; h++) {
-            const int c = (KG == 1 ? h : g) * 4 + q;
-            wv[jn][h] = wb[col * R::WCH + (c ^ ((col / R::CPB) & (R::WCH - 1)))];
-          }
+          const u32x4 v = o.wv[jn][kk >> 1];
+          bf[jn] = i8x8_to_half8(v[(kk & 1) * 2], v[(kk & 1) * 2 + 1]);
         }
       }
-      // every X operand of the step read from LDS at once, pinned in registers (an empty asm per value
-      // after all the reads), so that the reads are all in flight together
-      u32x4 ax[KKG][TM];
+    };
+    half8 bf[2][TN];
+    bops(bf[0], 0);
 #pragma unroll
-      for (int kk = 0; kk < KKG; kk++)
+    for (int kk = 0; kk < KKG; kk++) {
+      if (kk + 1 < KKG) bops(bf[(kk + 1) & 1], kk + 1);
 #pragma unroll
-        for (int i = 0; i < TM; i++) {
-          const int row = wm * (BM / WM) + i * 16 + r16;
-          const int ch = KG == 1 ? xchunk<MX>(q, kk) : xchunk<MX>(q, g * KKG + kk);
-          ax[kk][i] = xb[row * CH + (ch ^ (row & 15))];
-        }
-      issue_order();
+      for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int kk = 0; kk < KKG; kk++)
+        for (int jn = 0; jn < TN; jn++)
+          acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, o.ax[kk][i]), bf[kk & 1][jn],
+                                                              acc[i][jn], 0, 0, 0);
+    }
+  };
+  Ops P[2];
+  wait_loads<(RS - 2) * LS>();  // step 0 (this wave's loads)
+  ring_barrier();
+  issue_order();
+  src.load(xr[RS - 1], wr[RS - 1], er[RS - 1], (RS - 1) * KS, wave);
+  issue_order();
+  read_ops(P[0], 0);
+  for (uint32_t j0 = 0; j0 < steps; j0 += 2 * RS) {
 #pragma unroll
-        for (int i = 0; i < TM; i++) asm volatile("" : "+v"(ax[kk][i]));
-      auto bops = [&](half8 (&bf)[TN], int kk) __attribute__((always_inline)) {
-#pragma unroll
-        for (int jn = 0; jn < TN; jn++) {
-          if constexpr (MX) {
-            bf[jn] = fp4x8_to_half8(wd[jn][kk], sc[jn]);
-          } else {
-            const u32x4 v = wv[jn][kk >> 1];
-            bf[jn] = i8x8_to_half8(v[(kk & 1) * 2], v[(kk & 1) * 2 + 1]);
-          }
-        }
-      };
-      half8 bf[2][TN];
-      bops(bf[0], 0);
-#pragma unroll
-      for (int kk = 0; kk < KKG; kk++) {
-        if (kk + 1 < KKG) bops(bf[(kk + 1) & 1], kk + 1);
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-          for (int jn = 0; jn < TN; jn++)
-            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ax[kk][i]), bf[kk & 1][jn],
-                                                                acc[i][jn], 0, 0, 0);
+    for (int s = 0; s < 2 * RS; s++) {
+      const uint32_t j = j0 + s;
+      if (j >= steps) break;
+      wait_lds();  // this wave's reads of step j (on both paths: the MFMAs below then wait for nothing)
+      if (j + 1 < steps) {
+        wait_loads<(RS - 2) * LS>();
+        ring_barrier();
+        issue_order();
+        read_ops(P[(s + 1) & 1], (s + 1) % RS);
+        issue_order();
+        src.load(xr[s % RS], wr[s % RS], er[s % RS], (j + RS) * KS, wave);
+        issue_order();
       }
+      mfma_ops(P[s & 1]);
     }
   }
   wait_loads<0>();  // no load into LDS may land after the workgroup ends
@@ -796,18 +834,20 @@ __device__ __forceinline__ void gemm_ring_wg(uint32_t bx, const u32x4 *__restric
     ring_barrier();  // group 0 is done with the sums' buffers, which its stores reuse
     if (g == 1) return;
   }
-  if (staged(Y, N, mode)) {
-    // a wave's block in region wl of the X buffers, PER regions a buffer
-    using G = StageRows<TM, TN, TN * 16 + 4>;
-    constexpr int PER = BM * CH * 4 / G::FLOATS;
-    static_assert(PER >= 1 && (WM * WN + PER - 1) / PER <= RS, "the staged blocks fit the X buffers");
-    if constexpr (KG == 1) {
-      wait_lds();
-      ring_barrier();  // every wave is done with the ring's buffers
+  // staged stores where the waves' blocks fit the X buffers (a wave's block in region wl, PER regions
+  // a buffer), else straight from the accumulators
+  using G = StageRows<TM, TN, TN * 16 + 4>;
+  constexpr int PER = BM * CH * 4 / G::FLOATS;
+  if constexpr (PER >= 1 && (WM * WN + PER - 1) / PER <= RS) {
+    if (staged(Y, N, mode)) {
+      if constexpr (KG == 1) {
+        wait_lds();
+        ring_barrier();  // every wave is done with the ring's buffers
+      }
+      store_tile_staged<BM, WM, TM, TN, MX, TN * 16 + 4>(acc, s0, S, Y, M, N, m0, nw, wm, lane, mode,
+                                                         (float *)xr[wl / PER] + (wl % PER) * G::FLOATS);
+      return;
     }
-    store_tile_staged<BM, WM, TM, TN, MX, TN * 16 + 4>(acc, s0, S, Y, M, N, m0, nw, wm, lane, mode,
-                                                       (float *)xr[wl / PER] + (wl % PER) * G::FLOATS);
-    return;
   }
   store_tile<BM, WM, TM, TN, MX>(acc, s0, S, Y, M, N, m0, nw, wm, r16, q, mode);
 }
