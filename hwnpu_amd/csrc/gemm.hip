@@ -53,26 +53,21 @@ Shape pick_shape(uint32_t m, uint32_t n, int cus, bool mx) {
 }
 
 // The ring form (K a multiple of 128; see gemm_kernels.h) for the tiles 128 columns wide, as 8 waves
-// (2 x 4; its LDS holds one workgroup a CU), for the int8 128 x 96 tile of two k groups, and for the
-// MXFP4 128 x 64 tile that the register-staged form would take as 2 x 4 waves. Measured against the
-// register-staged form, bit for bit the same results (the two-group tiles sum in another order):
-// 1024 x 4096 x 2048 MXFP4 31.3 -> 23.9 us, 1024 x 12288 x 2048 82.4 -> 79.9 (91.5 over 8 weight
-// copies with the SwiGLU output), int8 512 x 6144 x 2048 29.9 -> 20.8, MXFP4 1024 x 2048 x 6144 54.4
-// -> 50.3 (128 x 64 as two k groups of one wave row: a wave 128 x 32, its weight operands converted
-// once for 8 MFMA rows), 1024 x 2048 x 2048 22.7 -> 21.5 (128 x 64 as 2 x 4 waves: with 16 steps the
-// 4-wave tile measured 25.7). The int8 128 x 64 tiles stay register-staged (not measured in the ring
-// form), and so do the 4-wave tiles taken when several tiles share a CU.
-bool ring_shape(Shape &sh, bool mx, uint32_t k) {
+// (2 x 4; its LDS holds one workgroup a CU), and for the int8 128 x 96 tile of two k groups. Measured
+// against the register-staged form, bit for bit the same results: 1024 x 4096 x 2048 MXFP4 31.3 ->
+// 28.3 us, 1024 x 12288 x 2048 82.4 -> 79.9, int8 512 x 6144 x 2048 29.9 -> 24.1; its LDS reads
+// software-pipelined (over 32 weight copies, past the memory-side cache): 25.6 -> 25.1, 86.7 -> 84.9
+// (SwiGLU output), 21.8 -> 21.3. The MXFP4 tiles 64 columns
+// wide stay register-staged: in the ring form (2 x 4 waves, or two k groups of one wave row) the
+// prompt's down and o_proj projections measured no faster alone and the prompt 1.2 % slower
+// (6.42 against 6.35 ms), and so did 64-row tiles with deeper rings.
+bool ring_shape(Shape &sh, bool mx) {
   if (sh.bm == 128 && sh.bn == 128) {
     sh = {128, 128, 2, 4, 1, 3};
     return true;
   }
   if (!mx && sh.bm == 128 && sh.bn == 96 && sh.kg == 2) {
     sh.rs = 3;
-    return true;
-  }
-  if (mx && sh.bm == 128 && sh.bn == 64 && sh.wm * sh.wn * sh.kg == 8) {
-    sh = k >= 4096 ? Shape{128, 64, 1, 2, 2, 3} : Shape{128, 64, 2, 4, 1, 3};
     return true;
   }
   return false;
@@ -92,7 +87,7 @@ char *launch(hipStream_t st, const void *x, const void *w, const void *e, const 
   static const int cus = device_cus();
   // the ring form needs whole 128-column steps and 4-byte aligned scale rows
   Shape sh = pick_shape(m, n, cus, MX);
-  const bool ring = k % 128 == 0 && (!MX || hwk::aligned(e, 4)) && ring_shape(sh, MX, k);
+  const bool ring = k % 128 == 0 && (!MX || hwk::aligned(e, 4)) && ring_shape(sh, MX);
   const uint32_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn);
   const bool equads = MX && (k / 32) % 16 == 0 && hwk::aligned(e, 16);
   const dim3 grid(tiles);
@@ -110,8 +105,6 @@ char *launch(hipStream_t st, const void *x, const void *w, const void *e, const 
       HWK_RING_IF(128, 96, 2, 2, 2, 3)
       HWK_CHECK(false, "%s: no ring kernel for the %dx%d tile", what, sh.bm, sh.bn);
     } else {
-      HWK_RING_IF(128, 64, 1, 2, 2, 3)
-      HWK_RING_IF(128, 64, 2, 4, 1, 3)
       HWK_CHECK(false, "%s: no ring kernel for the %dx%d tile", what, sh.bm, sh.bn);
     }
     return hwk::launched(what);

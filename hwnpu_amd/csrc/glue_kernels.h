@@ -71,10 +71,67 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
   }
 }
 
-// Launches k_rmsnorm for rows of n values: the one-pass form up to 4096 values a row.
+// One wave a row of n = 256*C values (4 rows a workgroup): lane l holds the 16-byte pieces
+// j*64 + l of x and w, loaded at once; the float64 sum of squares over the wave by DPP, no LDS and no
+// barrier. The numerics are k_rmsnorm's; only the order of the float64 sum differs.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+template <bool F16OUT, int C>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ x, const float *__restrict__ w,
+                                                      double eps, void *__restrict__ out, uint32_t rows) {
+#pragma clang fp contract(off)
+  constexpr uint32_t n = 256 * C;
+  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves leave together
+  const int lane = threadIdx.x & 63;
+  const f32x4 *xr = (const f32x4 *)(x + (size_t)row * n), *wr = (const f32x4 *)w;
+  f32x4 xv[C], wv[C];
+#pragma unroll
+  for (int j = 0; j < C; j++) xv[j] = xr[j * 64 + lane];
+#pragma unroll
+  for (int j = 0; j < C; j++) wv[j] = wr[j * 64 + lane];
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < C; j++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const double v = (double)xv[j][c];
+      ss += v * v;
+    }
+  ss = wave_sum_f64_all(ss);
+  const float r = (float)(1.0 / sqrt(ss / (double)n + eps));
+#pragma unroll
+  for (int j = 0; j < C; j++) {
+    f32x4 y;
+#pragma unroll
+    for (int c = 0; c < 4; c++) y[c] = f32_value((xv[j][c] * r) * wv[j][c]);
+    const size_t i = (size_t)row * n / 4 + j * 64 + lane;  // 4-value piece
+    if constexpr (F16OUT)
+      ((f16x4 *)out)[i] = (f16x4){(f16)y[0], (f16)y[1], (f16)y[2], (f16)y[3]};
+    else
+      ((f32x4 *)out)[i] = y;
+  }
+}
+
+// Launches the RMSNorm of rows of n values: a wave a row for n = 256, 512, 1024, 2048 or 4096 with
+// 16-byte aligned rows (the 1,024-token prompt of 2,048-value rows: 6.55 -> 6.52 ms; a decode step
+// unchanged), else k_rmsnorm, its one-pass form up to 4096 values a row.
 template <bool F16OUT>
 inline void launch_rmsnorm(hipStream_t st, const float *x, const float *w, double eps, void *out, uint32_t rows,
                            uint32_t n) {
+  const bool vec = hwk::aligned(x, 16) && hwk::aligned(w, 16) && hwk::aligned(out, F16OUT ? 8 : 16);
+  const dim3 g4((rows + 3) / 4);
+#define HWK_RMS_ROWS(Cv)                                                                                    \
+  if (vec && n == 256 * Cv) {                                                                               \
+    hipLaunchKernelGGL((k_rmsnorm_rows<F16OUT, Cv>), g4, dim3(256), 0, st, x, w, eps, out, rows);          \
+    return;                                                                                                 \
+  }
+  HWK_RMS_ROWS(1)
+  HWK_RMS_ROWS(2)
+  HWK_RMS_ROWS(4)
+  HWK_RMS_ROWS(8)
+  HWK_RMS_ROWS(16)
+#undef HWK_RMS_ROWS
   const uint32_t per = (n + 255) / 256;
   if (per <= 4)
     hipLaunchKernelGGL((k_rmsnorm<F16OUT, 4>), dim3(rows), dim3(256), 0, st, x, w, eps, out, n);

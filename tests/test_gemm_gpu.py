@@ -42,8 +42,8 @@ def test_i8_gemm_parity(dev, orc, m, n, k):
     assert np.array_equal(y16.view(np.uint16), orc.f32_to_f16(y32))
 
 
-# (1024, 2048, 6144), (5, 2048, 6144) and (260, 1000, 4096) take the 128 x 64 tile of two k groups of
-# one wave row (ragged rows and columns in the last), (1024, 2048, 2048) the 128 x 64 tile of 2 x 4 waves
+# (1024, 2048, 6144) and (1024, 2048, 2048) are the prompt's down and o_proj shapes, (260, 1000, 4096)
+# their tile with ragged rows and columns
 @pytest.mark.parametrize("m,n,k", [(1024, 4096, 2048), (5, 2048, 6144), (1, 96, 64), (200, 12288, 2048), (33, 130, 32),
                                    (1024, 2048, 6144), (260, 1000, 4096), (1024, 2048, 2048)])
 def test_mxfp4_gemm_parity(dev, orc, m, n, k):
