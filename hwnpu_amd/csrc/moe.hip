@@ -111,7 +111,8 @@ template <int PPW, bool ROUTE>
 void launch_gate_up(hipStream_t st, const void *x, const float *logits, const float *rbias, int32_t *idx, float *w,
                     const void *gu_w, const void *gu_e, const float *gu_b, float *act, const MoeArgs &a) {
   const uint32_t unique_max = a.T * a.k < a.E ? a.T * a.k : a.E;
-  const dim3 g1((a.I + 4 * PPW - 1) / (4 * PPW), unique_max);
+  // with the route folded in, one more column of workgroups: the route's own (moe_gate_up_wg)
+  const dim3 g1((a.I + 4 * PPW - 1) / (4 * PPW) + (ROUTE ? 1 : 0), unique_max);
   const int bpl1 = (int)((a.H / 32 + 63) / 64);
 #define HWK_GU(B)                                                                                         \
   hipLaunchKernelGGL((k_moe_gate_up<B, PPW, ROUTE>), g1, dim3(256), 0, st, (const uint4 *)x, logits, rbias, idx, w, \

@@ -9,8 +9,10 @@
 //
 // K5b is two launches and needs nothing from the host between them. The gate_up kernel gives each
 // (chosen expert, row-pair tile) to a workgroup: with the route folded in (hwk_moe_layer) every
-// workgroup first derives the token's choice from the router logits itself; otherwise it reads the
-// given idx. It reads the expert's rows once for all tokens that chose it, adds the gate/up biases,
+// workgroup derives the token's choice from the router logits itself (read off the logits' order
+// where that provably equals Choose's, so that its weight loads issue before Choose has run, in a
+// workgroup of its own that writes idx and w; else by Choose first); otherwise it reads the given
+// idx. It reads the expert's rows once for all tokens that chose it, adds the gate/up biases,
 // and writes the gated unit (SiLU, or gpt-oss's clamped one) in fp32 (it overflows fp16 at the
 // benchmark's scales). The down kernel gives each workgroup a tile of output rows for every chosen
 // expert (its waves take the experts in turn, all their rows' loads issued at once) and then adds,
@@ -79,6 +81,50 @@ __device__ void choose_wave(const float *__restrict__ logits, const float *__res
     idx_out[lane] = my_e;
     w_out[lane] = wj;
   }
+}
+
+// Routing.Choose's choice read off the logits alone, where that provably gives Choose's experts in
+// Choose's order (softmax scores, no bias): rank by d = logit - max (the float32 difference Choose
+// exponentiates; softmax is monotone in it), ties to the lower index. The choice is Choose's when the
+// d of consecutive ranks 0 .. min(k, E-1) differ by at least 2^-20 (their float64 exps then differ by
+// a factor above 1 + 9.5e-7, so their float32 roundings, and the roundings of those over the same
+// sum, differ: a float32 rounding moves a value by at most 2^-24 of it) and the last chosen has
+// d >= -80 (every chosen score a normal float32). Returns that, the same in every wave; every wave
+// gets the chosen set of the T tokens as mask, and wave 0 writes token t's choice in rank order to
+// ch[t*k ..].
+__device__ __forceinline__ bool spec_choice(const float *__restrict__ logits, uint32_t T, uint32_t E, uint32_t k,
+                                            int32_t *ch, uint64_t &mask) {
+  const uint32_t lane = threadIdx.x & 63;
+  const bool live = lane < E, w0 = threadIdx.x < 64;
+  const uint32_t kk = k < E ? k : E;  // the chosen a token
+  bool ok = true;
+  mask = 0;
+  for (uint32_t t = 0; t < T; t++) {
+    const float v = live ? logits[(size_t)t * E + lane] : -__builtin_inff();
+    const float m = group_max_dpp<64>(v);
+    const float d = v - m;
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < E; j++) {
+      const float dj = lane_f(d, j);
+      rank += (dj > d) || (dj == d && j < lane);
+    }
+    ok = ok && !__ballot(live && !(d == d));  // no NaN
+    float prev = 0.0f;
+    for (uint32_t r = 0; r <= kk && r < E; r++) {
+      const uint64_t who = __ballot(live && rank == r);
+      if (!who) {
+        ok = false;
+        break;
+      }
+      const float dr = lane_f(d, (uint32_t)__builtin_ctzll(who));
+      if (r > 0 && !(prev - dr >= 0x1p-20f)) ok = false;
+      if (r + 1 == kk && !(dr >= -80.0f)) ok = false;
+      prev = dr;
+    }
+    if (w0 && live && rank < k) ch[t * k + rank] = (int32_t)lane;
+    mask |= __ballot(live && rank < k);
+  }
+  return ok;
 }
 
 // ---- K5b helpers ----
@@ -193,19 +239,35 @@ __device__ __forceinline__ void moe_gate_up_wg(uint32_t bx, uint32_t by, const u
   __shared__ float gsum[PPW == 2 ? 1 : 2 * 64 * 4 * PPW];  // (token, wave, pair) -> (gate, up) sums
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t n = a.T * a.k;
+  uint64_t mask = 0;
+  bool spec = false;  // the choice read off the logits (spec_choice), the weight loads issued before Choose
   if constexpr (ROUTE) {
-    for (uint32_t t = wave; t < a.T; t += 4)
-      choose_wave(logits + (size_t)t * a.E, rbias, a.E, a.k, a.score, a.norm, a.scale, sidx + t * a.k, sw + t * a.k);
-    __syncthreads();
-    if (bx == 0 && by == 0 && threadIdx.x < n) {
-      idx[threadIdx.x] = sidx[threadIdx.x];
-      wout[threadIdx.x] = sw[threadIdx.x];
+    if (!rbias && a.score == HWK_SCORE_SOFTMAX) spec = spec_choice(logits, a.T, a.E, a.k, sidx, mask);
+    if (bx == (a.I + 4 * PPW - 1) / (4 * PPW)) {
+      // the route's own workgroup (one column past the experts' tiles): Choose's idx and w, beside
+      // the experts' loads; without the logits' choice the experts' workgroups route themselves
+      if (spec && by == 0)
+        for (uint32_t t = wave; t < a.T; t += 4)
+          choose_wave(logits + (size_t)t * a.E, rbias, a.E, a.k, a.score, a.norm, a.scale, idx + t * a.k,
+                      wout + t * a.k);
+      return;
+    }
+    if (!spec) {
+      for (uint32_t t = wave; t < a.T; t += 4)
+        choose_wave(logits + (size_t)t * a.E, rbias, a.E, a.k, a.score, a.norm, a.scale, sidx + t * a.k,
+                    sw + t * a.k);
+      __syncthreads();
+      if (bx == 0 && by == 0 && threadIdx.x < n) {
+        idx[threadIdx.x] = sidx[threadIdx.x];
+        wout[threadIdx.x] = sw[threadIdx.x];
+      }
+      mask = chosen_mask(sidx, n, a.E);
     }
   } else {
     if (threadIdx.x < n) sidx[threadIdx.x] = idx[threadIdx.x];
     __syncthreads();
+    mask = chosen_mask(sidx, n, a.E);
   }
-  uint64_t mask = chosen_mask(sidx, n, a.E);
   const uint32_t u = by;
   if (u >= (uint32_t)__builtin_popcountll(mask)) return;
   for (uint32_t i = 0; i < u; i++) mask &= mask - 1;
@@ -233,6 +295,12 @@ __device__ __forceinline__ void moe_gate_up_wg(uint32_t bx, uint32_t by, const u
   for (int p = 0; p < PPW; p++)
 #pragma unroll
     for (int r = 0; r < 2; r++) bias[p][r] = gb ? gb[erow + 2 * min(pair0 + p, I - 1) + r] : 0.0f;
+  if (spec) {
+    // wave 0's choice in sidx: its LDS writes done, then a bare barrier (__syncthreads would wait
+    // for the weight loads above too)
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+  }
   for (uint32_t t = 0; t < a.T; t++) {
     const int slot = slot_of(sidx, t, a.k, e);
     if (slot < 0) continue;

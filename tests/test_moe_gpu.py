@@ -163,6 +163,39 @@ def test_moe_layer_score_collision(dev, orc, T, row):
     check_close(out.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("T,case", [(1, "gap"), (2, "gap"), (1, "far"), (2, "clear")])
+def test_moe_layer_route_near_ties(dev, orc, T, case):
+    """The folded route reads the choice off the logits when the differences logit - max of the
+    first k+1 ranks are at least 2^-20 apart (and the k-th at least -80), else runs Choose first.
+    "gap": the 4th and 5th differ by 2^-21 (float32 spacing near -4; Choose's scores still differ),
+    "far": the 4th chosen at -95 (a denormal score), "clear": 2^-20 apart (near -8.5), taken from
+    the logits. Each must give Choose's idx bit for bit and the oracle's output."""
+    x, logits, gw, ge, dw, de = experts_case(T)
+    lg = logits.cpu().numpy()
+    lg[0, :] = -5.0 if case != "far" else -300.0
+    if case == "gap":
+        lg[0, :3] = [9.0, 8.5, 8.0]
+        lg[0, 5] = 5.0
+        lg[0, 7] = np.nextafter(np.float32(5.0), np.float32(6.0))
+        assert np.float32(lg[0, 7] - 9.0) - np.float32(lg[0, 5] - 9.0) == np.float32(2.0 ** -21)
+    elif case == "far":
+        lg[0, :4] = [0.0, -85.0, -90.0, -95.0]
+    else:
+        lg[0, :3] = [9.0, 8.5, 8.0]
+        lg[0, 5] = 0.5
+        lg[0, 7] = np.float32(0.5) + np.float32(2.0 ** -20)
+        assert np.float32(lg[0, 7] - 9.0) - np.float32(lg[0, 5] - 9.0) == np.float32(2.0 ** -20)
+    logits.copy_(torch.from_numpy(lg))
+    out, idx, w = ops.moe_layer(x, logits, 4, gw, ge, dw, de)
+    ii, ww = idx.cpu().numpy(), w.cpu().numpy()
+    for t in range(T):
+        oi, ow = orc.choose(lg[t], 4)
+        assert np.array_equal(ii[t], oi), (t, ii[t], oi)
+        assert np.all(ulp_diff(ww[t], ow) <= 1)
+    want = orc.experts(x.cpu().numpy().astype(np.float32), ii, ww, *_np(gw, ge, dw, de))
+    check_close(out.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("T,exp_hi", [(1, False), (5, False), (3, True)])
 def test_experts_gptoss_biases(dev, orc, T, exp_hi):
     """The gpt-oss gated unit (alpha 1.702, limit 7) with gate/up and down biases (host.go:44-57,
