@@ -87,7 +87,9 @@ char *launch(hipStream_t st, const void *x, const void *w, const void *e, const 
   static const int cus = device_cus();
   // the ring form needs whole 128-column steps and 4-byte aligned scale rows
   Shape sh = pick_shape(m, n, cus, MX);
-  const bool ring = k % 128 == 0 && (!MX || hwk::aligned(e, 4)) && ring_shape(sh, MX);
+  // the ring form addresses its operands by 32-bit byte offsets (under 4 GiB an operand)
+  const bool small = (uint64_t)m * k * 2 < (1ull << 32) && (uint64_t)n * (MX ? k / 2 : k) < (1ull << 32);
+  const bool ring = k % 128 == 0 && (!MX || hwk::aligned(e, 4)) && small && ring_shape(sh, MX);
   const uint32_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn);
   const bool equads = MX && (k / 32) % 16 == 0 && hwk::aligned(e, 16);
   const dim3 grid(tiles);

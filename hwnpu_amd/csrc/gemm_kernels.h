@@ -593,49 +593,52 @@ typedef __attribute__((address_space(3))) void lds_void;
 // those covers it waits for every load in flight (vmcnt(0): in the software-pipelined loop below,
 // two steps of six drained the prefetch that way). The ring's explicit vmcnt waits and barriers order
 // them instead; the "memory" clobber keeps LDS reads and the barriers on their side of each load.
-__device__ __forceinline__ void to_lds16(const void *src, void *lds) {
+__device__ __forceinline__ void to_lds16(const void *sbase, uint32_t voff, void *lds) {
   const uint32_t l = (uint32_t)(uintptr_t)(lds_void *)lds;
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(l)
+               : "memory", "m0");
 }
-__device__ __forceinline__ void to_lds4(const void *src, void *lds) {
+__device__ __forceinline__ void to_lds4(const void *sbase, uint32_t voff, void *lds) {
   const uint32_t l = (uint32_t)(uintptr_t)(lds_void *)lds;
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(l) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(l)
+               : "memory", "m0");
 }
 
-// The sources of a lane's loads into LDS, at K offset 0 (computed once; a step adds its K offset).
-// Out-of-range rows and columns read the last row/column.
+// The sources of a lane's loads into LDS: a uniform base (the operand's start plus the step's K
+// offset, in scalar registers) and the lane's byte offset from it (computed once: the loads take the
+// base + offset form, no per-lane address arithmetic a step). Out-of-range rows and columns read the
+// last row/column. The offsets are 32-bit: the launcher takes this form for operands under 4 GiB.
 template <int BM, int BN, bool MX, int WM, int WN, int KG, int RS>
 struct RingSrc {
   using R = RCfg<BM, BN, MX, WM, WN, KG, RS>;
-  const u32x4 *x[R::AX];
-  const uint8_t *w[R::AW];
-  const uint8_t *e;
+  const char *X, *W, *E;
+  uint32_t xo[R::AX], wo[R::AW], eo;
   uint32_t K;
-  __device__ __forceinline__ RingSrc(const u32x4 *X, const uint8_t *W, const uint8_t *E, uint32_t M, uint32_t N,
+  __device__ __forceinline__ RingSrc(const u32x4 *X_, const uint8_t *W_, const uint8_t *E_, uint32_t M, uint32_t N,
                                      uint32_t K_, uint32_t m0, uint32_t n0, int wave, int lane)
-      : K(K_) {
+      : X((const char *)X_), W((const char *)W_), E((const char *)E_), K(K_) {
 #pragma unroll
     for (int a = 0; a < R::AX; a++) {
       const int p = (a * R::NW + wave) * 64 + lane, row = p / CH, ch = (p % CH) ^ (row & 15);
-      x[a] = X + ((size_t)min(m0 + row, M - 1) * K + ch * 8) / 8;
+      xo[a] = (min(m0 + row, M - 1) * K + ch * 8) * 2;
     }
-    const size_t rowb = MX ? K / 2 : K;  // weight bytes a column
+    const uint32_t rowb = MX ? K / 2 : K;  // weight bytes a column
 #pragma unroll
     for (int a = 0; a < R::AW; a++) {
       const int p = (a * R::NW + wave) * 64 + lane, col = p / R::WCH;
       const int c = (p % R::WCH) ^ ((col / R::CPB) & (R::WCH - 1));
-      w[a] = W + (size_t)min(n0 + col, N - 1) * rowb + c * 16;
+      wo[a] = min(n0 + col, N - 1) * rowb + c * 16;
     }
-    e = MX ? E + (size_t)min(n0 + (uint32_t)(wave * 64 + lane), N - 1) * (K / 32) : nullptr;  // slots past BN: padding
+    eo = MX ? min(n0 + (uint32_t)(wave * 64 + lane), N - 1) * (K / 32) : 0u;  // slots past BN: padding
   }
   // The loads of the step at K offset k0 (clamped to the last step: a step past the end rereads it).
   __device__ __forceinline__ void load(u32x4 *xb, u32x4 *wb, uint32_t *eb, uint32_t k0, int wave) const {
     k0 = min(k0, K - KS);
 #pragma unroll
-    for (int a = 0; a < R::AX; a++) to_lds16(x[a] + k0 / 8, xb + (a * R::NW + wave) * 64);
+    for (int a = 0; a < R::AX; a++) to_lds16(X + k0 * 2, xo[a], xb + (a * R::NW + wave) * 64);
 #pragma unroll
-    for (int a = 0; a < R::AW; a++) to_lds16(w[a] + (MX ? k0 / 2 : k0), wb + (a * R::NW + wave) * 64);
-    if constexpr (MX) to_lds4(e + k0 / 32, eb + wave * 64);
+    for (int a = 0; a < R::AW; a++) to_lds16(W + (MX ? k0 / 2 : k0), wo[a], wb + (a * R::NW + wave) * 64);
+    if constexpr (MX) to_lds4(E + k0 / 32, eo, eb + wave * 64);
   }
 };
 
