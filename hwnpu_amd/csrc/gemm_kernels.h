@@ -595,13 +595,11 @@ typedef __attribute__((address_space(3))) void lds_void;
 // them instead; the "memory" clobber keeps LDS reads and the barriers on their side of each load.
 __device__ __forceinline__ void to_lds16(const void *sbase, uint32_t voff, void *lds) {
   const uint32_t l = (uint32_t)(uintptr_t)(lds_void *)lds;
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(l)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(l) : "memory");
 }
 __device__ __forceinline__ void to_lds4(const void *sbase, uint32_t voff, void *lds) {
   const uint32_t l = (uint32_t)(uintptr_t)(lds_void *)lds;
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(l)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(l) : "memory");
 }
 
 // The sources of a lane's loads into LDS: a uniform base (the operand's start plus the step's K
