@@ -9,7 +9,7 @@
 // in key order. The kv head is the workgroup index modulo kv_heads, so that with 8 kv heads every
 // workgroup of a head runs on the same XCD and the head's K and V stay in that XCD's L2. The tiles go
 // through LDS in three stages (rows padded so that every operand read is free of bank conflicts and
-// addressed by one per-lane register plus constant offsets), loaded into registers two tiles ahead.
+// addressed by one per-lane register plus constant offsets), loaded into registers a tile ahead.
 // On the fp16 MFMA (v_mfma_f32_16x16x32_f16) a wave computes the scores transposed, S^T = K Q^T, so
 // that a lane holds eight scores of one query: the online softmax (fp32, base 2) reduces them
 // in-lane and across its four lane groups (permlane swaps), and the probabilities already sit where
@@ -46,17 +46,18 @@ __device__ __forceinline__ short4v tr_read(const lds_char *p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v *)p);
 }
 
-// S key groups of four waves (S = 2: eight waves, a CU's two waves a SIMD): group gi takes the tiles
-// gi, gi + S, ... with stages of its own, so that the longest query blocks walk half their tiles in
-// order; the second group's (m, l, O^T) then meet the first's in LDS (the Merge rule in base 2).
-// Measured on the C5 prefill (1,024 tokens): 6.60 -> 6.37 ms a prompt against one group.
+// S key groups of four waves (S = 3: twelve waves, a CU's three waves a SIMD): group gi takes the
+// tiles gi, gi + S, ... with stages of its own, so that the longest query blocks walk a third of
+// their tiles in order; the other groups' (m, l, O^T) then meet the first's in LDS (the Merge rule in
+// base 2). Measured on the C5 prefill (1,024 tokens): one group 36.3 µs a layer, two 28.6-29.0,
+// three 27.1 (which fit the registers once a group's tiles were staged through one register set).
 template <int G, int S>
 __global__ __launch_bounds__(256 * S) void k_attn_prefill(const u32x4 *__restrict__ q, const u32x4 *__restrict__ kc,
                                                           const u32x4 *__restrict__ vc, void *__restrict__ out,
                                                           int mode, uint32_t T, uint32_t start, uint32_t heads,
                                                           uint32_t kvh, uint32_t cap, float scale_log2) {
   constexpr uint32_t QB = 64 / G;  // query positions a workgroup
-  static_assert(S == 1 || S == 2, "one or two key groups");
+  static_assert(S >= 1 && S <= 3, "one to three key groups");
   __shared__ __attribute__((aligned(16))) char lds_all[S * NST * STAGE];
   const int gi = threadIdx.x >> 8;  // key group
   char *lds = lds_all + gi * NST * STAGE;
@@ -186,13 +187,12 @@ __global__ __launch_bounds__(256 * S) void k_attn_prefill(const u32x4 *__restric
 
   // A group's step j's tile is in LDS stage j % 3 from the end of step j-2 on. Step j computes step
   // j+1's scores (so that their MFMAs run beside this tile's softmax), updates with step j's tile, and
-  // stores step j+2's tile into the stage step j-1 left (read for the last time in step j-1). Two
-  // register sets: ra holds even steps' tiles, rb odd ones, each refilled (two steps ahead) right
-  // after it is stored.
+  // stores step j+2's tile, loaded into ra during step j-1, into the stage step j-1 left (read for the
+  // last time in step j-1), then loads step j+3's tile into ra.
   // with S groups the steps are the group's own tiles: local step j is tile j * S + gi (stage j % 3);
   // every group runs as many steps as group 0 (a step past a group's last tile loads, stores and
   // computes nothing that is used), so that all waves meet at the same barriers
-  u32x4 ra[2 * PER], rb[2 * PER];
+  u32x4 ra[2 * PER];
   floatx4 sa[2], sb[2];
   const uint32_t steps = (tiles + S - 1) / S;
   auto T_ = [&](uint32_t j) { return j * S + gi; };
@@ -223,48 +223,63 @@ __global__ __launch_bounds__(256 * S) void k_attn_prefill(const u32x4 *__restric
     update(sc, T_(j), j % NST);
   };
   ld(ra, 0);
-  ld(rb, 1);
   stj(ra, 0);
+  ld(ra, 1);
+  stj(ra, 1);
   ld(ra, 2);
-  stj(rb, 1);
-  ld(rb, 3);
   __syncthreads();
   scj(sa, 0);
   for (uint32_t j = 0; j < steps; j += 2) {
     scj(sb, j + 1);
     upj(sa, j);
-    stj(ra, j + 2);
-    ld(ra, j + 4);
+    stj(ra, j + 2);  // loaded in the step before; its stage left by step j-1
+    ld(ra, j + 3);
     __syncthreads();
     if (j + 1 >= steps) break;
     scj(sa, j + 2);
     upj(sb, j + 1);
-    stj(rb, j + 3);
-    ld(rb, j + 5);
+    stj(ra, j + 3);
+    ld(ra, j + 4);
     __syncthreads();
   }
-  if constexpr (S == 2) {
-    // group 1's state to group 0 through its own stages (every tile is consumed: the last barrier
+  if constexpr (S > 1) {
+    // groups 1 .. S-1's states to group 0 through the stages (every tile is consumed: the last barrier
     // above follows the last update), group 0 merges: weights 2^(m - top), as the Merge rule
-    float *xo = (float *)(lds_all + NST * STAGE) + (size_t)(wave * 64 + lane) * 34;
-    if (gi == 1) {
+    float *xo = (float *)lds_all + (size_t)(wave * 64 + lane) * 34;
+    constexpr size_t GX = 256 * 34;  // floats a group's states take
+    if (gi > 0) {
+      float *xg = xo + (gi - 1) * GX;
 #pragma unroll
       for (int d = 0; d < 8; d++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) xo[d * 4 + r] = acc[d][r];
-      xo[32] = m;
-      xo[33] = l;
+        for (int r = 0; r < 4; r++) xg[d * 4 + r] = acc[d][r];
+      xg[32] = m;
+      xg[33] = l;
     }
     __syncthreads();
-    if (gi == 1) return;
-    const float m1 = xo[32], l1 = xo[33], top = fmaxf(m, m1);
-    const float a0 = top == -__builtin_inff() ? 0.0f : exp2f(m - top);
-    const float a1 = top == -__builtin_inff() ? 0.0f : exp2f(m1 - top);
-    l = l * a0 + l1 * a1;
+    if (gi > 0) return;
+    float mg[S], ag[S];
+    mg[0] = m;
+    float top = m;
+#pragma unroll
+    for (int g = 1; g < S; g++) {
+      mg[g] = xo[(g - 1) * GX + 32];
+      top = fmaxf(top, mg[g]);
+    }
+#pragma unroll
+    for (int g = 0; g < S; g++) ag[g] = top == -__builtin_inff() ? 0.0f : exp2f(mg[g] - top);
+    l = l * ag[0];
+#pragma unroll
+    for (int g = 1; g < S; g++) l = l + xo[(g - 1) * GX + 33] * ag[g];
 #pragma unroll
     for (int d = 0; d < 8; d++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[d][r] = acc[d][r] * a0 + xo[d * 4 + r] * a1;
+      for (int r = 0; r < 4; r++) {
+        float v = acc[d][r] * ag[0];
+#pragma unroll
+        for (int g = 1; g < S; g++) v = v + xo[(g - 1) * GX + d * 4 + r] * ag[g];
+        acc[d][r] = v;
+      }
   }
   if (!qlive) return;
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -308,8 +323,9 @@ HWK_API char *hwk_attn_prefill(void *stream, const void *q, const void *k, const
   const uint32_t QB = 64 / G;
   const dim3 grid((tokens + QB - 1) / QB * p->kv_heads);
   // two key groups a workgroup once the longest block has a few tiles (8 waves a CU: the longest
-  // blocks walk half their tiles each)
+  // blocks walk half their tiles each), three past 256 keys
   const bool two = start + tokens > 128;
+  const bool three = start + tokens > 256;
   const float scale_log2 = hwk::f32_of_bits(p->scale_bits) * kLog2e;
   hipStream_t st = (hipStream_t)stream;
 #define HWK_PF2(GG, SS)                                                                                             \
@@ -317,7 +333,9 @@ HWK_API char *hwk_attn_prefill(void *stream, const void *q, const void *k, const
                      (const u32x4 *)v, out, (int)p->out_mode, tokens, start, p->heads, p->kv_heads, p->capacity, scale_log2)
 #define HWK_PF(GG)                        \
   do {                                    \
-    if (two)                              \
+    if (three)                            \
+      HWK_PF2(GG, 3);                     \
+    else if (two)                         \
       HWK_PF2(GG, 2);                     \
     else                                  \
       HWK_PF2(GG, 1);                     \

@@ -189,9 +189,11 @@ def oracle_prefill(orc, q, k, v, start, scale):
     return o.transpose(1, 0, 2)
 
 
+# three key groups past 256 keys (the first and the last two), two past 128, one below
 @pytest.mark.parametrize("heads,kvh,T,start,cap", [
     (16, 8, 1024, 0, 1280),  # the model's prompt
-    (32, 8, 200, 0, 256), (16, 8, 37, 100, 160), (8, 8, 70, 5, 80), (16, 16, 1, 0, 8), (16, 8, 33, 31, 64)])
+    (32, 8, 200, 0, 256), (16, 8, 37, 100, 160), (8, 8, 70, 5, 80), (16, 16, 1, 0, 8), (16, 8, 33, 31, 64),
+    (32, 8, 300, 0, 320), (8, 8, 250, 10, 288)])
 def test_attn_prefill_causal(dev, orc, heads, kvh, T, start, cap):
     print(f"attn prefill heads={heads} kv={kvh} T={T} start={start} cap={cap}", flush=True)
     name = f"c3p.{heads}.{T}.{start}"
