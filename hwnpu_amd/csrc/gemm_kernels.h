@@ -593,6 +593,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 // those covers it waits for every load in flight (vmcnt(0): in the software-pipelined loop below,
 // two steps of six drained the prefetch that way). The ring's explicit vmcnt waits and barriers order
 // them instead; the "memory" clobber keeps LDS reads and the barriers on their side of each load.
+// The LDS address (wave-uniform) goes in M0 as an operand the compiler sets, the s_nop the wait state
+// between that write and the load; the global address is sbase (scalar) + voff (a lane's offset).
 __device__ __forceinline__ void to_lds16(const void *sbase, uint32_t voff, void *lds) {
   const uint32_t l = (uint32_t)(uintptr_t)(lds_void *)lds;
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(l) : "memory");
