@@ -108,14 +108,16 @@ void launch(hipStream_t st, const void *w, const void *s, const void *x, void *y
 // nc chunks a row: 64 lanes over up to 4 chunks a pass; narrower rows share a wave. The fp16 head
 // (151,936 rows of 256 chunks) takes 32 lanes a row, 8 chunks a lane, two rows a wave: the decode step
 // 1,521-1,523 tokens/s with 64 lanes over two rows a wave, 1,528-1,530 over one, 1,532.7-1,532.9 so
-// (16 lanes a row: 1,522; four or eight rows a wave of 64-lane rows: 1,497-1,517).
+// (16 lanes a row: 1,522; four or eight rows a wave of 64-lane rows: 1,497-1,517). The int8 GEMV of
+// 2,048-code rows (K2, 8192 x 2048) takes two row sets a wave: 5.17 -> 4.94 µs a launch against four
+// (one: 5.00-5.02; 32 lanes a row and one or two sets: 4.99-5.07; 16 lanes: 5.39).
 template <bool INT8>
 void dispatch(hipStream_t st, const void *w, const void *s, const void *x, void *y, uint32_t n, uint32_t nc,
               int mode) {
   if (nc >= 256 && !INT8) launch<INT8, 32, 8, 1>(st, w, s, x, y, n, nc, mode);
   else if (nc >= 256) launch<INT8, 64, 4, 2>(st, w, s, x, y, n, nc, mode);
   else if (nc > 128) launch<INT8, 64, 3, 2>(st, w, s, x, y, n, nc, mode);
-  else if (nc > 64) launch<INT8, 64, 2, 4>(st, w, s, x, y, n, nc, mode);
+  else if (nc > 64) launch<INT8, 64, 2, INT8 ? 2 : 4>(st, w, s, x, y, n, nc, mode);
   else if (nc > 32) launch<INT8, 64, 1, 4>(st, w, s, x, y, n, nc, mode);
   else if (nc > 16) launch<INT8, 32, 1, 4>(st, w, s, x, y, n, nc, mode);
   else if (nc > 8) launch<INT8, 16, 1, 4>(st, w, s, x, y, n, nc, mode);
