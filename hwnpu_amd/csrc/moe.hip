@@ -64,8 +64,9 @@ void launch_down_cfg(hipStream_t st, const float *act, const int32_t *idx, const
 
 // The waves of a down workgroup and the experts a wave loads at once, by the chosen (token, expert)
 // slots n = T*k (at most n distinct experts): every slot a wave of its own up to 4 (no load is a
-// padding copy), two a wave for 8 waves up to 32 (16 at once, a second round past 16 distinct
-// experts), else as many as the registers take.
+// padding copy), one a wave for 16 waves up to 32 (16 at once, a second round past 16 distinct
+// experts; at T = 5 30.5-30.8 µs a layer against 31.4 for two a wave in 8 waves, and 31.6 for one in
+// 8), else as many as the registers take.
 template <int LPR, int BPL>
 void launch_down(hipStream_t st, const float *act, const int32_t *idx, const float *w, const void *dw, const void *de,
                  const float *db, float *out, const MoeArgs &a) {
@@ -73,7 +74,7 @@ void launch_down(hipStream_t st, const float *act, const int32_t *idx, const flo
   if (n <= 4)
     launch_down_cfg<LPR, BPL, 1, 4>(st, act, idx, w, dw, de, db, out, a);
   else if (n <= 32)
-    launch_down_cfg<LPR, BPL, 2, 8>(st, act, idx, w, dw, de, db, out, a);
+    launch_down_cfg<LPR, BPL, 1, 16>(st, act, idx, w, dw, de, db, out, a);
   else
     launch_down_cfg<LPR, BPL, BPL <= 1 ? 8 : 12 / BPL, 8>(st, act, idx, w, dw, de, db, out, a);
 }
