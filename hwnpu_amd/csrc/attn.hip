@@ -408,29 +408,30 @@ __global__ void k_kv_quantize_i8(const f16 *__restrict__ x, int8_t *__restrict__
 }
 
 // The split of hwk_attn_decode: workgroups of W waves, each wave kpw keys (a multiple of 16), chunk =
-// W*kpw keys a workgroup. W = 8 for int8 caches from 8,192 keys and for fp16 caches of 8,192 to
-// 16,383 keys, else 4. Below 16,384 keys kpw is sized so that the launch runs about 2048 waves (8 a
-// CU, each with two tiles of loads in flight), between 32 and 256 keys, more when a head would exceed
-// kMaxChunks chunks; from 16,384 keys a kv head takes 32 chunks, so that the merge reads 32 partials a
-// query head (measured at 16K and 32K keys over chunks of 512-2048 keys and 4 or 8 waves: the
-// fastest, with the merge's cost growing with the chunks and the split's with the keys a workgroup).
+// W*kpw keys a workgroup. W = 8 for int8 caches from 8,192 keys, else 4. From 8,192 keys a kv head
+// takes 32 chunks, so that the merge reads 32 partials a query head (measured at 8K, 16K and 32K keys
+// over chunks of 128-2048 keys and 4 or 8 waves: the fastest, with the merge's cost growing with the
+// chunks and the split's with the keys a workgroup; fp16 at 8,192 keys: 11.6 us a call in 4-wave
+// workgroups against 12.0 in 8-wave ones). Below 8,192 keys kpw is sized so that the launch runs
+// about 2048 waves (8 a CU, each with two tiles of loads in flight), between 32 and 256 keys, more
+// when a head would exceed kMaxChunks chunks; and one 16-key tile a wave while a kv head then has at
+// most 16 chunks (fp16) or 32 (int8): at 512 keys 7.2 / 7.1 us a call against 7.6 / 7.9 for two
+// tiles, int8 at 2,048 keys 7.7 against 8.1 (fp16 at 2,048 keys, 32 chunks: 8.2 against 8.0).
 // A caller's split (a multiple of 64) is the chunk.
-uint32_t decode_waves(const hwk_attn_params *p) {
-  if (p->kv_int8) return p->len >= 8192 ? 8u : 4u;
-  return p->len >= 8192 && p->len < 16384 ? 8u : 4u;
-}
+uint32_t decode_waves(const hwk_attn_params *p) { return p->kv_int8 && p->len >= 8192 ? 8u : 4u; }
 
 uint32_t pick_kpw(const hwk_attn_params *p) {
   const uint32_t W = decode_waves(p);
   if (p->split) return p->split / W;
   uint64_t kpw;
-  if (p->len >= 16384) {
+  if (p->len >= 8192) {
     kpw = ((uint64_t)p->len + 32ull * W - 1) / (32ull * W);
   } else {
     const uint64_t keys = (uint64_t)p->len * p->kv_heads;
     kpw = (keys + 2047) / 2048;
     if (kpw < 32) kpw = 32;
     if (kpw > 256) kpw = 256;
+    if (kpw == 32 && ((uint64_t)p->len + 16ull * W - 1) / (16ull * W) <= (p->kv_int8 ? 32u : 16u)) kpw = 16;
   }
   kpw = (kpw + 15) / 16 * 16;
   const uint64_t min_kpw = ((uint64_t)p->len + (uint64_t)kMaxChunks * W - 1) / ((uint64_t)kMaxChunks * W);
