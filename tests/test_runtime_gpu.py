@@ -271,7 +271,8 @@ def test_co_attention_matches_library(device, program, orc, L, int8):
     if int8:
         k, ks = ops.kv_quantize_i8(k)
         v, vs = ops.kv_quantize_i8(v)
-    want = ops.attn_decode(q, k, v, L, ks, vs, out_mode="f16").cpu().numpy()
+    # the library's split set to the code object's (4 waves of kpw keys a workgroup)
+    want = ops.attn_decode(q, k, v, L, ks, vs, out_mode="f16", split=4 * kpw).cpu().numpy()
     chunk, nchunk = 4 * kpw, -(-L // (4 * kpw))
     slots = heads * nchunk
     arrs = [q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()] + ([ks.cpu().numpy(), vs.cpu().numpy()] if int8 else [])
